@@ -1,0 +1,127 @@
+/*
+ * C ABI of the MI355X (gfx950) AWQ W4A16 dequant-GEMM library (libawq_w4a16.so).
+ *
+ * Plain pointers and sizes only: every tensor argument is a device pointer owned by
+ * the caller, every size is an element count, `stream` is a hipStream_t passed as
+ * void* (NULL = the default stream).  No function allocates device memory; scratch
+ * space comes in through `workspace`.  Every function returns 0 on success or one of
+ * the AWQ_ERR_* codes below, never throws, and leaves no pending HIP error behind.
+ *
+ * Reference interfaces each entry point replaces (paths relative to the
+ * jiayingsong2023/litevLLM checkout):
+ *   awq_w4a16_dequant  <- awq_dequantize_triton / awq_dequantize_kernel
+ *                         (vllm/model_executor/layers/quantization/awq_triton.py:64-194)
+ *                         and dequantize_awq_pytorch / dequantize_symmetric_packed_int4_pytorch
+ *                         (vllm/model_executor/layers/quantization/tensor.py:835-901)
+ *   awq_w4a16_gemm     <- the launches inside awq_fused_gemm
+ *                         (vllm/kernels/triton/awq_fused_gemm.py:2395-2552) of
+ *                         _awq_native_tiled_gemm_{heuristic,split_k,autotuned}
+ *                         (awq_fused_gemm.py:1754-1990, 2296-2392) and, with qzeros == NULL,
+ *                         packed_int4_symmetric_fused_gemm (awq_fused_gemm.py:2555-2922)
+ *   awq_w4a16_gemm_workspace_bytes <- the split-K output zero-fill of awq_fused_gemm
+ *                         (awq_fused_gemm.py:2434-2443), replaced by an fp32 partial buffer
+ *   awq_w4a16_repack   <- no kernel in the reference: the lossless layout conversion the
+ *                         model loader would need at model_loader/__init__.py:756-797
+ *   awq_w4a16_moe_*    <- the dense-expert fused_moe path used for zero-point AWQ experts
+ *                         (vllm/model_executor/layers/fused_moe/fused_moe.py:4-77,
+ *                         models/gemma4/moe.py:661-751) and the grouped int4 MoE wrapper
+ *                         gemma4_moe_int4_prefill_grouped (kernels/triton/gemma4_moe_int4.py:2330-2584)
+ */
+#ifndef AWQ_W4A16_H
+#define AWQ_W4A16_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- packed layouts (G = group_size) ------------------------------------------
+ * AWQ_LAYOUT_AUTOAWQ : qweight int32 [K, N/8], nibble i of word (k, j) = W[k, 8j + order[i]],
+ *                      order = {0,2,4,6,1,3,5,7}; qzeros int32 [K/G, N/8] packed the same way;
+ *                      scales [K/G, N].  (AutoAWQ "GEMM" checkpoint layout.)
+ * AWQ_LAYOUT_KN_SEQ  : as AUTOAWQ but sequential nibbles (nibble i = column 8j + i); the
+ *                      geometry awq_dequantize_triton handles when scales.shape[0] != rows
+ *                      (awq_triton.py:107-118, 161).
+ * AWQ_LAYOUT_NK_SEQ  : reference runtime layout: qweight int32 [N, K/8], nibble i of word
+ *                      (n, j) = W[n, 8j + i]; qzeros int32 [N, ceil(K/G/8)] sequential along
+ *                      the group axis; scales [N, K/G]  (tensor.py:842-858).
+ */
+#define AWQ_LAYOUT_AUTOAWQ 0
+#define AWQ_LAYOUT_KN_SEQ 1
+#define AWQ_LAYOUT_NK_SEQ 2
+
+/* ---- element types ---- */
+#define AWQ_DTYPE_NONE 0 /* e.g. no bias */
+#define AWQ_DTYPE_F16 1
+#define AWQ_DTYPE_BF16 2
+#define AWQ_DTYPE_F32 3
+
+/* ---- error codes ---- */
+#define AWQ_OK 0
+#define AWQ_ERR_NULL 1        /* a required pointer is NULL */
+#define AWQ_ERR_SHAPE 2       /* sizes inconsistent (K % G, N % 8, K % 32, ...) */
+#define AWQ_ERR_UNSUPPORTED 3 /* dtype / layout / group size combination not provided */
+#define AWQ_ERR_WORKSPACE 4   /* workspace NULL or smaller than required */
+#define AWQ_ERR_LAUNCH 5      /* a HIP launch failed */
+#define AWQ_ERR_STRIDE 6      /* leading dimension smaller than the row length */
+
+/* Library version (major * 10000 + minor * 100 + patch). */
+int awq_w4a16_version(void);
+
+/* Static description of an error code (never NULL). */
+const char* awq_w4a16_strerror(int code);
+
+/* Dequantize a packed int4 matrix: out = RNE_outdtype((q - z) * s), computed so that
+ * the result equals one rounding of the exact product (float32 arithmetic in the
+ * reference, tensor.py:857-858 / awq_triton.py:138-145).
+ *   rows x cols is the *unpacked* matrix in the packed tensor's own orientation:
+ *   AUTOAWQ / KN_SEQ: rows = K, cols = N, out [K, N];  NK_SEQ: rows = N, cols = K, out [N, K].
+ *   qzeros == NULL selects symmetric mode z = 8 (tensor.py:891).
+ *   scale_dtype: F16 or BF16.  out_dtype: F16, BF16 or F32.  out is dense row-major.
+ */
+int awq_w4a16_dequant(const int32_t* qweight, const void* scales, const int32_t* qzeros, void* out,
+                      int64_t rows, int64_t cols, int32_t group_size, int32_t layout,
+                      int32_t scale_dtype, int32_t out_dtype, void* stream);
+
+/* Workspace bytes awq_w4a16_gemm needs for these arguments (0 if none).  The workspace
+ * holds fp32 split-K partials and per-tile arrival counters.  The counter region must be
+ * zero the first time a workspace is used; every call leaves it zero again, so a
+ * workspace allocated zeroed once can be reused by later calls on the same stream.
+ * Two calls that may run concurrently must not share a workspace. */
+size_t awq_w4a16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_size,
+                                      int32_t split_k, int32_t layout);
+
+/* C[M, N] = A[M, K] . dequant(W)^T (+ bias), W dequantized exactly as awq_w4a16_dequant
+ * does for act_dtype, products accumulated in fp32, one rounding to act_dtype at the end.
+ *   a: [M, K] act_dtype (F16 or BF16), row stride lda (elements).
+ *   layout: AUTOAWQ or KN_SEQ (qweight [K, N/8]) or NK_SEQ (qweight [N, K/8]).
+ *   qzeros == NULL: symmetric z = 8.  scales: scale_dtype (F16 or BF16).
+ *   bias: NULL or [N] of bias_dtype (F16, BF16 or F32), added once in fp32.
+ *   c: [M, N] act_dtype, row stride ldc.
+ *   split_k: number of contiguous K partitions whose fp32 partial sums are added in a fixed
+ *            order (0 = choose automatically).  For a given (M, N, K, split_k) the result is
+ *            bitwise reproducible.  Partition s covers k-steps [s*I, (s+1)*I) with
+ *            I = ceil(steps / split_k), as in awq_fused_gemm.py:1799-1801.
+ *   Requirements: N % 8 == 0, group_size % 32 == 0, K % group_size == 0.
+ */
+int awq_w4a16_gemm(const void* a, int64_t lda, const int32_t* qweight, const void* scales,
+                   const int32_t* qzeros, const void* bias, void* c, int64_t ldc, int64_t M,
+                   int64_t N, int64_t K, int32_t group_size, int32_t split_k, int32_t layout,
+                   int32_t act_dtype, int32_t scale_dtype, int32_t bias_dtype, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/* Lossless repack of a reference-layout (NK_SEQ) weight into the AUTOAWQ layout:
+ *   qweight_nk [N, K/8] -> qweight_kn [K, N/8];  qzeros_nk [N, ceil(K/G/8)] -> qzeros_kn [K/G, N/8]
+ *   (qzeros may be NULL);  scales_nk [N, K/G] -> scales_kn [K/G, N] (2-byte elements). */
+int awq_w4a16_repack_nk_to_autoawq(const int32_t* qweight_nk, const int32_t* qzeros_nk,
+                                   const void* scales_nk, int32_t* qweight_kn, int32_t* qzeros_kn,
+                                   void* scales_kn, int64_t N, int64_t K, int32_t group_size,
+                                   void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AWQ_W4A16_H */

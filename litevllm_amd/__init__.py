@@ -1,0 +1,19 @@
+"""MI355X-native AWQ W4A16 dequant-GEMM (gfx950 HIP kernels behind a C ABI) with the
+reference's Python call surface for that path."""
+from . import _lib, ops  # noqa: F401
+from .awq import AWQConfig  # noqa: F401
+from .awq_fused_gemm import (  # noqa: F401
+    awq_fused_gemm,
+    awq_fused_gemm_safe,
+    packed_int4_symmetric_fused_gemm,
+    packed_int4_symmetric_fused_gemm_safe,
+)
+from .awq_triton import (  # noqa: F401
+    awq_dequantize_triton,
+    awq_fused_capability_check,
+    awq_gemm_triton,
+    packed_int4_fused_capability_check,
+)
+from .tensor import AWQWeight, PackedInt4Weight  # noqa: F401
+
+__version__ = "0.1.0"

@@ -1,0 +1,201 @@
+"""Torch-facing wrappers of the C ABI: device memory and streams come from PyTorch,
+every byte of arithmetic runs in the HIP kernels of ``libawq_w4a16.so``.
+
+Layouts (``layout=`` keyword everywhere):
+  * ``"ref"``      reference runtime layout: qweight int32 [N, K/8] (sequential nibbles),
+                   scales [N, K/G], qzeros int32 [N, ceil(K/G/8)]
+  * ``"autoawq"``  AutoAWQ layout: qweight int32 [K, N/8] (order 0,2,4,6,1,3,5,7),
+                   scales [K/G, N], qzeros int32 [K/G, N/8]
+  * ``"kn_seq"``   [K, N/8] with sequential nibbles (the reference dequant's row-grouped geometry)
+"""
+from __future__ import annotations
+
+import threading
+import weakref
+
+import torch
+
+from . import _lib as L
+
+LAYOUTS = {"autoawq": L.LAYOUT_AUTOAWQ, "kn_seq": L.LAYOUT_KN_SEQ, "ref": L.LAYOUT_NK_SEQ}
+_DT = {torch.float16: L.DTYPE_F16, torch.bfloat16: L.DTYPE_BF16, torch.float32: L.DTYPE_F32}
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _DT[dt]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {dt}") from None
+
+
+def layout_code(layout: str) -> int:
+    try:
+        return LAYOUTS[layout]
+    except KeyError:
+        raise ValueError(f"unknown layout {layout!r}; expected one of {sorted(LAYOUTS)}") from None
+
+
+def _stream_ptr(device: torch.device) -> int:
+    return int(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else int(t.data_ptr())
+
+
+def _require_device(*tensors: torch.Tensor | None) -> torch.device:
+    """All tensors on one GPU; the kernels dereference these pointers on the device."""
+    devs = {t.device for t in tensors if t is not None}
+    if len(devs) != 1:
+        raise ValueError(f"tensors must share one device, got {sorted(map(str, devs))}")
+    dev = devs.pop()
+    if dev.type != "cuda":
+        raise ValueError(f"HIP kernels need GPU tensors, got device {dev}")
+    return dev
+
+
+def gemm_dims(qweight: torch.Tensor, layout: str) -> tuple[int, int]:
+    """(K, N) of a packed weight in the given layout."""
+    if layout == "ref":
+        return int(qweight.shape[1]) * 8, int(qweight.shape[0])
+    return int(qweight.shape[0]), int(qweight.shape[1]) * 8
+
+
+# ------------------------------------------------------------------ dequant
+def dequant(qweight: torch.Tensor, scales: torch.Tensor, qzeros: torch.Tensor | None,
+            group_size: int, layout: str = "ref", out_dtype: torch.dtype = torch.float16,
+            out: torch.Tensor | None = None) -> torch.Tensor:
+    """Unpacked matrix in the packed tensor's orientation: ``ref`` -> [N, K], else [K, N]."""
+    lib = L.load()
+    _require_device(qweight, scales, qzeros, out)
+    rows = int(qweight.shape[0])
+    cols = int(qweight.shape[1]) * 8
+    if out is None:
+        out = torch.empty((rows, cols), dtype=out_dtype, device=qweight.device)
+    qweight, scales = qweight.contiguous(), scales.contiguous()
+    qzeros = qzeros.contiguous() if qzeros is not None else None
+    rc = lib.awq_w4a16_dequant(_ptr(qweight), _ptr(scales), _ptr(qzeros), _ptr(out), rows, cols,
+                               int(group_size), layout_code(layout), dtype_code(scales.dtype),
+                               dtype_code(out.dtype), _stream_ptr(qweight.device))
+    L.check("awq_w4a16_dequant", rc)
+    return out
+
+
+# ------------------------------------------------------------------ repack
+def repack_ref_to_autoawq(qweight: torch.Tensor, scales: torch.Tensor, qzeros: torch.Tensor | None,
+                          group_size: int):
+    """Reference layout -> AutoAWQ layout on the device (lossless)."""
+    lib = L.load()
+    _require_device(qweight, scales, qzeros)
+    n, k = int(qweight.shape[0]), int(qweight.shape[1]) * 8
+    ng = k // int(group_size)
+    dev = qweight.device
+    qw = torch.empty((k, n // 8), dtype=torch.int32, device=dev)
+    sc = torch.empty((ng, n), dtype=scales.dtype, device=dev)
+    qz = torch.empty((ng, n // 8), dtype=torch.int32, device=dev) if qzeros is not None else None
+    qweight, scales = qweight.contiguous(), scales.contiguous()
+    qzeros = qzeros.contiguous() if qzeros is not None else None
+    rc = lib.awq_w4a16_repack_nk_to_autoawq(_ptr(qweight), _ptr(qzeros), _ptr(scales), _ptr(qw),
+                                            _ptr(qz), _ptr(sc), n, k, int(group_size),
+                                            _stream_ptr(dev))
+    L.check("awq_w4a16_repack_nk_to_autoawq", rc)
+    return qw, sc, qz
+
+
+class _RepackCache:
+    """Caches the AutoAWQ-layout copy of reference-layout weights, keyed by the packed
+    tensor's storage pointer, shape and version counter (the role the reference's
+    derived-pack cache plays at tensor.py:1251-1256)."""
+
+    def __init__(self, capacity: int = 512):
+        self.capacity = capacity
+        self._d: dict = {}
+        self._lock = threading.Lock()
+
+    def get(self, qweight, scales, qzeros, group_size):
+        key = (qweight.data_ptr(), tuple(qweight.shape), qweight._version, scales.data_ptr(),
+               scales._version, None if qzeros is None else (qzeros.data_ptr(), qzeros._version),
+               int(group_size), qweight.device.index)
+        with self._lock:
+            hit = self._d.get(key)
+            if hit is not None:
+                ref, val = hit
+                if ref() is qweight:
+                    return val
+        val = repack_ref_to_autoawq(qweight, scales, qzeros, group_size)
+        with self._lock:
+            if len(self._d) >= self.capacity:
+                self._d.pop(next(iter(self._d)))
+            self._d[key] = (weakref.ref(qweight), val)
+        return val
+
+    def clear(self):
+        with self._lock:
+            self._d.clear()
+
+
+REPACK_CACHE = _RepackCache()
+
+
+# ------------------------------------------------------------------ workspace
+class _Workspace:
+    """Zero-initialised scratch per (device, stream).  The kernels leave the counter region
+    at zero, so a buffer is zeroed only when it is (re)allocated."""
+
+    def __init__(self):
+        self._bufs: dict = {}
+        self._lock = threading.Lock()
+
+    def get(self, device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+        key = (device.index, stream)
+        with self._lock:
+            buf = self._bufs.get(key)
+            if buf is None or buf.numel() < nbytes:
+                size = max(nbytes, 1 << 20)
+                buf = torch.zeros(size, dtype=torch.uint8, device=device)
+                self._bufs[key] = buf
+            return buf
+
+
+WORKSPACE = _Workspace()
+
+
+# ------------------------------------------------------------------ GEMM
+def gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, qzeros: torch.Tensor | None,
+         group_size: int, bias: torch.Tensor | None = None, split_k: int = 0,
+         layout: str = "ref", out: torch.Tensor | None = None) -> torch.Tensor:
+    """``out[M, N] = a[M, K] @ dequant(W)^T (+ bias)`` on the HIP kernels.
+
+    ``split_k = 0`` lets the library choose its K partition; any value >= 1 fixes it
+    (results are bitwise reproducible for a fixed value).
+    """
+    lib = L.load()
+    if a.dim() != 2:
+        raise ValueError("a must be 2-D")
+    _require_device(a, qweight, scales, qzeros, bias, out)
+    K, N = gemm_dims(qweight, layout)
+    M = int(a.shape[0])
+    if int(a.shape[1]) != K:
+        raise ValueError(f"K mismatch: a has {a.shape[1]}, weight has {K}")
+    if layout == "ref":
+        qweight, scales, qzeros = REPACK_CACHE.get(qweight, scales, qzeros, group_size)
+        layout = "autoawq"
+    a = a.contiguous()
+    qweight, scales = qweight.contiguous(), scales.contiguous()
+    qzeros = qzeros.contiguous() if qzeros is not None else None
+    if out is None:
+        out = torch.empty((M, N), dtype=a.dtype, device=a.device)
+    if bias is not None:
+        bias = bias.contiguous()
+    dev = a.device
+    stream = _stream_ptr(dev)
+    lc = layout_code(layout)
+    ws_bytes = int(lib.awq_w4a16_gemm_workspace_bytes(M, N, K, int(group_size), int(split_k), lc))
+    ws = WORKSPACE.get(dev, stream, ws_bytes) if ws_bytes else None
+    rc = lib.awq_w4a16_gemm(
+        _ptr(a), int(a.stride(0)), _ptr(qweight), _ptr(scales), _ptr(qzeros), _ptr(bias), _ptr(out),
+        int(out.stride(0)), M, N, K, int(group_size), int(split_k), lc, dtype_code(a.dtype),
+        dtype_code(scales.dtype), dtype_code(bias.dtype) if bias is not None else L.DTYPE_NONE,
+        _ptr(ws), ws_bytes if ws is not None else 0, stream)
+    L.check("awq_w4a16_gemm", rc)
+    return out

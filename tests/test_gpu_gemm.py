@@ -1,0 +1,246 @@
+"""GPU parity: HIP kernels (through the C ABI) against the CPU oracle.
+
+Bars (stated per test):
+  * dequantized weights: bit-exact (uint16 patterns / fp32 values equal);
+  * GEMM outputs vs the exact oracle (float64 sum of exact fp16 products): every
+    element within 1 fp16 ulp of the exact value (ulp taken at max(|y|, 1), see
+    ``oracle.awq_oracle.fp16_ulp``), i.e. fp32 accumulation plus one final rounding;
+  * GEMM outputs vs the reference's own CPU path (dequant + F.linear): elementwise
+    |d| <= max(2e-2, 1 ulp(|ref|)) and mean relative error sum|d|/sum|ref| <= 1e-3.
+    The 2e-2 bound alone is below one fp16 ulp for |y| >= 32 (one rounding flip
+    between two fp32 summation orders already exceeds it), hence the ulp clause.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import awq_oracle as O
+from oracle import ref_cpu as R
+from oracle.gen import make_awq_problem
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+
+
+def _lib():
+    from litevllm_amd import ops
+    return ops
+
+
+def _to_dev(p):
+    return {k: (torch.from_numpy(v).to(DEV) if isinstance(v, np.ndarray) else v) for k, v in p.items()}
+
+
+def _note(msg):
+    print(msg, flush=True)
+
+
+def _check_vs_exact(y, ye, what):
+    rep = O.error_report(y, ye)
+    assert rep["max_ulp"] <= 1.0, (what, rep)
+    return rep
+
+
+def _check_vs_ref(y, yr, what):
+    y = np.asarray(y, dtype=np.float64)
+    yr = np.asarray(yr, dtype=np.float64)
+    d = np.abs(y - yr)
+    bound = np.maximum(2e-2, O.fp16_ulp(yr, floor=2.0 ** -14))
+    assert (d <= bound).all(), (what, float(d.max()), float((d / bound).max()))
+    mrel = float(d.sum() / max(np.abs(yr).sum(), 1e-30))
+    assert mrel <= 1e-3, (what, mrel)
+
+
+# ------------------------------------------------------------------ dequant
+@pytest.mark.parametrize("layout", ["autoawq", "kn_seq", "ref"])
+@pytest.mark.parametrize("zp", [True, False])
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("scale_dtype", [torch.float16, torch.bfloat16])
+def test_dequant_bit_exact(layout, zp, out_dtype, scale_dtype):
+    ops = _lib()
+    _note(f"dequant layout={layout} zp={zp} out={out_dtype} scales={scale_dtype}")
+    rng = np.random.default_rng(11)
+    K, N, G = 512, 384, 64
+    W = rng.integers(0, 16, size=(K, N), dtype=np.int32)
+    Z = rng.integers(0, 16, size=(K // G, N), dtype=np.int32)
+    S = (np.abs(rng.standard_normal((K // G, N))) * 0.02 + 1e-4).astype(np.float32)
+    S_t = torch.from_numpy(S).to(scale_dtype)
+    S_np = S_t.float().numpy()                     # the exact scale values used
+    # expected: one rounding of the exact product, by layout orientation
+    exact = (W.reshape(K // G, G, N) - (Z[:, None, :] if zp else 8)).astype(np.float64) * S_np[:, None, :].astype(np.float64)
+    exact = exact.reshape(K, N)
+    if layout == "autoawq":
+        qw, qz, sc = O.pack_awq(W), O.pack_awq(Z), S_t
+    elif layout == "kn_seq":
+        qw, qz, sc = O.pack_ref(W), O.pack_ref(Z), S_t
+    else:
+        qw, qz = O.pack_ref(np.ascontiguousarray(W.T)), O.pack_ref(np.ascontiguousarray(Z.T))
+        sc = S_t.t().contiguous()
+        exact = exact.T
+    out = ops.dequant(torch.from_numpy(qw).to(DEV), sc.to(DEV),
+                      torch.from_numpy(qz).to(DEV) if zp else None, G, layout=layout,
+                      out_dtype=out_dtype).cpu()
+    want = torch.from_numpy(np.ascontiguousarray(exact)).to(out_dtype)
+    assert torch.equal(out.view(torch.int16) if out_dtype != torch.float32 else out.view(torch.int32),
+                       want.view(torch.int16) if out_dtype != torch.float32 else want.view(torch.int32))
+
+
+def test_dequant_matches_numpy_oracle_config0():
+    ops = _lib()
+    p = make_awq_problem(M=1, K=2048, N=5632, group_size=128, seed=0)
+    t = _to_dev(p)
+    w = ops.dequant(t["qweight"], t["scales"], t["qzeros"], 128, layout="autoawq").cpu().numpy()
+    w_ref = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"], 128)
+    assert np.array_equal(w.view(np.uint16), w_ref.view(np.uint16))
+
+
+def test_repack_ref_to_autoawq_on_device():
+    ops = _lib()
+    p = make_awq_problem(M=1, K=1024, N=512, group_size=128, seed=1)
+    qr, zr, sr = O.repack_awq_to_ref(p["qweight"], p["qzeros"], p["scales"])
+    qw, sc, qz = ops.repack_ref_to_autoawq(torch.from_numpy(qr).to(DEV), torch.from_numpy(sr).to(DEV),
+                                           torch.from_numpy(zr).to(DEV), 128)
+    assert np.array_equal(qw.cpu().numpy(), p["qweight"])
+    assert np.array_equal(qz.cpu().numpy(), p["qzeros"])
+    assert np.array_equal(sc.cpu().numpy(), p["scales"])
+
+
+# ------------------------------------------------------------------ GEMM shapes
+SHAPES = [
+    # (M, K, N, G)  -- skinny (M <= 32) and prefill kernels, partial column tiles
+    (1, 256, 512, 128), (1, 2048, 5632, 128), (2, 512, 4096, 128), (3, 1024, 1000 // 8 * 8, 64),
+    (5, 512, 264, 32), (8, 4096, 1024, 128), (16, 1024, 2048, 128), (17, 512, 520, 128),
+    (32, 2048, 1536, 128), (33, 512, 512, 128), (64, 1024, 768, 64), (100, 512, 2056, 128),
+    (256, 1024, 1024, 128), (300, 2048, 512, 128),
+]
+
+
+@pytest.mark.parametrize("M,K,N,G", SHAPES)
+def test_gemm_autoawq_vs_oracle(M, K, N, G):
+    ops = _lib()
+    _note(f"gemm autoawq M={M} K={K} N={N} G={G}")
+    p = make_awq_problem(M=M, K=K, N=N, group_size=G, seed=M * 7 + N)
+    t = _to_dev(p)
+    y = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, layout="autoawq").cpu().numpy()
+    w = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"], G)       # [K, N]
+    _check_vs_exact(y, O.linear_exact(p["x"], w.T), f"M={M} K={K} N={N}")
+    qr, zr, sr = O.repack_awq_to_ref(p["qweight"], p["qzeros"], p["scales"]) if (K // G) % 8 == 0 else (None,) * 3
+    if qr is not None:
+        yr = R.awq_linear_cpu(torch.from_numpy(p["x"]), torch.from_numpy(qr), torch.from_numpy(sr),
+                              torch.from_numpy(zr), G).numpy()
+        _check_vs_ref(y, yr, f"M={M} K={K} N={N}")
+
+
+@pytest.mark.parametrize("M", [1, 7, 40])
+@pytest.mark.parametrize("bias_dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_gemm_bias(M, bias_dtype):
+    ops = _lib()
+    _note(f"gemm bias M={M} {bias_dtype}")
+    K, N, G = 1024, 768, 128
+    p = make_awq_problem(M=M, K=K, N=N, group_size=G, seed=5)
+    t = _to_dev(p)
+    b = torch.randn(N, generator=torch.Generator().manual_seed(3)).to(bias_dtype)
+    y = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, bias=b.to(DEV), layout="autoawq").cpu().numpy()
+    w = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"], G)
+    _check_vs_exact(y, O.linear_exact(p["x"], w.T, b.double().numpy()), f"bias M={M}")
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 1024, 512), (9, 512, 1024), (24, 512, 256), (128, 1024, 512)])
+def test_gemm_bf16_activations(M, K, N):
+    ops = _lib()
+    _note(f"gemm bf16 M={M} K={K} N={N}")
+    G = 128
+    p = make_awq_problem(M=M, K=K, N=N, group_size=G, seed=9)
+    t = _to_dev(p)
+    xb = torch.from_numpy(p["x"]).to(torch.bfloat16)
+    y = ops.gemm(xb.to(DEV), t["qweight"], t["scales"], t["qzeros"], G, layout="autoawq").float().cpu().numpy()
+    # weights rounded once to bf16 from the exact product (fused path, awq_fused_gemm.py:1966-1976)
+    wb = O.bf16_bits_to_f32(O.dequant_awq(p["qweight"], p["scales"], p["qzeros"], G, out_dtype="bfloat16"))
+    ye = xb.double().numpy() @ wb.astype(np.float64)
+    # one bf16 rounding of the fp32 sum: |d| <= 1 bf16 ulp of max(|y|, 1)
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(ye), 1.0))) - 7)
+    assert (np.abs(y - ye) <= ulp).all(), float((np.abs(y - ye) / ulp).max())
+
+
+@pytest.mark.parametrize("M,K,N,G", [(1, 1024, 512, 32), (4, 512, 256, 128), (64, 512, 512, 64)])
+def test_gemm_symmetric(M, K, N, G):
+    ops = _lib()
+    _note(f"gemm symmetric M={M} K={K} N={N} G={G}")
+    p = make_awq_problem(M=M, K=K, N=N, group_size=G, seed=13)
+    t = _to_dev(p)
+    y = ops.gemm(t["x"], t["qweight"], t["scales"], None, G, layout="autoawq").cpu().numpy()
+    w = O.dequant_awq(p["qweight"], p["scales"], None, G, zero_point=False)
+    _check_vs_exact(y, O.linear_exact(p["x"], w.T), "symmetric")
+
+
+def test_gemm_kn_seq_layout():
+    ops = _lib()
+    M, K, N, G = 3, 512, 512, 128
+    p = make_awq_problem(M=M, K=K, N=N, group_size=G, seed=17)
+    W = O.unpack_awq(p["qweight"])
+    Z = O.unpack_awq(p["qzeros"])
+    qw, qz = O.pack_ref(W), O.pack_ref(Z)
+    y = ops.gemm(torch.from_numpy(p["x"]).to(DEV), torch.from_numpy(qw).to(DEV),
+                 torch.from_numpy(p["scales"]).to(DEV), torch.from_numpy(qz).to(DEV), G,
+                 layout="kn_seq").cpu().numpy()
+    w = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"], G)
+    _check_vs_exact(y, O.linear_exact(p["x"], w.T), "kn_seq")
+
+
+# ------------------------------------------------------------------ split-K
+@pytest.mark.parametrize("M", [1, 8, 32])
+def test_split_k_config2_bit_stable(M):
+    """Config 2: K=12288, N=4096, split-K in {1, 4, 8}: each split is bitwise
+    reproducible across calls, and every split is within the bars of the oracle."""
+    ops = _lib()
+    K, N, G = 12288, 4096, 128
+    p = make_awq_problem(M=M, K=K, N=N, group_size=G, seed=2)
+    t = _to_dev(p)
+    w = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"], G)
+    ye = O.linear_exact(p["x"], w.T)
+    for sk in (1, 4, 8):
+        _note(f"split-K M={M} split={sk}")
+        y1 = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, split_k=sk, layout="autoawq")
+        y2 = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, split_k=sk, layout="autoawq")
+        assert torch.equal(y1.view(torch.int16), y2.view(torch.int16)), f"split {sk} not bit-stable"
+        _check_vs_exact(y1.cpu().numpy(), ye, f"split {sk}")
+
+
+# ------------------------------------------------------------------ benchmark configs
+@pytest.mark.parametrize("M,N", [(m, n) for m in (1, 4, 16) for n in (4096, 6144, 24576)])
+def test_config1_decode_sweep(M, N):
+    ops = _lib()
+    _note(f"config1 M={M} N={N}")
+    K, G = 4096, 128
+    p = make_awq_problem(M=M, K=K, N=N, group_size=G, seed=1)
+    t = _to_dev(p)
+    y = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, layout="autoawq").cpu().numpy()
+    w = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"], G)
+    _check_vs_exact(y, O.linear_exact(p["x"], w.T), f"config1 M={M} N={N}")
+    qr, zr, sr = O.repack_awq_to_ref(p["qweight"], p["qzeros"], p["scales"])
+    yr = R.awq_linear_cpu(torch.from_numpy(p["x"]), torch.from_numpy(qr), torch.from_numpy(sr),
+                          torch.from_numpy(zr), G).numpy()
+    _check_vs_ref(y, yr, f"config1 M={M} N={N}")
+
+
+@pytest.mark.parametrize("M,N", [(512, 12288), (2048, 24576)])
+def test_config3_prefill(M, N):
+    """Full-size prefill: every output against a torch fp32 GEMM on the (bit-exact
+    checked) dequantized weight; 128 sampled rows against the exact oracle."""
+    ops = _lib()
+    _note(f"config3 M={M} N={N}")
+    K, G = 4096, 128
+    p = make_awq_problem(M=M, K=K, N=N, group_size=G, seed=3, outliers=True)
+    t = _to_dev(p)
+    y = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, layout="autoawq")
+    wd = ops.dequant(t["qweight"], t["scales"], t["qzeros"], G, layout="autoawq")     # [K, N]
+    w = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"], G)
+    assert np.array_equal(wd.cpu().numpy().view(np.uint16), w.view(np.uint16))
+    y32 = (t["x"].float() @ wd.float())
+    d = (y.float() - y32).abs()
+    ulp = torch.exp2(torch.floor(torch.log2(y32.abs().clamp_min(1.0))) - 10)
+    assert bool((d <= 1.0 * ulp + 1e-3 * y32.abs().clamp_min(1.0) * 2 ** -10).all()), float((d / ulp).max())
+    rows = np.random.default_rng(0).choice(M, size=128, replace=False)
+    ye = O.linear_exact(p["x"][rows], w.T)
+    _check_vs_exact(y.cpu().numpy()[rows], ye, f"config3 M={M} N={N}")
