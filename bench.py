@@ -1,0 +1,246 @@
+"""Benchmark of the AWQ W4A16 hot path on one MI355X.
+
+Workload (``config.workload``): the decode GEMV sweep of the benchmark configuration
+(configs[1]): M in {1, 4, 16}, K = 4096, N in {4096, 6144, 24576}, group 128, AutoAWQ
+packing, fp16 activations.  One *step* = the nine GEMMs once, each on its own weight
+copy; steps rotate over enough copies (>= 1 GiB) that weights are read from HBM, not from
+the 256 MB Infinity Cache.  The whole step is captured once in a HIP graph and replayed, so
+host launch overhead is not timed.
+
+``value`` = algorithmic bytes of one step (weights + scales + zeros + x + y, no split-K
+scratch, no re-reads) x steps / elapsed time, in GB/s.
+
+Extra measurements on the same JSON line:
+  * ``roofline``: the decode kernel at M=1, N=24576 (the heaviest single launch and the
+    headline M=1 target) -- algorithmic bytes per launch / average launch duration from HIP
+    events around back-to-back launches on the launch stream, against 8 TB/s;
+  * ``prefill``: configs[3] at M=2048, N=24576 in TFLOP/s against 2.5 PFLOP/s dense fp16;
+  * ``cpu_baseline``: the reference's CPU path (dequant + F.linear, restated in
+    ``oracle/ref_cpu.py``) on a bounded sample of the same sweep, timed on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+K_DEC, G = 4096, 128
+SWEEP = [(m, n) for m in (1, 4, 16) for n in (4096, 6144, 24576)]
+
+
+def alg_bytes(M, K, N, g=G):
+    return K * N // 2 + (K // g) * N * 2 + (K // g) * (N // 8) * 4 + M * K * 2 + M * N * 2
+
+
+def _weights(torch, K, N, copies, dev, seed):
+    """`copies` independent AutoAWQ-packed weight sets, generated on the device with the
+    benchmark distributions (int4 uniform, zeros uniform, scales |N(0,.02)|+1e-4)."""
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    out = []
+    for _ in range(copies):
+        qw = torch.randint(-2**31, 2**31 - 1, (K, N // 8), dtype=torch.int32, device=dev, generator=gen)
+        qz = torch.randint(-2**31, 2**31 - 1, (K // G, N // 8), dtype=torch.int32, device=dev, generator=gen)
+        sc = (torch.randn((K // G, N), device=dev, generator=gen).abs() * 0.02 + 1e-4).half()
+        out.append((qw, qz, sc))
+    return out
+
+
+def _time_graph(torch, fn, reps, warmup=3):
+    """Capture fn() in a HIP graph, replay `reps` times between events; returns ms/replay."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(warmup):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    g.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        g.replay()
+    end.record()
+    end.synchronize()
+    return start.elapsed_time(end) / reps, g
+
+
+def cpu_baseline(sample_seconds=20.0):
+    """The reference CPU path restated (oracle/ref_cpu.py), cold: dequant + F.linear per call,
+    over the sweep shapes in order until ~sample_seconds of work (at least one full sweep
+    pass when that fits).  Returns GB/s of algorithmic bytes."""
+    import numpy as np
+    import torch
+    from oracle import ref_cpu as R
+
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    cores = max(1, min(cores, 16))
+    torch.set_num_threads(cores)
+    rng = np.random.default_rng(0)
+    done_bytes, t_total, calls, shapes = 0, 0.0, 0, []
+    warm = False
+    for M, N in SWEEP * 4:
+        K = K_DEC
+        qw = torch.from_numpy(rng.integers(-2**31, 2**31 - 1, size=(N, K // 8), dtype=np.int64).astype(np.int32))
+        qz = torch.from_numpy(rng.integers(-2**31, 2**31 - 1, size=(N, K // G // 8), dtype=np.int64).astype(np.int32))
+        sc = torch.from_numpy((np.abs(rng.standard_normal((N, K // G))) * 0.02 + 1e-4).astype(np.float16))
+        x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16))
+        if not warm:
+            R.awq_linear_cpu(x, qw, sc, qz, G)
+            warm = True
+        t0 = time.perf_counter()
+        R.awq_linear_cpu(x, qw, sc, qz, G)
+        dt = time.perf_counter() - t0
+        t_total += dt
+        done_bytes += alg_bytes(M, K, N)
+        calls += 1
+        shapes.append(f"{M}x{K}x{N}")
+        if t_total >= sample_seconds:
+            break
+    return {
+        "value": round(done_bytes / t_total / 1e9, 3), "unit": "GB/s", "cores": int(torch.get_num_threads()),
+        "kind": "port",
+        "sample": f"{calls} cold calls (dequant + F.linear, fp16, K=4096, G=128) over the decode sweep "
+                  f"shapes in order, {t_total:.1f} s of CPU work",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--only", default="", help="profile mode: 'decode-m1n24576' or 'prefill' launches only")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path "
+              "(--gpus must be 1)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from litevllm_amd import ops
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    gen = torch.Generator(device=dev).manual_seed(1)
+
+    if args.only == "decode-m1n24576":
+        W = _weights(torch, K_DEC, 24576, 24, dev, 7)
+        x = torch.randn((1, K_DEC), device=dev, generator=gen).half()
+        for _ in range(args.steps):
+            for qw, qz, sc in W:
+                ops.gemm(x, qw, sc, qz, G, layout="autoawq")
+        torch.cuda.synchronize()
+        return
+    if args.only == "prefill":
+        W = _weights(torch, K_DEC, 24576, 2, dev, 9)
+        x = torch.randn((2048, K_DEC), device=dev, generator=gen).half()
+        for _ in range(args.steps):
+            for qw, qz, sc in W:
+                ops.gemm(x, qw, sc, qz, G, layout="autoawq")
+        torch.cuda.synchronize()
+        return
+
+    # ---- decode sweep: rotate >= 1 GiB of weights ----
+    step_bytes = sum(alg_bytes(m, K_DEC, n) for m, n in SWEEP)
+    wbytes_step = sum(K_DEC * n // 2 + (K_DEC // G) * n * 2 + (K_DEC // G) * (n // 8) * 4 for _, n in SWEEP)
+    copies = max(2, -(-(1 << 30) // wbytes_step))
+    W = {}
+    for i, (m, n) in enumerate(SWEEP):
+        W[(m, n)] = _weights(torch, K_DEC, n, copies, dev, 100 + i)
+    X = {m: torch.randn((m, K_DEC), device=dev, generator=gen).half() for m in (1, 4, 16)}
+    Y = {(m, n): torch.empty((m, n), device=dev, dtype=torch.float16) for m, n in SWEEP}
+
+    def step_fn(c):
+        for m, n in SWEEP:
+            qw, qz, sc = W[(m, n)][c]
+            ops.gemm(X[m], qw, sc, qz, G, layout="autoawq", out=Y[(m, n)])
+
+    def rotation():
+        for c in range(copies):
+            step_fn(c)
+
+    for _ in range(max(1, args.warmup)):
+        rotation()
+    torch.cuda.synchronize()
+    reps = max(1, -(-args.steps // copies))
+    ms_rot, graph = _time_graph(torch, rotation, reps)
+    steps_timed = reps * copies
+    ms_per_step = ms_rot / copies
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    del graph
+
+    # ---- per-shape launch durations (graph of back-to-back launches, rotated copies) ----
+    per_shape = {}
+    for m, n in SWEEP:
+        def one(m=m, n=n):
+            for c in range(copies):
+                qw, qz, sc = W[(m, n)][c]
+                ops.gemm(X[m], qw, sc, qz, G, layout="autoawq", out=Y[(m, n)])
+        ms, g = _time_graph(torch, one, 5)
+        del g
+        us = ms * 1e3 / copies
+        b = alg_bytes(m, K_DEC, n)
+        per_shape[f"M{m}_N{n}"] = {"us": round(us, 3), "GBps": round(b / (us * 1e-6) / 1e9, 1),
+                                   "hbm_frac": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    r = per_shape["M1_N24576"]
+    roof_bytes = alg_bytes(1, K_DEC, 24576)
+    roofline = {"bound": "hbm", "achieved": r["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(r["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "skinny_kn_kernel M=1 K=4096 N=24576", "bytes_per_launch": roof_bytes,
+                "avg_launch_us": r["us"]}
+    del W
+
+    # ---- prefill (configs[3], M=2048, N=24576) ----
+    prefill = None
+    if not args.no_prefill:
+        M, N = 2048, 24576
+        Wp = _weights(torch, K_DEC, N, 3, dev, 9)
+        xp = torch.randn((M, K_DEC), device=dev, generator=gen).half()
+        yp = torch.empty((M, N), device=dev, dtype=torch.float16)
+
+        def pf():
+            for qw, qz, sc in Wp:
+                ops.gemm(xp, qw, sc, qz, G, layout="autoawq", out=yp)
+        ms, g = _time_graph(torch, pf, 3)
+        del g
+        us = ms * 1e3 / len(Wp)
+        tflops = 2.0 * M * N * K_DEC / (us * 1e-6) / 1e12
+        prefill = {"M": M, "K": K_DEC, "N": N, "us": round(us, 1), "TFLOPs": round(tflops, 1),
+                   "mfma_frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "peak_TFLOPs": MFMA_F16_PEAK_TFLOPS}
+        del Wp
+
+    line = {
+        "metric": "AWQ W4A16 decode GEMV sweep throughput (algorithmic GB/s, M=1-16)",
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps_timed,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f16 activations, int4 weights (fp32 accumulate)",
+        "data": "synthetic (seeded int4/zeros/scales/activations with the benchmark distributions)",
+        "config": {"workload": "configs[1] decode sweep: M in {1,4,16}, K=4096, N in {4096,6144,24576}, "
+                               "group 128, AutoAWQ packing", "weight_copies_rotated": copies,
+                   "bytes_per_step": step_bytes},
+        "roofline": roofline,
+        "per_shape": per_shape,
+        "prefill": prefill,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -86,10 +86,11 @@ int awq_w4a16_dequant(const int32_t* qweight, const void* scales, const int32_t*
                       int32_t scale_dtype, int32_t out_dtype, void* stream);
 
 /* Workspace bytes awq_w4a16_gemm needs for these arguments (0 if none).  The workspace
- * holds fp32 split-K partials and per-tile arrival counters.  The counter region must be
- * zero the first time a workspace is used; every call leaves it zero again, so a
- * workspace allocated zeroed once can be reused by later calls on the same stream.
- * Two calls that may run concurrently must not share a workspace. */
+ * starts with a fixed 64 KiB region of per-tile arrival counters followed by fp32 split-K
+ * partials.  The counter region must be zero the first time a workspace is used; every
+ * call leaves it zero again, so a workspace allocated zeroed once can be reused by later
+ * calls of any shape on the same stream.  Two calls that may run concurrently must not
+ * share a workspace. */
 size_t awq_w4a16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_size,
                                       int32_t split_k, int32_t layout);
 

@@ -45,13 +45,15 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // Column offset held by nibble i of a packed word.
 template <bool SEQ>
 __host__ __device__ constexpr int nib_col(int i) {
-  return SEQ ? i : ((i & 1) ? 4 + (i >> 1) : (i >> 1));  // AutoAWQ order {0,2,4,6,1,3,5,7}
+  return SEQ ? i : (i < 4 ? 2 * i : 2 * (i - 4) + 1);  // AutoAWQ order {0,2,4,6,1,3,5,7}
 }
 // Nibble holding column offset c (inverse of nib_col).
 template <bool SEQ>
 __host__ __device__ constexpr int col_nib(int c) {
-  return SEQ ? c : (c < 4 ? 2 * c : 2 * (c - 4) + 1);
+  return SEQ ? c : ((c & 1) ? 4 + (c >> 1) : (c >> 1));
 }
+static_assert(nib_col<false>(1) == 2 && nib_col<false>(4) == 1 && nib_col<false>(7) == 7, "AWQ order");
+static_assert(col_nib<false>(nib_col<false>(3)) == 3 && col_nib<false>(nib_col<false>(6)) == 6, "inverse");
 
 __device__ __forceinline__ f16x2 as_h2(uint32_t u) { return __builtin_bit_cast(f16x2, u); }
 __device__ __forceinline__ uint32_t as_u(f16x2 h) { return __builtin_bit_cast(uint32_t, h); }
@@ -84,10 +86,21 @@ __device__ __forceinline__ float bits2f(uint16_t b) {
 //   P odd : (bits & 0x00F000F0) | 0x5400  ->    64 + q  (nibble in mantissa bits 4-7,
 //                                                          exponent of 64 has ulp 1/16)
 // P >= 2 first shifts the word right by 8.  Both forms are exact.
+// The masks and magic exponents live in VGPRs (MagicK) so that each nibble pair costs a
+// single v_and_or_b32: gfx9 VOP3 encodings cannot carry 32-bit literals, and with literal
+// operands the compiler splits the operation into v_and_b32 + v_or_b32.
+struct MagicK {
+  uint32_t lo_mask, hi_mask, lo_magic, hi_magic;
+};
+__device__ __forceinline__ MagicK magic_consts() {
+  MagicK k{0x000F000Fu, 0x00F000F0u, 0x64006400u, 0x54005400u};
+  asm volatile("" : "+v"(k.lo_mask), "+v"(k.hi_mask), "+v"(k.lo_magic), "+v"(k.hi_magic));
+  return k;
+}
 template <int P>
-__device__ __forceinline__ uint32_t magic_bits(uint32_t m) {
+__device__ __forceinline__ uint32_t magic_bits(uint32_t m, const MagicK& k) {
   const uint32_t v = (P >= 2) ? (m >> 8) : m;
-  return (P & 1) ? ((v & 0x00F000F0u) | 0x54005400u) : ((v & 0x000F000Fu) | 0x64006400u);
+  return (P & 1) ? ((v & k.hi_mask) | k.hi_magic) : ((v & k.lo_mask) | k.lo_magic);
 }
 // Zero operand matching magic_bits<P>: the same bias plus z, broadcast to both halves.
 __device__ __forceinline__ uint32_t zero_magic(int p_odd, uint32_t z) {
@@ -228,51 +241,62 @@ struct GemmArgs {
   int bias_dtype;
 };
 
-// Per-group constants of the 8 columns of packed word `word` (KN layouts).
-template <bool SEQ, bool ZP, bool FAST>
-__device__ __forceinline__ void load_word_consts(const GemmArgs& p, int g, int word,
-                                                 ColConst (&cc)[8]) {
-  const u32x4 s4 = *(const u32x4*)(p.sc + (int64_t)g * p.N + 8 * word);
-  const uint32_t zw = ZP ? p.qz[(int64_t)g * (p.N >> 3) + word] : 0x88888888u;
+// Raw per-group constants of one packed word: 8 scales (16 bytes) and the zero word.
+struct WordSZ {
+  u32x4 s4;
+  uint32_t zw;
+};
+
+template <bool ZP>
+__device__ __forceinline__ WordSZ load_sz(const GemmArgs& p, int g, int word) {
+  WordSZ r;
+  r.s4 = *(const u32x4*)(p.sc + (int64_t)g * p.N + 8 * word);
+  r.zw = ZP ? p.qz[(int64_t)g * (p.N >> 3) + word] : 0x88888888u;
+  return r;
+}
+
+// Per-column dequant constants of the 8 nibbles of a word.
+template <bool SEQ, bool FAST>
+__device__ __forceinline__ void prep_consts(const WordSZ& sz, bool scale_bf16, ColConst (&cc)[8]) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int c = nib_col<SEQ>(i);
-    const uint32_t sbits = (s4[c >> 1] >> (16 * (c & 1))) & 0xFFFFu;
-    cc[i].zm = zero_magic(i & 1, (zw >> (4 * i)) & 0xF);
-    cc[i].sc = sbits * 0x00010001u;
-    cc[i].scf = 0.0f;
-  }
-}
-template <bool SEQ, bool ZP>
-__device__ __forceinline__ void load_word_consts_generic(const GemmArgs& p, int g, int word,
-                                                         bool scale_bf16, ColConst (&cc)[8]) {
-  const u32x4 s4 = *(const u32x4*)(p.sc + (int64_t)g * p.N + 8 * word);
-  const uint32_t zw = ZP ? p.qz[(int64_t)g * (p.N >> 3) + word] : 0x88888888u;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int c = nib_col<SEQ>(i);
-    const uint16_t sbits = (uint16_t)((s4[c >> 1] >> (16 * (c & 1))) & 0xFFFFu);
-    cc[i].zm = zero_magic(i & 1, (zw >> (4 * i)) & 0xF);
-    cc[i].sc = 0;
-    cc[i].scf = scale_bf16 ? bf_bits2f(sbits) : h_bits2f(sbits);
+    const uint32_t sbits = (sz.s4[c >> 1] >> (16 * (c & 1))) & 0xFFFFu;
+    cc[i].zm = zero_magic(i & 1, (sz.zw >> (4 * i)) & 0xF);
+    if constexpr (FAST) {
+      cc[i].sc = sbits * 0x00010001u;
+      cc[i].scf = 0.0f;
+    } else {
+      cc[i].sc = 0;
+      cc[i].scf = scale_bf16 ? bf_bits2f((uint16_t)sbits) : h_bits2f((uint16_t)sbits);
+    }
   }
 }
 
-// Row-pair two words of one column-word (rows k, k+1) and return the MFMA operand
-// register for nibble i: bits [15:0] = row k, bits [31:16] = row k+1.
-template <int I>
-__device__ __forceinline__ uint32_t pair_magic(uint32_t w0, uint32_t w1) {
-  const uint32_t m = (I < 4) ? ((w0 & 0xFFFFu) | (w1 << 16)) : ((w0 >> 16) | (w1 & 0xFFFF0000u));
-  return magic_bits<I & 3>(m);
+// Row pairing with one byte permute: lo16(w0) | lo16(w1) << 16 and hi16(w0) | hi16(w1) << 16.
+// (v_perm_b32 selects bytes 0-3 from its second operand and 4-7 from its first.)
+__device__ __forceinline__ uint32_t pair_lo(uint32_t w0, uint32_t w1) {
+  return __builtin_amdgcn_perm(w1, w0, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t pair_hi(uint32_t w0, uint32_t w1) {
+  return __builtin_amdgcn_perm(w1, w0, 0x07060302u);
 }
 
-// Eight rows (k .. k+7) of one packed word -> MFMA operand (8 K-consecutive values) of nibble I.
+// Eight rows (k .. k+7) of one packed word, pre-paired into lo/hi words, -> MFMA operand
+// (8 K-consecutive values of the column held by nibble I).
 template <int I, bool FAST, typename T>
-__device__ __forceinline__ u32x4 word_rows_operand(const uint32_t (&w)[8], const ColConst& cc) {
+__device__ __forceinline__ u32x4 rows_operand(const uint32_t (&mlo)[4], const uint32_t (&mhi)[4],
+                                              const ColConst& cc, const MagicK& k) {
   u32x4 r;
 #pragma unroll
-  for (int u = 0; u < 4; ++u) r[u] = deq2<FAST, T>(pair_magic<I>(w[2 * u], w[2 * u + 1]), cc);
+  for (int u = 0; u < 4; ++u) r[u] = deq2<FAST, T>(magic_bits<I & 3>(I < 4 ? mlo[u] : mhi[u], k), cc);
   return r;
+}
+
+// Buffer resource over a whole tensor (raw addressing, bounds = nbytes, loads past the end
+// return zero).  Keeps per-row addresses out of VGPRs: the row offset rides in an SGPR.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t nbytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)nbytes, 0x00020000);
 }
 
 // ----------------------------------------------------------------------------------
@@ -282,14 +306,37 @@ __device__ __forceinline__ u32x4 word_rows_operand(const uint32_t (&w)[8], const
 //  32-row k-step, rows 8q .. 8q+7.  For each (w, nibble i) the lane builds one 16x32 MFMA
 //  operand (16 weight columns x 32 k) and multiplies it with the activation operand
 //  (32 k x 16 tokens), so a wave covers 128*WPL columns x 16*MT tokens.
-template <int WPL, int MT, bool SEQ, bool ZP, typename T, bool FAST>
-__global__ void __launch_bounds__(256) skinny_kn_kernel(const GemmArgs p, int scale_bf16) {
+//
+//  Work is cut in whole quantization groups: split s of the grid covers groups
+//  [s*I, (s+1)*I), and each of the 4 waves takes a contiguous quarter of those.  A wave's
+//  loop handles 4 k-steps per iteration (4/SPG groups, SPG = k-steps per group) with a
+//  4-deep register ring: while slot u is computed, the loads for the same slot of the next
+//  iteration are already queued, and the group constants of the next iteration are loaded
+//  once per group.  The body is straight-line, so the compiler's counter waits let the next
+//  iteration's loads run under the current iteration's math.
+//
+//  Split-K: with nsplit > 1 every block publishes its fp32 partial tile with device-coherent
+//  (sc0 sc1) stores, waits for them, and bumps the tile's arrival counter; the block that
+//  arrives last reads all partials with device-coherent loads and sums them in split order.
+//  No cache-wide writeback/invalidate fence is needed because every byte exchanged between
+//  blocks bypasses the non-coherent part of the per-XCD L2.
+constexpr int kCoherent = 0x11;  // buffer cache-policy bits sc0 | sc1: device-coherent access
+
+#ifndef AWQ_SKINNY_WAVES_PER_EU
+#define AWQ_SKINNY_WAVES_PER_EU 2
+#endif
+template <int WPL, int MT, int SPG, bool SEQ, bool ZP, typename T, bool FAST>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AWQ_SKINNY_WAVES_PER_EU, AWQ_SKINNY_WAVES_PER_EU)))
+skinny_kn_kernel(const GemmArgs p, int scale_bf16) {
   constexpr int NACC = WPL * 8 * MT;  // f32x4 accumulators per lane
   constexpr int CH = NACC < 16 ? NACC : 16;
+  constexpr int PF = 4;               // k-steps per loop iteration (ring depth)
+  constexpr int IG = PF / SPG;        // groups per iteration
   __shared__ f32x4 red[3 * CH * 64];
   __shared__ int s_last;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR) by construction
   const int q = lane >> 4, r = lane & 15;
   const int NW = p.N >> 3;
   const int tile = blockIdx.x, split = blockIdx.y;
@@ -297,13 +344,13 @@ __global__ void __launch_bounds__(256) skinny_kn_kernel(const GemmArgs p, int sc
   const bool wvalid = word0 < NW;
   const int wld = wvalid ? word0 : 0;  // clamped, always in bounds
 
-  const int nk = p.K >> 5;
-  const int s0 = split * p.steps_per_split;
-  const int s1 = min(nk, s0 + p.steps_per_split);
-  const int len = max(0, s1 - s0);
-  const int per = (len + 3) >> 2;
-  const int ws0 = s0 + wave * per;
-  const int ws1 = min(s1, ws0 + per);
+  // group range of this wave
+  const int ngroups = p.K / p.G;
+  const int gs0 = split * p.steps_per_split;  // steps_per_split counts groups here
+  const int gs1 = min(ngroups, gs0 + p.steps_per_split);
+  const int per = (max(0, gs1 - gs0) + 3) >> 2;
+  const int wg0 = min(gs1, gs0 + wave * per);
+  const int wg1 = min(gs1, wg0 + per);
 
   f32x4 acc[WPL][8][MT];
 #pragma unroll
@@ -313,70 +360,111 @@ __global__ void __launch_bounds__(256) skinny_kn_kernel(const GemmArgs p, int sc
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) acc[w][i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  ColConst cc[WPL][8];
-  int cur_g = -1;
+  if (wg0 < wg1) {
+    const int ks_begin = wg0 * SPG, ks_end = wg1 * SPG;  // k-steps [ks_begin, ks_end)
+    const int ks_last = ks_end - 1;
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(p.qw, (uint32_t)((uint64_t)p.K * NW * 4u));
+    const uint32_t row_bytes = (uint32_t)NW * 4u;
+    const uint32_t lane_off = (uint32_t)(8 * q) * row_bytes + (uint32_t)wld * 4u;
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(p.a, (uint32_t)((uint64_t)p.M * (uint64_t)p.lda * 2u));
+    const uint32_t x_lane_off = ((uint32_t)r * (uint32_t)p.lda + 8u * (uint32_t)q) * 2u;
+    const MagicK mk = magic_consts();
 
-  uint32_t raw[8][WPL];
-  u32x4 xa[MT];
-  auto load_step = [&](int ks, uint32_t (&dst)[8][WPL], u32x4 (&xd)[MT]) {
-    const int k = ks * 32 + 8 * q;
+    uint32_t raw[PF][8][WPL];
+    u32x4 xr[PF][MT];
+    WordSZ szc[IG][WPL];  // raw constants of the groups of the iteration being computed
+    ColConst cc[WPL][8];
+
+    auto issue = [&](int ks, uint32_t (&dst)[8][WPL], u32x4 (&xd)[MT]) {
+      const uint32_t kbase = (uint32_t)ks * 32u * row_bytes;  // wave-uniform
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t* src = p.qw + (int64_t)(k + j) * NW + wld;
-      if constexpr (WPL == 4) {
-        const u32x4 v = __builtin_nontemporal_load((const u32x4*)src);
-        dst[j][0] = v[0]; dst[j][1] = v[1]; dst[j][2] = v[2]; dst[j][3] = v[3];
-      } else if constexpr (WPL == 2) {
-        const u32x2 v = __builtin_nontemporal_load((const u32x2*)src);
-        dst[j][0] = v[0]; dst[j][1] = v[1];
-      } else {
-        dst[j][0] = __builtin_nontemporal_load(src);
+      for (int j = 0; j < 8; ++j) {
+        const int soff = (int)(kbase + (uint32_t)j * row_bytes);
+        if constexpr (WPL == 4) {
+          const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, (int)lane_off, soff, 2));
+          dst[j][0] = v[0]; dst[j][1] = v[1]; dst[j][2] = v[2]; dst[j][3] = v[3];
+        } else if constexpr (WPL == 2) {
+          const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(wrs, (int)lane_off, soff, 2));
+          dst[j][0] = v[0]; dst[j][1] = v[1];
+        } else {
+          dst[j][0] = __builtin_amdgcn_raw_buffer_load_b32(wrs, (int)lane_off, soff, 2);
+        }
       }
-    }
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int row = mt * 16 + r;
-      xd[mt] = (row < p.M) ? *(const u32x4*)(p.a + (int64_t)row * p.lda + ks * 32 + 8 * q)
-                           : u32x4{0u, 0u, 0u, 0u};
-    }
-  };
-
-  if (ws0 < ws1) load_step(ws0, raw, xa);
-  for (int ks = ws0; ks < ws1; ++ks) {
-    uint32_t nraw[8][WPL];
-    u32x4 nxa[MT];
-    if (ks + 1 < ws1) load_step(ks + 1, nraw, nxa);
-    const int g = (ks * 32) / p.G;
-    if (g != cur_g) {
-      cur_g = g;
+      for (int mt = 0; mt < MT; ++mt) {
+        // rows >= M fall outside the buffer range and read as zero: no branch, so the
+        // compiler's counter waits stay exact across the loop
+        const uint32_t xoff = ((uint32_t)(mt * 16) * (uint32_t)p.lda + (uint32_t)(ks * 32)) * 2u;
+        xd[mt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)x_lane_off, (int)xoff, 0));
+      }
+    };
+    // group constants through buffer loads too: as intrinsic calls they are not merged
+    // with the prologue's loads into one load at the loop header (which would put them
+    // right before their use and stall every group boundary)
+    const __amdgpu_buffer_rsrc_t srs = make_rsrc(p.sc, (uint32_t)((uint64_t)ngroups * p.N * 2u));
+    const __amdgpu_buffer_rsrc_t zrs = make_rsrc(p.qz, ZP ? (uint32_t)((uint64_t)ngroups * NW * 4u) : 0u);
+    auto issue_sz = [&](int g, WordSZ (&dst)[WPL]) {
+      g = min(g, wg1 - 1);
+      const int s_soff = (int)((uint32_t)g * (uint32_t)p.N * 2u);
+      const int z_soff = (int)((uint32_t)g * (uint32_t)NW * 4u);
 #pragma unroll
       for (int w = 0; w < WPL; ++w) {
-        if constexpr (FAST) load_word_consts<SEQ, ZP, true>(p, g, wld + w, cc[w]);
-        else load_word_consts_generic<SEQ, ZP>(p, g, wld + w, scale_bf16 != 0, cc[w]);
+        dst[w].s4 = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(srs, (int)(16u * (uint32_t)(wld + w)), s_soff, 0));
+        dst[w].zw = ZP ? __builtin_amdgcn_raw_buffer_load_b32(zrs, (int)(4u * (uint32_t)(wld + w)), z_soff, 0) : 0x88888888u;
       }
-    }
+    };
+    auto compute = [&](const uint32_t (&rw)[8][WPL], const u32x4 (&xv)[MT]) {
 #pragma unroll
-    for (int w = 0; w < WPL; ++w) {
-      uint32_t col[8];
+      for (int w = 0; w < WPL; ++w) {
+        uint32_t mlo[4], mhi[4];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) col[j] = raw[j][w];
+        for (int u = 0; u < 4; ++u) {
+          mlo[u] = pair_lo(rw[2 * u][w], rw[2 * u + 1][w]);
+          mhi[u] = pair_hi(rw[2 * u][w], rw[2 * u + 1][w]);
+        }
 #define AWQ_SKINNY_NIB(I)                                                        \
-      {                                                                          \
-        const u32x4 op = word_rows_operand<I, FAST, T>(col, cc[w][I]);           \
-        _Pragma("unroll") for (int mt = 0; mt < MT; ++mt)                        \
-            acc[w][I][mt] = MfmaOp<T>::run(op, xa[mt], acc[w][I][mt]);          \
-      }
-      AWQ_SKINNY_NIB(0) AWQ_SKINNY_NIB(1) AWQ_SKINNY_NIB(2) AWQ_SKINNY_NIB(3)
-      AWQ_SKINNY_NIB(4) AWQ_SKINNY_NIB(5) AWQ_SKINNY_NIB(6) AWQ_SKINNY_NIB(7)
+        {                                                                        \
+          const u32x4 op = rows_operand<I, FAST, T>(mlo, mhi, cc[w][I], mk);     \
+          _Pragma("unroll") for (int mt = 0; mt < MT; ++mt)                      \
+              acc[w][I][mt] = MfmaOp<T>::run(op, xv[mt], acc[w][I][mt]);         \
+        }
+        AWQ_SKINNY_NIB(0) AWQ_SKINNY_NIB(1) AWQ_SKINNY_NIB(2) AWQ_SKINNY_NIB(3)
+        AWQ_SKINNY_NIB(4) AWQ_SKINNY_NIB(5) AWQ_SKINNY_NIB(6) AWQ_SKINNY_NIB(7)
 #undef AWQ_SKINNY_NIB
+      }
+    };
+    auto prep = [&](const WordSZ (&szv)[WPL]) {
+#pragma unroll
+      for (int w = 0; w < WPL; ++w) prep_consts<SEQ, FAST>(szv[w], scale_bf16 != 0, cc[w]);
+    };
+
+    // prologue: first iteration's k-steps.  Slots past the wave's range re-load its last
+    // k-step (cache hits, never used).  The slot that starts a group also carries that
+    // group's raw constants, so they travel (and are waited for) with its weight words.
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+      if (u % SPG == 0) issue_sz(min(ks_begin + u, ks_last) / SPG, szc[u / SPG]);
+      issue(min(ks_begin + u, ks_last), raw[u], xr[u]);
     }
-    if (ks + 1 < ws1) {
+
+    int ks0 = ks_begin;
+    for (; ks0 + PF <= ks_end; ks0 += PF) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
+      for (int u = 0; u < PF; ++u) {
+        if (u % SPG == 0) prep(szc[u / SPG]);
+        compute(raw[u], xr[u]);
+        const int nks = min(ks0 + u + PF, ks_last);
+        if (u % SPG == 0) issue_sz(nks / SPG, szc[u / SPG]);
+        issue(nks, raw[u], xr[u]);
+      }
+    }
+    // tail (only when the wave's range is not a multiple of PF k-steps)
 #pragma unroll
-        for (int w = 0; w < WPL; ++w) raw[j][w] = nraw[j][w];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) xa[mt] = nxa[mt];
+    for (int u = 0; u < PF; ++u) {
+      if (ks0 + u < ks_end) {
+        if (u % SPG == 0) prep(szc[u / SPG]);
+        compute(raw[u], xr[u]);
+      }
     }
   }
 
@@ -420,9 +508,10 @@ __global__ void __launch_bounds__(256) skinny_kn_kernel(const GemmArgs p, int sc
             if (word >= NW) continue;
             float o[8];
 #pragma unroll
-            for (int cidx = 0; cidx < 8; ++cidx) {
-              o[cidx] = acc[w][col_nib<SEQ>(cidx)][mt][v];
-              if (p.bias) o[cidx] += load_bias(p.bias, p.bias_dtype, 8 * word + cidx);
+            for (int cidx = 0; cidx < 8; ++cidx) o[cidx] = acc[w][col_nib<SEQ>(cidx)][mt][v];
+            if (p.bias) {
+#pragma unroll
+              for (int cidx = 0; cidx < 8; ++cidx) o[cidx] += load_bias(p.bias, p.bias_dtype, 8 * word + cidx);
             }
             u32x4 st;
             st[0] = pack2<T>(o[0], o[1]);
@@ -437,9 +526,11 @@ __global__ void __launch_bounds__(256) skinny_kn_kernel(const GemmArgs p, int sc
     return;
   }
 
-  // ---- split-K: publish fp32 partials, the last block of this tile reduces them ----
+  // ---- split-K: publish the fp32 partial tile, the last block of the tile reduces ----
+  const uint32_t part_bytes = (uint32_t)p.nsplit * (uint32_t)M * (uint32_t)N * 4u;
+  const __amdgpu_buffer_rsrc_t prs = make_rsrc(p.partial, part_bytes);
   if (wave == 0) {
-    float* part = p.partial + (int64_t)split * M * N;
+    const uint32_t split_off = (uint32_t)split * (uint32_t)M * (uint32_t)N * 4u;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int m = mt * 16 + r;
@@ -450,43 +541,46 @@ __global__ void __launch_bounds__(256) skinny_kn_kernel(const GemmArgs p, int sc
         for (int w = 0; w < WPL; ++w) {
           const int word = tile * 16 * WPL + (4 * q + v) * WPL + w;
           if (word >= NW) continue;
-          f32x4* dst = (f32x4*)(part + (int64_t)m * N + 8 * word);
-          dst[0] = f32x4{acc[w][col_nib<SEQ>(0)][mt][v], acc[w][col_nib<SEQ>(1)][mt][v],
-                         acc[w][col_nib<SEQ>(2)][mt][v], acc[w][col_nib<SEQ>(3)][mt][v]};
-          dst[1] = f32x4{acc[w][col_nib<SEQ>(4)][mt][v], acc[w][col_nib<SEQ>(5)][mt][v],
-                         acc[w][col_nib<SEQ>(6)][mt][v], acc[w][col_nib<SEQ>(7)][mt][v]};
+          const uint32_t off = ((uint32_t)m * (uint32_t)N + 8u * (uint32_t)word) * 4u;
+          const f32x4 lo = f32x4{acc[w][col_nib<SEQ>(0)][mt][v], acc[w][col_nib<SEQ>(1)][mt][v],
+                                 acc[w][col_nib<SEQ>(2)][mt][v], acc[w][col_nib<SEQ>(3)][mt][v]};
+          const f32x4 hi = f32x4{acc[w][col_nib<SEQ>(4)][mt][v], acc[w][col_nib<SEQ>(5)][mt][v],
+                                 acc[w][col_nib<SEQ>(6)][mt][v], acc[w][col_nib<SEQ>(7)][mt][v]};
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, lo), prs, (int)off, (int)split_off, kCoherent);
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, hi), prs, (int)(off + 16u), (int)split_off, kCoherent);
         }
       }
     }
   }
-  __threadfence();
+  __builtin_amdgcn_s_waitcnt(0);  // the partial stores have completed (device-coherent)
   __syncthreads();
   if (tid == 0) {
-    const int prev = atomicAdd(&p.counters[tile], 1);
+    const int prev = __hip_atomic_fetch_add(&p.counters[tile], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = (prev == p.nsplit - 1);
   }
   __syncthreads();
   if (!s_last) return;
-  __threadfence();
   const int col0 = tile * 16 * WPL * 8;
   const int ncols = min(16 * WPL * 8, N - col0);
   const int nq = ncols >> 2;  // float4 chunks per row
   for (int idx = tid; idx < M * nq; idx += 256) {
     const int m = idx / nq, cq = idx - m * nq;
     const int col = col0 + 4 * cq;
-    const float* src = p.partial + (int64_t)m * N + col;
-    f32x4 s = *(const f32x4*)src;
-    for (int sp = 1; sp < p.nsplit; ++sp) s += *(const f32x4*)(src + (int64_t)sp * M * N);
+    const uint32_t off = ((uint32_t)m * (uint32_t)N + (uint32_t)col) * 4u;
+    const uint32_t sstride = (uint32_t)M * (uint32_t)N * 4u;
+    f32x4 sum = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(prs, (int)off, 0, kCoherent));
+    for (int sp = 1; sp < p.nsplit; ++sp)
+      sum += __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(prs, (int)off, (int)(sp * sstride), kCoherent));
     if (p.bias) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) s[e] += load_bias(p.bias, p.bias_dtype, col + e);
+      for (int e = 0; e < 4; ++e) sum[e] += load_bias(p.bias, p.bias_dtype, col + e);
     }
     u32x2 st;
-    st[0] = pack2<T>(s[0], s[1]);
-    st[1] = pack2<T>(s[2], s[3]);
+    st[0] = pack2<T>(sum[0], sum[1]);
+    st[1] = pack2<T>(sum[2], sum[3]);
     *(u32x2*)(p.c + (int64_t)m * p.ldc + col) = st;
   }
-  if (tid == 0) p.counters[tile] = 0;  // leave the workspace ready for the next call
+  if (tid == 0) __hip_atomic_store(&p.counters[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ----------------------------------------------------------------------------------
@@ -546,36 +640,40 @@ __global__ void __launch_bounds__(256) gemm_kn_kernel(const GemmArgs p, int scal
     }
   };
   uint32_t braw[2][8];
-  auto load_b = [&](int st, uint32_t (&dst)[2][8]) {
+  WordSZ bsz[2];
+  auto load_b = [&](int st, uint32_t (&dst)[2][8], WordSZ (&szd)[2]) {
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub)
+    for (int sub = 0; sub < 2; ++sub) {
 #pragma unroll
       for (int j = 0; j < 8; ++j)
         dst[sub][j] = __builtin_nontemporal_load(p.qw + (int64_t)(st * BK + sub * 32 + 8 * q + j) * NW + wld);
+      szd[sub] = load_sz<ZP>(p, (st * BK + sub * 32) / p.G, wld);
+    }
   };
 
   ColConst cc[8];
   int cur_g = -1;
+  const MagicK mk = magic_consts();
 
   load_a(0);
   store_a(0);
-  load_b(0, braw);
+  load_b(0, braw, bsz);
   __syncthreads();
 
   for (int st = 0; st < nst; ++st) {
     const int buf = st & 1;
     uint32_t bnext[2][8];
+    WordSZ sznext[2];
     if (st + 1 < nst) {
       load_a(st + 1);
-      load_b(st + 1, bnext);
+      load_b(st + 1, bnext, sznext);
     }
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
       const int g = (st * BK + sub * 32) / p.G;
       if (g != cur_g) {
         cur_g = g;
-        if constexpr (FAST) load_word_consts<SEQ, ZP, true>(p, g, wld, cc);
-        else load_word_consts_generic<SEQ, ZP>(p, g, wld, scale_bf16 != 0, cc);
+        prep_consts<SEQ, FAST>(bsz[sub], scale_bf16 != 0, cc);
       }
       u32x4 af[MTL];
 #pragma unroll
@@ -584,9 +682,15 @@ __global__ void __launch_bounds__(256) gemm_kn_kernel(const GemmArgs p, int scal
         const int ch = sub * 4 + q;
         af[mt] = lds_a[buf][row * 8 + (ch ^ (row & 7))];
       }
+      uint32_t mlo[4], mhi[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        mlo[u] = pair_lo(braw[sub][2 * u], braw[sub][2 * u + 1]);
+        mhi[u] = pair_hi(braw[sub][2 * u], braw[sub][2 * u + 1]);
+      }
 #define AWQ_GEMM_NIB(I)                                                          \
       {                                                                          \
-        const u32x4 bop = word_rows_operand<I, FAST, T>(braw[sub], cc[I]);       \
+        const u32x4 bop = rows_operand<I, FAST, T>(mlo, mhi, cc[I], mk);         \
         _Pragma("unroll") for (int mt = 0; mt < MTL; ++mt)                       \
             acc[mt][I] = MfmaOp<T>::run(af[mt], bop, acc[mt][I]);                \
       }
@@ -597,9 +701,11 @@ __global__ void __launch_bounds__(256) gemm_kn_kernel(const GemmArgs p, int scal
     if (st + 1 < nst) {
       store_a(buf ^ 1);
 #pragma unroll
-      for (int sub = 0; sub < 2; ++sub)
+      for (int sub = 0; sub < 2; ++sub) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) braw[sub][j] = bnext[sub][j];
+        bsz[sub] = sznext[sub];
+      }
     }
     __syncthreads();
   }
@@ -705,6 +811,12 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 bool dtype_16(int d) { return d == AWQ_DTYPE_F16 || d == AWQ_DTYPE_BF16; }
 
 // ---- skinny planning ----
+// Workspace layout: [0, AWQ_COUNTER_BYTES) arrival counters (zero between calls), then fp32
+// partials.  The counter region sits at a fixed offset so calls of different shapes that
+// share one workspace always find it zeroed.
+constexpr size_t AWQ_COUNTER_BYTES = 65536;
+constexpr int SKINNY_PF = 4;
+
 struct SkinnyPlan {
   int wpl, mt;
   int tiles, nsplit, steps_per_split;
@@ -713,49 +825,49 @@ struct SkinnyPlan {
 
 int pick_wpl(int64_t M, int64_t N) {
   const int64_t nw = N / 8;
-  int wpl = (M <= 8) ? 4 : 2;
+  int wpl = 2;
   while (wpl > 1 && (nw % wpl) != 0) wpl >>= 1;
   return wpl;
 }
 
-SkinnyPlan plan_skinny(int64_t M, int64_t N, int64_t K, int split_k) {
+SkinnyPlan plan_skinny(int64_t M, int64_t N, int64_t K, int64_t G, int split_k) {
   SkinnyPlan s{};
   s.wpl = pick_wpl(M, N);
   s.mt = (M > 16) ? 2 : 1;
+  if (s.mt == 2) s.wpl = 1;
   const int64_t cols = 16 * s.wpl * 8;
   s.tiles = (int)cdiv(N, cols);
-  const int64_t nk = K / 32;
+  const int64_t ng = K / G;       // partition unit: one quantization group
+  const int64_t spg = G / 32;     // k-steps per group
   int64_t ns;
   if (split_k > 0) {
     ns = split_k;
   } else {
-    // aim for whole rounds of resident blocks with at least one k-step per wave
-    const int64_t slots = (int64_t)num_cus() * (s.wpl == 4 ? 1 : 2);
-    const int64_t max_ns = std::max<int64_t>(1, nk / 4);
+    // Fill the chip with one round of resident blocks (2 per CU) while giving every wave
+    // at least 8 k-steps where the problem allows; prefer fewer partitions on ties.
+    const int64_t slots = (int64_t)num_cus() * 2;
+    const int64_t max_ns = std::max<int64_t>(1, (ng * spg) / 32);
     int64_t best = 1;
-    double best_score = -1.0;
+    double best_score = -1e30;
     for (int64_t c = 1; c <= max_ns; ++c) {
       const int64_t blocks = (int64_t)s.tiles * c;
       const double rounds = (double)cdiv(blocks, slots);
-      const double eff = (double)blocks / (rounds * (double)slots);
-      // prefer full rounds; among near-equal fills prefer fewer splits
-      const double score = eff - 0.002 * (double)c;
-      if (blocks >= slots / 2 && score > best_score + 1e-9) {
+      const double fill = (double)blocks / (rounds * (double)slots);
+      const double score = fill - 0.003 * (double)c - 0.25 * (rounds - 1.0);
+      if (score > best_score + 1e-9) {
         best_score = score;
         best = c;
       }
     }
-    if (best_score < 0) best = max_ns;
     ns = best;
   }
-  ns = std::max<int64_t>(1, std::min<int64_t>(ns, nk));
-  s.steps_per_split = (int)cdiv(nk, ns);
-  s.nsplit = (int)cdiv(nk, s.steps_per_split);  // no empty partitions
+  ns = std::max<int64_t>(1, std::min<int64_t>(ns, ng));
+  s.steps_per_split = (int)cdiv(ng, ns);           // groups per partition
+  s.nsplit = (int)cdiv(ng, s.steps_per_split);     // no empty partitions
   s.ws_bytes = 0;
   if (s.nsplit > 1) {
     const size_t part = (size_t)s.nsplit * (size_t)M * (size_t)N * sizeof(float);
-    const size_t part_al = (part + 255) & ~(size_t)255;
-    s.ws_bytes = part_al + (size_t)s.tiles * sizeof(int);
+    s.ws_bytes = AWQ_COUNTER_BYTES + part;
   }
   return s;
 }
@@ -763,17 +875,21 @@ SkinnyPlan plan_skinny(int64_t M, int64_t N, int64_t K, int split_k) {
 template <int WPL, int MT, bool SEQ, bool ZP, typename T, bool FAST>
 void launch_skinny_t(const GemmArgs& a, const SkinnyPlan& s, int sbf, hipStream_t st) {
   dim3 grid(s.tiles, s.nsplit);
-  hipLaunchKernelGGL((skinny_kn_kernel<WPL, MT, SEQ, ZP, T, FAST>), grid, dim3(256), 0, st, a, sbf);
+  const int spg = a.G / 32;
+  if (spg == 4)
+    hipLaunchKernelGGL((skinny_kn_kernel<WPL, MT, 4, SEQ, ZP, T, FAST>), grid, dim3(256), 0, st, a, sbf);
+  else if (spg == 2)
+    hipLaunchKernelGGL((skinny_kn_kernel<WPL, MT, 2, SEQ, ZP, T, FAST>), grid, dim3(256), 0, st, a, sbf);
+  else
+    hipLaunchKernelGGL((skinny_kn_kernel<WPL, MT, 1, SEQ, ZP, T, FAST>), grid, dim3(256), 0, st, a, sbf);
 }
 
 template <bool SEQ, bool ZP, typename T, bool FAST>
 void launch_skinny_sel(const GemmArgs& a, const SkinnyPlan& s, int sbf, hipStream_t st) {
   if (s.mt == 2) {
-    if (s.wpl == 2) launch_skinny_t<2, 2, SEQ, ZP, T, FAST>(a, s, sbf, st);
-    else launch_skinny_t<1, 2, SEQ, ZP, T, FAST>(a, s, sbf, st);
+    launch_skinny_t<1, 2, SEQ, ZP, T, FAST>(a, s, sbf, st);
   } else {
-    if (s.wpl == 4) launch_skinny_t<4, 1, SEQ, ZP, T, FAST>(a, s, sbf, st);
-    else if (s.wpl == 2) launch_skinny_t<2, 1, SEQ, ZP, T, FAST>(a, s, sbf, st);
+    if (s.wpl == 2) launch_skinny_t<2, 1, SEQ, ZP, T, FAST>(a, s, sbf, st);
     else launch_skinny_t<1, 1, SEQ, ZP, T, FAST>(a, s, sbf, st);
   }
 }
@@ -909,7 +1025,9 @@ size_t awq_w4a16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t g
   (void)group_size;
   (void)layout;
   if (M <= 0 || N <= 0 || K <= 0 || M > 32 || (K % 32) != 0) return 0;
-  return plan_skinny(M, N, K, split_k).ws_bytes;
+  if (group_size != 32 && group_size != 64 && group_size != 128) return 0;
+  if (group_size <= 0 || (group_size % 32) != 0 || (K % group_size) != 0) return 0;
+  return plan_skinny(M, N, K, group_size, split_k).ws_bytes;
 }
 
 int awq_w4a16_gemm(const void* a, int64_t lda, const int32_t* qweight, const void* scales,
@@ -931,6 +1049,7 @@ int awq_w4a16_gemm(const void* a, int64_t lda, const int32_t* qweight, const voi
       (((uintptr_t)qweight) & 15))
     return AWQ_ERR_STRIDE;
   if (layout == AWQ_LAYOUT_NK_SEQ) return AWQ_ERR_UNSUPPORTED;
+  if (K * (N / 8) * 4 > 0x7FFFFFFFLL) return AWQ_ERR_UNSUPPORTED;  // 32-bit buffer offsets
   if (layout != AWQ_LAYOUT_AUTOAWQ && layout != AWQ_LAYOUT_KN_SEQ) return AWQ_ERR_UNSUPPORTED;
   hipStream_t st = (hipStream_t)stream;
 
@@ -950,17 +1069,18 @@ int awq_w4a16_gemm(const void* a, int64_t lda, const int32_t* qweight, const voi
   ga.bias_dtype = bias ? bias_dtype : AWQ_DTYPE_NONE;
 
   if (K == 0) return AWQ_ERR_SHAPE;
-  const bool skinny = M <= 32;
+  // the decode kernel's group-aligned loop covers group sizes 32, 64 and 128
+  const bool skinny = M <= 32 && (group_size == 32 || group_size == 64 || group_size == 128);
   SkinnyPlan sp{};
   if (skinny) {
-    sp = plan_skinny(M, N, K, split_k);
+    sp = plan_skinny(M, N, K, group_size, split_k);
     ga.nsplit = sp.nsplit;
     ga.steps_per_split = sp.steps_per_split;
     if (sp.ws_bytes) {
       if (!workspace || workspace_bytes < sp.ws_bytes) return AWQ_ERR_WORKSPACE;
-      const size_t part = (size_t)sp.nsplit * (size_t)M * (size_t)N * sizeof(float);
-      ga.partial = (float*)workspace;
-      ga.counters = (int*)((char*)workspace + ((part + 255) & ~(size_t)255));
+      if ((size_t)sp.tiles * sizeof(int) > AWQ_COUNTER_BYTES) return AWQ_ERR_UNSUPPORTED;
+      ga.counters = (int*)workspace;
+      ga.partial = (float*)((char*)workspace + AWQ_COUNTER_BYTES);
     }
   } else {
     if ((K % 64) != 0) return AWQ_ERR_SHAPE;

@@ -139,22 +139,27 @@ REPACK_CACHE = _RepackCache()
 
 # ------------------------------------------------------------------ workspace
 class _Workspace:
-    """Zero-initialised scratch per (device, stream).  The kernels leave the counter region
-    at zero, so a buffer is zeroed only when it is (re)allocated."""
+    """Zero-initialised split-K scratch, one per device.  The kernels leave its counter
+    region at zero, so a buffer is zeroed only when it is (re)allocated.  Calls are
+    serialised on the caller's stream (the reference issues every AWQ matmul from one
+    engine thread on the current stream); work on two streams at once needs
+    ``reserve(device, nbytes, key)`` with distinct keys."""
 
     def __init__(self):
         self._bufs: dict = {}
         self._lock = threading.Lock()
 
-    def get(self, device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
-        key = (device.index, stream)
+    def get(self, device: torch.device, nbytes: int, key=None) -> torch.Tensor:
+        k = (device.index, key)
         with self._lock:
-            buf = self._bufs.get(key)
+            buf = self._bufs.get(k)
             if buf is None or buf.numel() < nbytes:
-                size = max(nbytes, 1 << 20)
+                size = max(nbytes, 16 << 20)
                 buf = torch.zeros(size, dtype=torch.uint8, device=device)
-                self._bufs[key] = buf
+                self._bufs[k] = buf
             return buf
+
+    reserve = get
 
 
 WORKSPACE = _Workspace()
@@ -191,7 +196,7 @@ def gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, qzeros: t
     stream = _stream_ptr(dev)
     lc = layout_code(layout)
     ws_bytes = int(lib.awq_w4a16_gemm_workspace_bytes(M, N, K, int(group_size), int(split_k), lc))
-    ws = WORKSPACE.get(dev, stream, ws_bytes) if ws_bytes else None
+    ws = WORKSPACE.get(dev, ws_bytes) if ws_bytes else None
     rc = lib.awq_w4a16_gemm(
         _ptr(a), int(a.stride(0)), _ptr(qweight), _ptr(scales), _ptr(qzeros), _ptr(bias), _ptr(out),
         int(out.stride(0)), M, N, K, int(group_size), int(split_k), lc, dtype_code(a.dtype),
