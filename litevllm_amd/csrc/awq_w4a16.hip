@@ -367,7 +367,12 @@ skinny_kn_kernel(const GemmArgs p, int scale_bf16) {
     const uint32_t row_bytes = (uint32_t)NW * 4u;
     const uint32_t lane_off = (uint32_t)(8 * q) * row_bytes + (uint32_t)wld * 4u;
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(p.a, (uint32_t)((uint64_t)p.M * (uint64_t)p.lda * 2u));
-    const uint32_t x_lane_off = ((uint32_t)r * (uint32_t)p.lda + 8u * (uint32_t)q) * 2u;
+    // the whole row offset rides in the VGPR offset: buffer range checks cover the VGPR
+    // offset only (the SGPR offset is excluded), so rows >= M read as zero
+    uint32_t x_lane_off[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+      x_lane_off[mt] = ((uint32_t)(mt * 16 + r) * (uint32_t)p.lda + 8u * (uint32_t)q) * 2u;
     const MagicK mk = magic_consts();
 
     uint32_t raw[PF][8][WPL];
@@ -394,8 +399,8 @@ skinny_kn_kernel(const GemmArgs p, int scale_bf16) {
       for (int mt = 0; mt < MT; ++mt) {
         // rows >= M fall outside the buffer range and read as zero: no branch, so the
         // compiler's counter waits stay exact across the loop
-        const uint32_t xoff = ((uint32_t)(mt * 16) * (uint32_t)p.lda + (uint32_t)(ks * 32)) * 2u;
-        xd[mt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)x_lane_off, (int)xoff, 0));
+        const uint32_t xoff = (uint32_t)(ks * 32) * 2u;
+        xd[mt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)x_lane_off[mt], (int)xoff, 0));
       }
     };
     // group constants through buffer loads too: as intrinsic calls they are not merged
