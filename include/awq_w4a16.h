@@ -47,10 +47,15 @@ extern "C" {
  * AWQ_LAYOUT_NK_SEQ  : reference runtime layout: qweight int32 [N, K/8], nibble i of word
  *                      (n, j) = W[n, 8j + i]; qzeros int32 [N, ceil(K/G/8)] sequential along
  *                      the group axis; scales [N, K/G]  (tensor.py:842-858).
+ * AWQ_LAYOUT_DECODE_STREAM : an AUTOAWQ qweight re-ordered by awq_w4a16_pack_decode_stream so
+ *                      that the decode kernel reads it as contiguous 8 KiB runs; qzeros and
+ *                      scales stay in the AUTOAWQ layout.  Accepted by awq_w4a16_gemm for
+ *                      M <= 32, group sizes 32/64/128, f16 activations and scales.
  */
 #define AWQ_LAYOUT_AUTOAWQ 0
 #define AWQ_LAYOUT_KN_SEQ 1
 #define AWQ_LAYOUT_NK_SEQ 2
+#define AWQ_LAYOUT_DECODE_STREAM 3
 
 /* ---- element types ---- */
 #define AWQ_DTYPE_NONE 0 /* e.g. no bias */
@@ -120,6 +125,17 @@ int awq_w4a16_repack_nk_to_autoawq(const int32_t* qweight_nk, const int32_t* qze
                                    const void* scales_nk, int32_t* qweight_kn, int32_t* qzeros_kn,
                                    void* scales_kn, int64_t N, int64_t K, int32_t group_size,
                                    void* stream);
+
+/* Bytes of the decode stream copy of a [K, N/8] qweight (N rounded up to 512 columns). */
+int64_t awq_w4a16_decode_stream_bytes(int64_t K, int64_t N);
+
+/* Lossless re-ordering of an AUTOAWQ (or KN_SEQ) qweight [K, N/8] into the decode stream
+ * layout (out holds awq_w4a16_decode_stream_bytes(K, N) bytes).  No counterpart in the
+ * reference: it plays the role of the derived packs the reference caches on its weight
+ * objects (vllm/model_executor/layers/quantization/tensor.py:1251-1256), built once per
+ * weight so that decode-shaped calls stream the weight contiguously.  K % 32 == 0. */
+int awq_w4a16_pack_decode_stream(const int32_t* qweight_kn, int32_t* out, int64_t K, int64_t N,
+                                 void* stream);
 
 #ifdef __cplusplus
 }

@@ -16,6 +16,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 LAYOUT_AUTOAWQ = 0
 LAYOUT_KN_SEQ = 1
 LAYOUT_NK_SEQ = 2
+LAYOUT_DECODE_STREAM = 3
 
 DTYPE_NONE = 0
 DTYPE_F16 = 1
@@ -43,6 +44,8 @@ SIGNATURES = {
                                       _c_i32, _c_p, _c_sz, _c_p]),
     "awq_w4a16_repack_nk_to_autoawq": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64,
                                                       _c_i64, _c_i32, _c_p]),
+    "awq_w4a16_decode_stream_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "awq_w4a16_pack_decode_stream": (ctypes.c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_p]),
 }
 
 _lock = threading.Lock()

@@ -1,10 +1,12 @@
 """Build ``libawq_w4a16.so`` in-tree with hipcc for gfx950 (no JIT cache, no torch extension).
 
-Usage: ``python -m litevllm_amd.build``.  The shared library lands next to this file so it
-travels with the source tree to the GPU box.
+Usage: ``python -m litevllm_amd.build``.  Each translation unit under ``csrc/`` compiles to
+an object in ``_build/`` in parallel, then one link produces the shared library next to this
+file, so it travels with the source tree to the GPU box.
 """
 from __future__ import annotations
 
+import concurrent.futures as cf
 import os
 import shutil
 import subprocess
@@ -12,10 +14,15 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
-SRC = os.path.join(HERE, "csrc", "awq_w4a16.hip")
+CSRC = os.path.join(HERE, "csrc")
 INC = os.path.join(ROOT, "include")
+BUILD_DIR = os.path.join(ROOT, "_build")
 OUT = os.path.join(HERE, "libawq_w4a16.so")
 ARCH = "gfx950"
+SOURCES = ["awq_capi.hip", "awq_dequant.hip", "awq_decode.hip", "awq_gemm.hip"]
+
+# hipcc's host pass does not know the packed-fp32 target feature and says so: harmless
+_NOISE = "is not a recognized feature for this target"
 
 
 def hipcc() -> str:
@@ -25,29 +32,49 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm required to build the HIP library)")
 
 
-def compile_cmd(out: str = OUT) -> list[str]:
+def common_flags(extra: list[str] | None = None) -> list[str]:
     return [
-        hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+        f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
         # packed-fp32 VALU forms are kept out of the generated code on purpose
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-        f"-I{INC}", "-o", out, SRC,
+        f"-I{INC}", f"-I{CSRC}", *(extra or []),
     ]
 
 
-def build(verbose: bool = True) -> str:
-    tmp = OUT + ".tmp"
-    cmd = compile_cmd(tmp)
-    if verbose:
-        print("[build]", " ".join(cmd), flush=True)
+def compile_cmd(src: str, obj: str, extra: list[str] | None = None) -> list[str]:
+    return [hipcc(), *common_flags(extra), "-c", "-o", obj, src]
+
+
+def _run(cmd: list[str]) -> str:
     res = subprocess.run(cmd, capture_output=True, text=True)
-    noise = "is not a recognized feature for this target"
-    err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
+    err = "\n".join(l for l in res.stderr.splitlines() if _NOISE not in l)
     if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
-    if err.strip() and verbose:
-        print(err, file=sys.stderr)
-    os.replace(tmp, OUT)
-    return OUT
+        raise RuntimeError(f"hipcc failed ({res.returncode}): {' '.join(cmd)}\n{err}")
+    return err
+
+
+def build(verbose: bool = True, out: str = OUT, sources: list[str] | None = None,
+          extra: list[str] | None = None, build_dir: str = BUILD_DIR) -> str:
+    """Compile every translation unit (in parallel) and link ``out``."""
+    os.makedirs(build_dir, exist_ok=True)
+    srcs = [s if os.path.isabs(s) else os.path.join(CSRC, s) for s in (sources or SOURCES)]
+    objs = [os.path.join(build_dir, os.path.splitext(os.path.basename(s))[0] + ".o") for s in srcs]
+    jobs = min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
+    with cf.ThreadPoolExecutor(jobs) as ex:
+        futs = {ex.submit(_run, compile_cmd(s, o, extra)): s for s, o in zip(srcs, objs)}
+        for f in cf.as_completed(futs):
+            err = f.result()
+            if verbose:
+                print(f"[build] compiled {os.path.basename(futs[f])}", flush=True)
+                if err.strip():
+                    print(err, file=sys.stderr)
+    tmp = out + ".tmp"
+    link = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    _run(link)
+    os.replace(tmp, out)
+    if verbose:
+        print(f"[build] linked {out}", flush=True)
+    return out
 
 
 if __name__ == "__main__":

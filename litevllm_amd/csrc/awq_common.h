@@ -1,0 +1,216 @@
+// Shared device helpers of the MI355X (gfx950 / CDNA4) AWQ W4A16 kernels.
+//
+// Reference behaviour followed (paths relative to the jiayingsong2023/litevLLM checkout):
+//   dequant value  (q - z) * s rounded once   vllm/model_executor/layers/quantization/tensor.py:857-858,
+//                                             vllm/kernels/triton/awq_fused_gemm.py:1966, 1976
+//   fp32 accumulation, one output rounding,   awq_fused_gemm.py:1969-1990
+//   bias added in fp32 before that rounding
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "awq_w4a16.h"
+
+namespace awq {
+
+typedef _Float16 f16;
+typedef __bf16 bf16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+__host__ __device__ constexpr uint32_t cdiv_u(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
+
+// Column offset held by nibble i of a packed word.
+template <bool SEQ>
+__host__ __device__ constexpr int nib_col(int i) {
+  return SEQ ? i : (i < 4 ? 2 * i : 2 * (i - 4) + 1);  // AutoAWQ order {0,2,4,6,1,3,5,7}
+}
+// Nibble holding column offset c (inverse of nib_col).
+template <bool SEQ>
+__host__ __device__ constexpr int col_nib(int c) {
+  return SEQ ? c : ((c & 1) ? 4 + (c >> 1) : (c >> 1));
+}
+static_assert(nib_col<false>(1) == 2 && nib_col<false>(4) == 1 && nib_col<false>(7) == 7, "AWQ order");
+static_assert(col_nib<false>(nib_col<false>(3)) == 3 && col_nib<false>(nib_col<false>(6)) == 6, "inverse");
+
+__device__ __forceinline__ f16x2 as_h2(uint32_t u) { return __builtin_bit_cast(f16x2, u); }
+__device__ __forceinline__ uint32_t as_u(f16x2 h) { return __builtin_bit_cast(uint32_t, h); }
+
+__device__ __forceinline__ uint16_t f2h_bits(float x) { return __builtin_bit_cast(uint16_t, (f16)x); }
+__device__ __forceinline__ uint16_t f2bf_bits(float x) { return __builtin_bit_cast(uint16_t, (bf16)x); }
+__device__ __forceinline__ float h_bits2f(uint16_t b) { return (float)__builtin_bit_cast(f16, b); }
+__device__ __forceinline__ float bf_bits2f(uint16_t b) {
+  return __builtin_bit_cast(float, (uint32_t)b << 16);
+}
+
+template <typename T>
+__device__ __forceinline__ uint16_t to_bits(float x) {
+  if constexpr (std::is_same<T, f16>::value) return f2h_bits(x);
+  else return f2bf_bits(x);
+}
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return (uint32_t)to_bits<T>(lo) | ((uint32_t)to_bits<T>(hi) << 16);
+}
+template <typename T>
+__device__ __forceinline__ float from_bits(uint16_t b) {
+  if constexpr (std::is_same<T, f16>::value) return h_bits2f(b);
+  else return bf_bits2f(b);
+}
+
+// Magic-exponent int4 -> fp16 conversion.  For a 32-bit word m whose two 16-bit halves
+// each hold four nibbles, nibble position P (0..3) of both halves becomes an f16x2:
+//   P even: (bits & 0x000F000F) | 0x6400  ->  1024 + q  (nibble in mantissa bits 0-3)
+//   P odd : (bits & 0x00F000F0) | 0x5400  ->    64 + q  (nibble in mantissa bits 4-7,
+//                                                          exponent of 64 has ulp 1/16)
+// P >= 2 first shifts the word right by 8.  Both forms are exact.
+// The masks and magic exponents live in VGPRs (MagicK) so that each nibble pair costs a
+// single v_and_or_b32: gfx9 VOP3 encodings cannot carry 32-bit literals, and with literal
+// operands the compiler splits the operation into v_and_b32 + v_or_b32.
+struct MagicK {
+  uint32_t lo_mask, hi_mask, lo_magic, hi_magic;
+};
+__device__ __forceinline__ MagicK magic_consts() {
+  MagicK k{0x000F000Fu, 0x00F000F0u, 0x64006400u, 0x54005400u};
+  asm volatile("" : "+v"(k.lo_mask), "+v"(k.hi_mask), "+v"(k.lo_magic), "+v"(k.hi_magic));
+  return k;
+}
+template <int P>
+__device__ __forceinline__ uint32_t magic_bits(uint32_t m, const MagicK& k) {
+  const uint32_t v = (P >= 2) ? (m >> 8) : m;
+  return (P & 1) ? ((v & k.hi_mask) | k.hi_magic) : ((v & k.lo_mask) | k.lo_magic);
+}
+// Zero operand matching magic_bits<P>: the same bias plus z, broadcast to both halves.
+__device__ __forceinline__ uint32_t zero_magic(int p_odd, uint32_t z) {
+  const uint32_t h = p_odd ? (0x5400u | (z << 4)) : (0x6400u | z);
+  return h * 0x00010001u;
+}
+
+// Per-column dequant constants for one group.
+//  FAST (f16 activations and f16 scales): zm = biased zero, sc = scale, both broadcast f16x2;
+//  W = (magic - zm) * sc -- the subtraction is exact, the multiply rounds once.
+//  otherwise: zm as above, scf = fp32 scale; W = T(float(magic - zm) * scf), exact product,
+//  one rounding to T.
+struct ColConst {
+  uint32_t zm;
+  uint32_t sc;   // f16x2 bits (FAST)
+  float scf;     // fp32 scale (generic)
+};
+
+// Two dequantized values (two K-adjacent rows of one column) as 32 bits of T.
+template <bool FAST, typename T>
+__device__ __forceinline__ uint32_t deq2(uint32_t magic, const ColConst& cc) {
+  const f16x2 d = as_h2(magic) - as_h2(cc.zm);  // exact small integers
+  if constexpr (FAST) {
+    return as_u(d * as_h2(cc.sc));
+  } else {
+    return pack2<T>((float)d.x * cc.scf, (float)d.y * cc.scf);
+  }
+}
+
+template <typename T> struct MfmaOp;
+template <> struct MfmaOp<f16> {
+  static __device__ __forceinline__ f32x4 run(const u32x4& a, const u32x4& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+template <> struct MfmaOp<bf16> {
+  static __device__ __forceinline__ f32x4 run(const u32x4& a, const u32x4& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+
+__device__ __forceinline__ float load_bias(const void* bias, int dtype, int col) {
+  if (dtype == AWQ_DTYPE_F16) return h_bits2f(((const uint16_t*)bias)[col]);
+  if (dtype == AWQ_DTYPE_BF16) return bf_bits2f(((const uint16_t*)bias)[col]);
+  if (dtype == AWQ_DTYPE_F32) return ((const float*)bias)[col];
+  return 0.0f;
+}
+
+// Shared argument block of the GEMM kernels.
+struct GemmArgs {
+  const uint16_t* a;
+  const uint32_t* qw;
+  const uint16_t* sc;
+  const uint32_t* qz;
+  const void* bias;
+  uint16_t* c;
+  float* partial;   // [nsplit, M, N] fp32 (decode kernel with nsplit > 1)
+  int* counters;    // [column tiles]   (zero on entry and on exit)
+  int64_t lda, ldc;
+  int M, N, K, G;
+  int nsplit, groups_per_split;
+  int bias_dtype;
+};
+
+// Raw per-group constants of one packed word: 8 scales (16 bytes) and the zero word.
+struct WordSZ {
+  u32x4 s4;
+  uint32_t zw;
+};
+
+// Per-column dequant constants of the 8 nibbles of a word.
+template <bool SEQ, bool FAST>
+__device__ __forceinline__ void prep_consts(const WordSZ& sz, bool scale_bf16, ColConst (&cc)[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int c = nib_col<SEQ>(i);
+    const uint32_t sbits = (sz.s4[c >> 1] >> (16 * (c & 1))) & 0xFFFFu;
+    cc[i].zm = zero_magic(i & 1, (sz.zw >> (4 * i)) & 0xF);
+    if constexpr (FAST) {
+      cc[i].sc = sbits * 0x00010001u;
+      cc[i].scf = 0.0f;
+    } else {
+      cc[i].sc = 0;
+      cc[i].scf = scale_bf16 ? bf_bits2f((uint16_t)sbits) : h_bits2f((uint16_t)sbits);
+    }
+  }
+}
+
+// Row pairing with one byte permute: lo16(w0) | lo16(w1) << 16 and hi16(w0) | hi16(w1) << 16.
+// (v_perm_b32 selects bytes 0-3 from its second operand and 4-7 from its first.)
+__device__ __forceinline__ uint32_t pair_lo(uint32_t w0, uint32_t w1) {
+  return __builtin_amdgcn_perm(w1, w0, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t pair_hi(uint32_t w0, uint32_t w1) {
+  return __builtin_amdgcn_perm(w1, w0, 0x07060302u);
+}
+
+// Eight rows (k .. k+7) of one packed word, pre-paired into lo/hi words, -> MFMA operand
+// (8 K-consecutive values of the column held by nibble I).
+template <int I, bool FAST, typename T>
+__device__ __forceinline__ u32x4 rows_operand(const uint32_t (&mlo)[4], const uint32_t (&mhi)[4],
+                                              const ColConst& cc, const MagicK& k) {
+  u32x4 r;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) r[u] = deq2<FAST, T>(magic_bits<I & 3>(I < 4 ? mlo[u] : mhi[u], k), cc);
+  return r;
+}
+
+// Buffer resource over a whole tensor (raw addressing, bounds = nbytes).  Range checks
+// cover the VGPR offset only (the SGPR offset is excluded), so anything that must read as
+// zero past the end has to carry its position in the VGPR offset.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t nbytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)nbytes, 0x00020000);
+}
+
+// Buffer cache-policy bits: sc1 = device scope.  Stores with it are visible to every XCD
+// once complete; loads with it do not hit lines another XCD's L2 may hold stale.
+constexpr int kDeviceCoherent = 0x10;
+
+}  // namespace awq
+
+// Host-side launchers (one per translation unit).
+namespace awq_host {
+int num_cus();
+}

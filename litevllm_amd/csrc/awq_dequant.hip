@@ -1,0 +1,259 @@
+// Standalone int4 -> fp16/bf16/fp32 dequant (both packed geometries, sequential or AutoAWQ
+// nibble order) and the lossless reference-layout -> AutoAWQ-layout repack, on gfx950.
+//
+// Dequant is the role of awq_dequantize_kernel (vllm/model_executor/layers/quantization/
+// awq_triton.py:64-147) and dequantize_awq_pytorch / dequantize_symmetric_packed_int4_pytorch
+// (tensor.py:835-901): out = RNE((q - z) * s), the product exact in fp32, one rounding.
+#include "awq_common.h"
+#include "awq_launch.h"
+
+namespace awq {
+
+// Standalone dequant.
+// KN layouts: qweight [K, N/8]; thread = one word (k, j) -> out[k, 8j .. 8j+7].
+template <bool SEQ, bool ZP, typename ST, int OUT>
+__global__ void __launch_bounds__(256) dequant_kn_kernel(const uint32_t* __restrict__ qw,
+                                                         const uint16_t* __restrict__ sc,
+                                                         const uint32_t* __restrict__ qz,
+                                                         void* __restrict__ out, int64_t K,
+                                                         int64_t N, int G) {
+  const int64_t NW = N >> 3;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= K * NW) return;
+  const int64_t k = idx / NW, j = idx - k * NW;
+  const int64_t g = k / G;
+  const uint32_t w = qw[idx];
+  const uint32_t zw = ZP ? qz[g * NW + j] : 0x88888888u;
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int q = (w >> (4 * i)) & 0xF, z = (zw >> (4 * i)) & 0xF;
+    const float s = from_bits<ST>(sc[g * N + 8 * j + nib_col<SEQ>(i)]);
+    v[nib_col<SEQ>(i)] = (float)(q - z) * s;  // exact in fp32
+  }
+  const int64_t o = k * N + 8 * j;
+  if constexpr (OUT == AWQ_DTYPE_F32) {
+    f32x4* d = (f32x4*)((float*)out + o);
+    d[0] = f32x4{v[0], v[1], v[2], v[3]};
+    d[1] = f32x4{v[4], v[5], v[6], v[7]};
+  } else {
+    using T = typename std::conditional<OUT == AWQ_DTYPE_F16, f16, bf16>::type;
+    u32x4 r;
+    r[0] = pack2<T>(v[0], v[1]);
+    r[1] = pack2<T>(v[2], v[3]);
+    r[2] = pack2<T>(v[4], v[5]);
+    r[3] = pack2<T>(v[6], v[7]);
+    *(u32x4*)((uint16_t*)out + o) = r;
+  }
+}
+
+// NK layout: qweight [N, K/8]; thread = one word (n, kw) -> out[n, 8kw .. 8kw+7].
+template <bool ZP, typename ST, int OUT>
+__global__ void __launch_bounds__(256) dequant_nk_kernel(const uint32_t* __restrict__ qw,
+                                                         const uint16_t* __restrict__ sc,
+                                                         const uint32_t* __restrict__ qz,
+                                                         void* __restrict__ out, int64_t N,
+                                                         int64_t K, int G) {
+  const int64_t KW = K >> 3, NG = K / G, ZW = (NG + 7) >> 3;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= N * KW) return;
+  const int64_t n = idx / KW, kw = idx - n * KW;
+  const int64_t g = (kw * 8) / G;
+  const uint32_t w = qw[idx];
+  const int z = ZP ? (int)((qz[n * ZW + (g >> 3)] >> (4 * (g & 7))) & 0xF) : 8;
+  const float s = from_bits<ST>(sc[n * NG + g]);
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = (float)((int)((w >> (4 * i)) & 0xF) - z) * s;
+  const int64_t o = n * K + 8 * kw;
+  if constexpr (OUT == AWQ_DTYPE_F32) {
+    f32x4* d = (f32x4*)((float*)out + o);
+    d[0] = f32x4{v[0], v[1], v[2], v[3]};
+    d[1] = f32x4{v[4], v[5], v[6], v[7]};
+  } else {
+    using T = typename std::conditional<OUT == AWQ_DTYPE_F16, f16, bf16>::type;
+    u32x4 r;
+    r[0] = pack2<T>(v[0], v[1]);
+    r[1] = pack2<T>(v[2], v[3]);
+    r[2] = pack2<T>(v[4], v[5]);
+    r[3] = pack2<T>(v[6], v[7]);
+    *(u32x4*)((uint16_t*)out + o) = r;
+  }
+}
+
+// Repack reference layout -> AutoAWQ layout.
+// Weights: thread = 8x8 nibble block: input words (n0+e, kw) e<8 -> output words (8kw+t, n0/8) t<8.
+__global__ void __launch_bounds__(256) repack_w_kernel(const uint32_t* __restrict__ in,
+                                                       uint32_t* __restrict__ out, int64_t N,
+                                                       int64_t K) {
+  const int64_t KW = K >> 3, NWd = N >> 3;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= KW * NWd) return;
+  const int64_t nb = idx / KW, kw = idx - nb * KW;  // consecutive threads: consecutive kw
+  uint32_t w[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) w[e] = in[(nb * 8 + e) * KW + kw];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {  // k = 8kw + t
+    uint32_t o = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {  // output nibble i holds column 8nb + order[i]
+      const int e = nib_col<false>(i);
+      o |= ((w[e] >> (4 * t)) & 0xFu) << (4 * i);
+    }
+    out[(kw * 8 + t) * NWd + nb] = o;
+  }
+}
+// Zeros: [N, ZW] sequential along groups -> [NG, N/8] interleaved; thread = output word.
+__global__ void __launch_bounds__(256) repack_z_kernel(const uint32_t* __restrict__ in,
+                                                       uint32_t* __restrict__ out, int64_t N,
+                                                       int64_t NG) {
+  const int64_t ZW = (NG + 7) >> 3, NWd = N >> 3;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= NG * NWd) return;
+  const int64_t g = idx / NWd, j = idx - g * NWd;
+  uint32_t o = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t n = 8 * j + nib_col<false>(i);
+    o |= ((in[n * ZW + (g >> 3)] >> (4 * (g & 7))) & 0xFu) << (4 * i);
+  }
+  out[idx] = o;
+}
+// Scales: 2-byte transpose [N, NG] -> [NG, N].
+__global__ void __launch_bounds__(256) repack_s_kernel(const uint16_t* __restrict__ in,
+                                                       uint16_t* __restrict__ out, int64_t N,
+                                                       int64_t NG) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= N * NG) return;
+  const int64_t g = idx / N, n = idx - g * N;
+  out[idx] = in[n * NG + g];
+}
+
+// Decode stream pack (layout documented at decode_stream_bytes): thread = one 16-byte slot.
+__global__ void __launch_bounds__(256) pack_stream_kernel(const uint32_t* __restrict__ in,
+                                                          u32x4* __restrict__ out, int64_t K,
+                                                          int64_t NW, int64_t tiles) {
+  const int64_t KS = K / 32;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= tiles * KS * 512) return;
+  const int l = (int)(idx & 63), j = (int)((idx >> 6) & 7);
+  const int64_t ts = idx >> 9;  // t * KS + s
+  const int64_t t = ts / KS, s = ts - t * KS;
+  const int q = l >> 4, r = l & 15;
+  const int64_t row = s * 32 + 8 * q + j;
+  const int64_t w0 = t * 64 + 4 * r;
+  u32x4 v;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) v[w] = (w0 + w < NW) ? in[row * NW + w0 + w] : 0u;
+  out[idx] = v;
+}
+
+}  // namespace awq
+
+namespace awq_host {
+using namespace awq;
+
+static int launch_status() {
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? AWQ_OK : AWQ_ERR_LAUNCH;
+}
+static bool dtype_16(int d) { return d == AWQ_DTYPE_F16 || d == AWQ_DTYPE_BF16; }
+
+template <typename F>
+int with_out_dtype(int out_dtype, F&& f) {
+  switch (out_dtype) {
+    case AWQ_DTYPE_F16: f(std::integral_constant<int, AWQ_DTYPE_F16>{}); return AWQ_OK;
+    case AWQ_DTYPE_BF16: f(std::integral_constant<int, AWQ_DTYPE_BF16>{}); return AWQ_OK;
+    case AWQ_DTYPE_F32: f(std::integral_constant<int, AWQ_DTYPE_F32>{}); return AWQ_OK;
+    default: return AWQ_ERR_UNSUPPORTED;
+  }
+}
+
+int launch_dequant(const int32_t* qweight, const void* scales, const int32_t* qzeros, void* out,
+                   int64_t rows, int64_t cols, int32_t group_size, int32_t layout,
+                   int32_t scale_dtype, int32_t out_dtype, hipStream_t st) {
+  if (!qweight || !scales || !out) return AWQ_ERR_NULL;
+  if (rows < 0 || cols < 0 || group_size <= 0 || (group_size % 8) != 0) return AWQ_ERR_SHAPE;
+  if (!dtype_16(scale_dtype)) return AWQ_ERR_UNSUPPORTED;
+  const bool zp = qzeros != nullptr;
+  const bool sbf = scale_dtype == AWQ_DTYPE_BF16;
+  if (layout == AWQ_LAYOUT_AUTOAWQ || layout == AWQ_LAYOUT_KN_SEQ) {
+    const int64_t K = rows, N = cols;
+    if ((N % 8) != 0 || (K % group_size) != 0) return AWQ_ERR_SHAPE;
+    const int64_t n = K * (N / 8);
+    if (n == 0) return AWQ_OK;
+    const dim3 grid((unsigned)cdiv(n, 256));
+    const uint32_t* qw = (const uint32_t*)qweight;
+    const uint32_t* qz = (const uint32_t*)qzeros;
+    const uint16_t* sc = (const uint16_t*)scales;
+    int rc = with_out_dtype(out_dtype, [&](auto od) {
+      constexpr int OD = decltype(od)::value;
+#define AWQ_DQ_KN(SEQ, ZP, ST) hipLaunchKernelGGL((dequant_kn_kernel<SEQ, ZP, ST, OD>), grid, dim3(256), 0, st, qw, sc, qz, out, K, N, (int)group_size)
+      const bool seq = layout == AWQ_LAYOUT_KN_SEQ;
+      if (seq) {
+        if (zp) { if (sbf) AWQ_DQ_KN(true, true, bf16); else AWQ_DQ_KN(true, true, f16); }
+        else { if (sbf) AWQ_DQ_KN(true, false, bf16); else AWQ_DQ_KN(true, false, f16); }
+      } else {
+        if (zp) { if (sbf) AWQ_DQ_KN(false, true, bf16); else AWQ_DQ_KN(false, true, f16); }
+        else { if (sbf) AWQ_DQ_KN(false, false, bf16); else AWQ_DQ_KN(false, false, f16); }
+      }
+#undef AWQ_DQ_KN
+    });
+    if (rc != AWQ_OK) return rc;
+    return launch_status();
+  }
+  if (layout == AWQ_LAYOUT_NK_SEQ) {
+    const int64_t N = rows, K = cols;
+    if ((K % 8) != 0 || (K % group_size) != 0) return AWQ_ERR_SHAPE;
+    const int64_t n = N * (K / 8);
+    if (n == 0) return AWQ_OK;
+    const dim3 grid((unsigned)cdiv(n, 256));
+    const uint32_t* qw = (const uint32_t*)qweight;
+    const uint32_t* qz = (const uint32_t*)qzeros;
+    const uint16_t* sc = (const uint16_t*)scales;
+    int rc = with_out_dtype(out_dtype, [&](auto od) {
+      constexpr int OD = decltype(od)::value;
+#define AWQ_DQ_NK(ZP, ST) hipLaunchKernelGGL((dequant_nk_kernel<ZP, ST, OD>), grid, dim3(256), 0, st, qw, sc, qz, out, N, K, (int)group_size)
+      if (zp) { if (sbf) AWQ_DQ_NK(true, bf16); else AWQ_DQ_NK(true, f16); }
+      else { if (sbf) AWQ_DQ_NK(false, bf16); else AWQ_DQ_NK(false, f16); }
+#undef AWQ_DQ_NK
+    });
+    if (rc != AWQ_OK) return rc;
+    return launch_status();
+  }
+  return AWQ_ERR_UNSUPPORTED;
+}
+
+int launch_repack_nk_to_autoawq(const int32_t* qweight_nk, const int32_t* qzeros_nk,
+                                const void* scales_nk, int32_t* qweight_kn, int32_t* qzeros_kn,
+                                void* scales_kn, int64_t N, int64_t K, int32_t group_size,
+                                hipStream_t st) {
+  if (!qweight_nk || !qweight_kn || !scales_nk || !scales_kn) return AWQ_ERR_NULL;
+  if (qzeros_nk && !qzeros_kn) return AWQ_ERR_NULL;
+  if (N < 0 || K < 0 || group_size <= 0 || (N % 8) || (K % 8) || (K % group_size)) return AWQ_ERR_SHAPE;
+  const int64_t NG = K / group_size;
+  const int64_t nw = (K / 8) * (N / 8);
+  if (nw > 0)
+    hipLaunchKernelGGL(repack_w_kernel, dim3((unsigned)cdiv(nw, 256)), dim3(256), 0, st,
+                       (const uint32_t*)qweight_nk, (uint32_t*)qweight_kn, N, K);
+  if (qzeros_nk && NG * (N / 8) > 0)
+    hipLaunchKernelGGL(repack_z_kernel, dim3((unsigned)cdiv(NG * (N / 8), 256)), dim3(256), 0, st,
+                       (const uint32_t*)qzeros_nk, (uint32_t*)qzeros_kn, N, NG);
+  if (N * NG > 0)
+    hipLaunchKernelGGL(repack_s_kernel, dim3((unsigned)cdiv(N * NG, 256)), dim3(256), 0, st,
+                       (const uint16_t*)scales_nk, (uint16_t*)scales_kn, N, NG);
+  return launch_status();
+}
+
+int launch_pack_decode_stream(const int32_t* qweight_kn, int32_t* out, int64_t K, int64_t N,
+                              hipStream_t st) {
+  const int64_t NW = N / 8, tiles = cdiv(NW, 64);
+  const int64_t n = tiles * (K / 32) * 512;
+  if (n > 0)
+    hipLaunchKernelGGL(pack_stream_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st,
+                       (const uint32_t*)qweight_kn, (u32x4*)out, K, NW, tiles);
+  return launch_status();
+}
+
+}  // namespace awq_host

@@ -1,0 +1,56 @@
+// Host-side planning and launch interfaces shared by the translation units of
+// libawq_w4a16.so (internal; the public interface is include/awq_w4a16.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "awq_common.h"
+
+namespace awq_host {
+
+// Workspace layout of the decode kernel's split-K: [0, kCounterBytes) per-tile arrival
+// counters (zero between calls), then fp32 partials [nsplit, M, N].
+constexpr size_t kCounterBytes = 65536;
+
+struct DecodePlan {
+  int wpl, mt, nwv, depth;
+  int tiles, nsplit, groups_per_split;
+  size_t ws_bytes;
+};
+
+// Which instantiations of the decode kernel serve a call:
+//   kDecodeStream : weights in the decode stream layout (AutoAWQ nibble order, f16 act/scales)
+//   kDecodeWide   : AutoAWQ [K, N/8], f16 activations and scales (every tile width)
+//   kDecodeNarrow : the other dtype / layout combinations (one word per lane)
+enum DecodeMode { kDecodeStream = 0, kDecodeWide = 1, kDecodeNarrow = 2 };
+inline DecodeMode decode_mode(int layout, int act, int sdt) {
+  if (layout == AWQ_LAYOUT_DECODE_STREAM) return kDecodeStream;
+  if (layout == AWQ_LAYOUT_AUTOAWQ && act == AWQ_DTYPE_F16 && sdt == AWQ_DTYPE_F16) return kDecodeWide;
+  return kDecodeNarrow;
+}
+DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t G, int split_k, DecodeMode mode);
+bool launch_decode(const awq::GemmArgs& a, const DecodePlan& s, DecodeMode mode, bool seq, bool zp,
+                   int act, int sdt, hipStream_t st);
+
+// Decode stream layout: for tile t (64 packed words = 512 columns), k-step s (32 rows),
+// chunk j (0..7) and lane l = 16 q + r, 16 bytes = words 64 t + 4 r .. + 3 of row 32 s + 8 q + j
+// (zero past the last word), stored at byte ((t * K/32 + s) * 8 + j) * 1024 + 16 l.
+inline int64_t decode_stream_bytes(int64_t K, int64_t N) { return awq::cdiv(N / 8, 64) * 64 * K * 4; }
+int launch_pack_decode_stream(const int32_t* qweight_kn, int32_t* out, int64_t K, int64_t N,
+                              hipStream_t st);
+
+// Prefill GEMM (M > 32 or group sizes the decode kernel does not cover).
+bool launch_prefill(const awq::GemmArgs& a, bool seq, bool zp, int act, int sdt, hipStream_t st);
+
+// Standalone dequant and repack.
+int launch_dequant(const int32_t* qweight, const void* scales, const int32_t* qzeros, void* out,
+                   int64_t rows, int64_t cols, int32_t group_size, int32_t layout,
+                   int32_t scale_dtype, int32_t out_dtype, hipStream_t st);
+int launch_repack_nk_to_autoawq(const int32_t* qweight_nk, const int32_t* qzeros_nk,
+                                const void* scales_nk, int32_t* qweight_kn, int32_t* qzeros_kn,
+                                void* scales_kn, int64_t N, int64_t K, int32_t group_size,
+                                hipStream_t st);
+
+}  // namespace awq_host

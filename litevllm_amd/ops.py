@@ -7,6 +7,12 @@ Layouts (``layout=`` keyword everywhere):
   * ``"autoawq"``  AutoAWQ layout: qweight int32 [K, N/8] (order 0,2,4,6,1,3,5,7),
                    scales [K/G, N], qzeros int32 [K/G, N/8]
   * ``"kn_seq"``   [K, N/8] with sequential nibbles (the reference dequant's row-grouped geometry)
+
+Decode-shaped calls (M <= 32, fp16 activations and scales, group 32/64/128) read a one-time,
+lossless re-ordering of the AutoAWQ qweight (the library's decode stream layout) that the
+decode kernel streams as contiguous 8 KiB runs.  It is built on first use and cached per
+weight tensor, the way the reference caches derived packs on its weight objects
+(``tensor.py:1251-1256``); ``prepare_decode_stream`` builds it ahead of time.
 """
 from __future__ import annotations
 
@@ -102,31 +108,55 @@ def repack_ref_to_autoawq(qweight: torch.Tensor, scales: torch.Tensor, qzeros: t
     return qw, sc, qz
 
 
-class _RepackCache:
-    """Caches the AutoAWQ-layout copy of reference-layout weights, keyed by the packed
-    tensor's storage pointer, shape and version counter (the role the reference's
-    derived-pack cache plays at tensor.py:1251-1256)."""
+def pack_decode_stream(qweight: torch.Tensor) -> torch.Tensor:
+    """AutoAWQ (or kn_seq) qweight [K, N/8] -> the decode stream layout (int32, flat)."""
+    lib = L.load()
+    _require_device(qweight)
+    if qweight.dtype != torch.int32 or qweight.dim() != 2:
+        raise ValueError("qweight must be a 2-D int32 tensor [K, N/8]")
+    k, n = int(qweight.shape[0]), int(qweight.shape[1]) * 8
+    nbytes = int(lib.awq_w4a16_decode_stream_bytes(k, n))
+    if nbytes <= 0:
+        raise ValueError(f"no decode stream layout for K={k}, N={n} (need K % 32 == 0)")
+    qweight = qweight.contiguous()
+    out = torch.empty(nbytes // 4, dtype=torch.int32, device=qweight.device)
+    rc = lib.awq_w4a16_pack_decode_stream(_ptr(qweight), _ptr(out), k, n, _stream_ptr(qweight.device))
+    L.check("awq_w4a16_pack_decode_stream", rc)
+    return out
 
-    def __init__(self, capacity: int = 512):
+
+class _DerivedCache:
+    """Caches tensors derived from a packed weight, keyed by the source tensors' storage
+    pointers, shapes and version counters and checked against a weak reference to the
+    source (the role the reference's derived-pack cache plays at tensor.py:1251-1256)."""
+
+    def __init__(self, build, capacity: int = 1024):
+        self.build = build
         self.capacity = capacity
         self._d: dict = {}
         self._lock = threading.Lock()
 
-    def get(self, qweight, scales, qzeros, group_size):
-        key = (qweight.data_ptr(), tuple(qweight.shape), qweight._version, scales.data_ptr(),
-               scales._version, None if qzeros is None else (qzeros.data_ptr(), qzeros._version),
-               int(group_size), qweight.device.index)
+    @staticmethod
+    def _key(*tensors):
+        return tuple(None if t is None else (t.data_ptr(), tuple(t.shape), t._version, t.device.index)
+                     for t in tensors)
+
+    def get(self, src: torch.Tensor, *others, args=()):
+        key = (self._key(src, *others), args)
         with self._lock:
             hit = self._d.get(key)
             if hit is not None:
                 ref, val = hit
-                if ref() is qweight:
+                if ref() is src:
                     return val
-        val = repack_ref_to_autoawq(qweight, scales, qzeros, group_size)
+        val = self.build(src, *others, *args)
         with self._lock:
-            if len(self._d) >= self.capacity:
+            # drop entries whose source tensor is gone, then the oldest beyond capacity
+            for k in [k for k, (r, _) in self._d.items() if r() is None]:
+                del self._d[k]
+            while len(self._d) >= self.capacity:
                 self._d.pop(next(iter(self._d)))
-            self._d[key] = (weakref.ref(qweight), val)
+            self._d[key] = (weakref.ref(src), val)
         return val
 
     def clear(self):
@@ -134,7 +164,17 @@ class _RepackCache:
             self._d.clear()
 
 
-REPACK_CACHE = _RepackCache()
+def _repack_builder(qweight, scales, qzeros, group_size):
+    return repack_ref_to_autoawq(qweight, scales, qzeros, group_size)
+
+
+REPACK_CACHE = _DerivedCache(_repack_builder)
+STREAM_CACHE = _DerivedCache(pack_decode_stream)
+
+
+def prepare_decode_stream(qweight: torch.Tensor) -> torch.Tensor:
+    """Build (and cache) the decode stream copy of an AutoAWQ qweight ahead of the first call."""
+    return STREAM_CACHE.get(qweight)
 
 
 # ------------------------------------------------------------------ workspace
@@ -166,13 +206,30 @@ WORKSPACE = _Workspace()
 
 
 # ------------------------------------------------------------------ GEMM
+DECODE_MAX_M = 32
+DECODE_GROUPS = (32, 64, 128)
+
+
+def _use_decode_stream(M, K, group_size, a, scales, layout, decode_stream):
+    if decode_stream is False or layout != "autoawq":
+        return False
+    eligible = (M <= DECODE_MAX_M and int(group_size) in DECODE_GROUPS and K % 32 == 0
+                and a.dtype == torch.float16 and scales.dtype == torch.float16)
+    if decode_stream is True and not eligible:
+        raise ValueError("the decode stream layout needs M <= 32, group 32/64/128 and fp16 "
+                         "activations and scales")
+    return eligible
+
+
 def gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, qzeros: torch.Tensor | None,
          group_size: int, bias: torch.Tensor | None = None, split_k: int = 0,
-         layout: str = "ref", out: torch.Tensor | None = None) -> torch.Tensor:
+         layout: str = "ref", out: torch.Tensor | None = None,
+         decode_stream: bool | None = None) -> torch.Tensor:
     """``out[M, N] = a[M, K] @ dequant(W)^T (+ bias)`` on the HIP kernels.
 
     ``split_k = 0`` lets the library choose its K partition; any value >= 1 fixes it
-    (results are bitwise reproducible for a fixed value).
+    (results are bitwise reproducible for a fixed value).  ``decode_stream`` (default: when
+    eligible) routes decode-shaped calls through the cached decode stream copy of the weight.
     """
     lib = L.load()
     if a.dim() != 2:
@@ -183,7 +240,7 @@ def gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, qzeros: t
     if int(a.shape[1]) != K:
         raise ValueError(f"K mismatch: a has {a.shape[1]}, weight has {K}")
     if layout == "ref":
-        qweight, scales, qzeros = REPACK_CACHE.get(qweight, scales, qzeros, group_size)
+        qweight, scales, qzeros = REPACK_CACHE.get(qweight, scales, qzeros, args=(int(group_size),))
         layout = "autoawq"
     a = a.contiguous()
     qweight, scales = qweight.contiguous(), scales.contiguous()
@@ -195,6 +252,9 @@ def gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, qzeros: t
     dev = a.device
     stream = _stream_ptr(dev)
     lc = layout_code(layout)
+    if _use_decode_stream(M, K, group_size, a, scales, layout, decode_stream):
+        qweight = STREAM_CACHE.get(qweight)
+        lc = L.LAYOUT_DECODE_STREAM
     ws_bytes = int(lib.awq_w4a16_gemm_workspace_bytes(M, N, K, int(group_size), int(split_k), lc))
     ws = WORKSPACE.get(dev, ws_bytes) if ws_bytes else None
     rc = lib.awq_w4a16_gemm(

@@ -117,12 +117,14 @@ SHAPES = [
 
 
 @pytest.mark.parametrize("M,K,N,G", SHAPES)
-def test_gemm_autoawq_vs_oracle(M, K, N, G):
+@pytest.mark.parametrize("stream", [None, False])
+def test_gemm_autoawq_vs_oracle(M, K, N, G, stream):
     ops = _lib()
-    _note(f"gemm autoawq M={M} K={K} N={N} G={G}")
+    _note(f"gemm autoawq M={M} K={K} N={N} G={G} stream={stream}")
     p = make_awq_problem(M=M, K=K, N=N, group_size=G, seed=M * 7 + N)
     t = _to_dev(p)
-    y = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, layout="autoawq").cpu().numpy()
+    y = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, layout="autoawq",
+                 decode_stream=stream).cpu().numpy()
     w = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"], G)       # [K, N]
     _check_vs_exact(y, O.linear_exact(p["x"], w.T), f"M={M} K={K} N={N}")
     qr, zr, sr = O.repack_awq_to_ref(p["qweight"], p["qzeros"], p["scales"]) if (K // G) % 8 == 0 else (None,) * 3
@@ -200,22 +202,24 @@ def test_split_k_config2_bit_stable(M):
     w = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"], G)
     ye = O.linear_exact(p["x"], w.T)
     for sk in (1, 4, 8):
-        _note(f"split-K M={M} split={sk}")
-        y1 = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, split_k=sk, layout="autoawq")
-        y2 = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, split_k=sk, layout="autoawq")
+        _note(f"split-K M={M} split={sk} (AutoAWQ layout read directly)")
+        y1 = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, split_k=sk, layout="autoawq", decode_stream=False)
+        y2 = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, split_k=sk, layout="autoawq", decode_stream=False)
         assert torch.equal(y1.view(torch.int16), y2.view(torch.int16)), f"split {sk} not bit-stable"
         _check_vs_exact(y1.cpu().numpy(), ye, f"split {sk}")
 
 
 # ------------------------------------------------------------------ benchmark configs
 @pytest.mark.parametrize("M,N", [(m, n) for m in (1, 4, 16) for n in (4096, 6144, 24576)])
-def test_config1_decode_sweep(M, N):
+@pytest.mark.parametrize("stream", [None, False])
+def test_config1_decode_sweep(M, N, stream):
     ops = _lib()
-    _note(f"config1 M={M} N={N}")
+    _note(f"config1 M={M} N={N} stream={stream}")
     K, G = 4096, 128
     p = make_awq_problem(M=M, K=K, N=N, group_size=G, seed=1)
     t = _to_dev(p)
-    y = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, layout="autoawq").cpu().numpy()
+    y = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, layout="autoawq",
+                 decode_stream=stream).cpu().numpy()
     w = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"], G)
     _check_vs_exact(y, O.linear_exact(p["x"], w.T), f"config1 M={M} N={N}")
     qr, zr, sr = O.repack_awq_to_ref(p["qweight"], p["qzeros"], p["scales"])
@@ -244,3 +248,58 @@ def test_config3_prefill(M, N):
     rows = np.random.default_rng(0).choice(M, size=128, replace=False)
     ye = O.linear_exact(p["x"][rows], w.T)
     _check_vs_exact(y.cpu().numpy()[rows], ye, f"config3 M={M} N={N}")
+
+
+# ------------------------------------------------------------------ decode stream layout
+def _stream_layout_numpy(qw_kn):
+    """The decode stream layout restated with numpy gathers: chunk (t, s, j), lane l = 16q + r
+    holds words 64t + 4r .. +3 of row 32s + 8q + j (zero past the last word)."""
+    K, NW = qw_kn.shape
+    tiles = -(-NW // 64)
+    pad = np.zeros((K, tiles * 64), dtype=np.int32)
+    pad[:, :NW] = qw_kn
+    v = pad.reshape(K // 32, 4, 8, tiles, 16, 4)          # [s, q, j, t, r, w]
+    return np.ascontiguousarray(v.transpose(3, 0, 2, 1, 4, 5)).reshape(-1)
+
+
+@pytest.mark.parametrize("K,N", [(256, 4096), (128, 1000), (64, 520)])
+def test_pack_decode_stream_layout(K, N):
+    ops = _lib()
+    rng = np.random.default_rng(K + N)
+    qw = rng.integers(-2**31, 2**31 - 1, size=(K, N // 8), dtype=np.int64).astype(np.int32)
+    got = ops.pack_decode_stream(torch.from_numpy(qw).to(DEV)).cpu().numpy()
+    assert np.array_equal(got, _stream_layout_numpy(qw))
+
+
+@pytest.mark.parametrize("M,K,N,G", [(1, 2048, 5632, 128), (4, 4096, 6144, 128), (16, 1024, 1000, 64),
+                                     (3, 512, 520, 32), (32, 2048, 1536, 128), (24, 1024, 4096, 128)])
+@pytest.mark.parametrize("zp", [True, False])
+def test_gemm_decode_stream_vs_oracle(M, K, N, G, zp):
+    """Decode-shaped calls through the stream copy: within 1 ulp of the exact oracle, and
+    identical to an explicit stream call (cache hit path)."""
+    ops = _lib()
+    _note(f"decode stream M={M} K={K} N={N} G={G} zp={zp}")
+    p = make_awq_problem(M=M, K=K, N=N, group_size=G, seed=M + N + K)
+    t = _to_dev(p)
+    qz = t["qzeros"] if zp else None
+    y = ops.gemm(t["x"], t["qweight"], t["scales"], qz, G, layout="autoawq", decode_stream=True)
+    y2 = ops.gemm(t["x"], t["qweight"], t["scales"], qz, G, layout="autoawq")
+    assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
+    w = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"] if zp else None, G, zero_point=zp)
+    _check_vs_exact(y.cpu().numpy(), O.linear_exact(p["x"], w.T), f"stream M={M} N={N}")
+
+
+@pytest.mark.parametrize("M", [1, 16, 32])
+def test_decode_stream_split_k_bit_stable(M):
+    ops = _lib()
+    K, N, G = 12288, 4096, 128
+    p = make_awq_problem(M=M, K=K, N=N, group_size=G, seed=21)
+    t = _to_dev(p)
+    w = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"], G)
+    ye = O.linear_exact(p["x"], w.T)
+    for sk in (1, 4, 8):
+        _note(f"stream split-K M={M} split={sk}")
+        y1 = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, split_k=sk, layout="autoawq", decode_stream=True)
+        y2 = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, split_k=sk, layout="autoawq", decode_stream=True)
+        assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+        _check_vs_exact(y1.cpu().numpy(), ye, f"stream split {sk}")
