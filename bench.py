@@ -76,10 +76,10 @@ def _time_graph(torch, fn, reps, warmup=3):
     return start.elapsed_time(end) / reps, g
 
 
-def cpu_baseline(sample_seconds=20.0):
+def cpu_baseline(sample_seconds=12.0):
     """The reference CPU path restated (oracle/ref_cpu.py), cold: dequant + F.linear per call,
-    over the sweep shapes in order until ~sample_seconds of work (at least one full sweep
-    pass when that fits).  Returns GB/s of algorithmic bytes."""
+    cycling over the decode sweep shapes until ~sample_seconds of timed CPU work.  Returns
+    GB/s of algorithmic bytes."""
     import numpy as np
     import torch
     from oracle import ref_cpu as R
@@ -88,32 +88,42 @@ def cpu_baseline(sample_seconds=20.0):
     cores = max(1, min(cores, 16))
     torch.set_num_threads(cores)
     rng = np.random.default_rng(0)
-    done_bytes, t_total, calls, shapes = 0, 0.0, 0, []
-    warm = False
-    for M, N in SWEEP * 4:
+    probs = {}
+    for M, N in SWEEP:
         K = K_DEC
-        qw = torch.from_numpy(rng.integers(-2**31, 2**31 - 1, size=(N, K // 8), dtype=np.int64).astype(np.int32))
-        qz = torch.from_numpy(rng.integers(-2**31, 2**31 - 1, size=(N, K // G // 8), dtype=np.int64).astype(np.int32))
-        sc = torch.from_numpy((np.abs(rng.standard_normal((N, K // G))) * 0.02 + 1e-4).astype(np.float16))
-        x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16))
-        if not warm:
-            R.awq_linear_cpu(x, qw, sc, qz, G)
-            warm = True
-        t0 = time.perf_counter()
-        R.awq_linear_cpu(x, qw, sc, qz, G)
-        dt = time.perf_counter() - t0
-        t_total += dt
-        done_bytes += alg_bytes(M, K, N)
-        calls += 1
-        shapes.append(f"{M}x{K}x{N}")
-        if t_total >= sample_seconds:
-            break
+        if N not in probs:
+            qw = torch.from_numpy(rng.integers(-2**31, 2**31 - 1, size=(N, K // 8), dtype=np.int64).astype(np.int32))
+            qz = torch.from_numpy(rng.integers(-2**31, 2**31 - 1, size=(N, K // G // 8), dtype=np.int64).astype(np.int32))
+            sc = torch.from_numpy((np.abs(rng.standard_normal((N, K // G))) * 0.02 + 1e-4).astype(np.float16))
+            probs[N] = (qw, sc, qz)  # awq_linear_cpu argument order
+    xs = {m: torch.from_numpy(rng.standard_normal((m, K_DEC)).astype(np.float16)) for m in (1, 4, 16)}
+    R.awq_linear_cpu(xs[1], *probs[4096], G)  # warm-up
+    done_bytes, t_total, calls = 0, 0.0, 0
+    while t_total < sample_seconds:
+        for M, N in SWEEP:
+            t0 = time.perf_counter()
+            R.awq_linear_cpu(xs[M], *probs[N], G)
+            t_total += time.perf_counter() - t0
+            done_bytes += alg_bytes(M, K_DEC, N)
+            calls += 1
     return {
         "value": round(done_bytes / t_total / 1e9, 3), "unit": "GB/s", "cores": int(torch.get_num_threads()),
         "kind": "port",
-        "sample": f"{calls} cold calls (dequant + F.linear, fp16, K=4096, G=128) over the decode sweep "
-                  f"shapes in order, {t_total:.1f} s of CPU work",
+        "sample": f"{calls} cold calls (reference CPU path restated: int64-shift dequant + fp32 math + "
+                  f"F.linear in fp16, K=4096, G=128) cycling over the nine decode sweep shapes, "
+                  f"{t_total:.1f} s of CPU work",
     }
+
+
+def _traffic():
+    """HBM bytes per launch of the roofline kernel from the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-kernel calibration), or None."""
+    path = os.path.join(ROOT, "profiles", "decode_m1_k4096_n24576_traffic.json")
+    try:
+        with open(path) as f:
+            return int(json.load(f)["hbm_bytes_per_launch"])
+    except (OSError, ValueError, KeyError):
+        return None
 
 
 def main():
@@ -123,7 +133,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true")
-    ap.add_argument("--only", default="", help="profile mode: 'decode-m1n24576' or 'prefill' launches only")
+    ap.add_argument("--only", default="", help="profile mode: 'decode-m1n24576', 'prefill' or "
+                    "'copy-64MiB' (counter calibration) launches only")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -141,9 +152,19 @@ def main():
     if args.only == "decode-m1n24576":
         W = _weights(torch, K_DEC, 24576, 24, dev, 7)
         x = torch.randn((1, K_DEC), device=dev, generator=gen).half()
+        for qw, qz, sc in W:
+            ops.prepare_decode_stream(qw)
+        torch.cuda.synchronize()
         for _ in range(args.steps):
             for qw, qz, sc in W:
                 ops.gemm(x, qw, sc, qz, G, layout="autoawq")
+        torch.cuda.synchronize()
+        return
+    if args.only == "copy-64MiB":
+        src = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
         torch.cuda.synchronize()
         return
     if args.only == "prefill":
@@ -200,9 +221,9 @@ def main():
     r = per_shape["M1_N24576"]
     roof_bytes = alg_bytes(1, K_DEC, 24576)
     roofline = {"bound": "hbm", "achieved": r["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(r["GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "skinny_kn_kernel M=1 K=4096 N=24576", "bytes_per_launch": roof_bytes,
-                "avg_launch_us": r["us"]}
+                "frac": round(r["GBps"] / HBM_PEAK_GBS, 4), "traffic": _traffic(),
+                "kernel": "decode_kn_kernel (decode stream layout) M=1 K=4096 N=24576",
+                "bytes_per_launch": roof_bytes, "avg_launch_us": r["us"]}
     del W
 
     # ---- prefill (configs[3], M=2048, N=24576) ----
@@ -228,7 +249,7 @@ def main():
         "metric": "AWQ W4A16 decode GEMV sweep throughput (algorithmic GB/s, M=1-16)",
         "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps_timed,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "f16 activations, int4 weights (fp32 accumulate)",
+        "scaling": "weak", "vs_baseline": None, "dtype": "f16",
         "data": "synthetic (seeded int4/zeros/scales/activations with the benchmark distributions)",
         "config": {"workload": "configs[1] decode sweep: M in {1,4,16}, K=4096, N in {4096,6144,24576}, "
                                "group 128, AutoAWQ packing", "weight_copies_rotated": copies,

@@ -125,12 +125,10 @@ int awq_w4a16_gemm(const void* a, int64_t lda, const int32_t* qweight, const voi
   if (decode_covers(M, group_size)) {
     const DecodeMode mode = decode_mode(layout, act_dtype, scale_dtype);
     const DecodePlan sp = plan_decode(M, N, K, group_size, split_k, mode);
-    ga.nsplit = sp.nsplit;
-    ga.groups_per_split = sp.groups_per_split;
     if (sp.ws_bytes) {
       if (!workspace || workspace_bytes < sp.ws_bytes) return AWQ_ERR_WORKSPACE;
       if ((size_t)sp.tiles * sizeof(int) > kCounterBytes) return AWQ_ERR_UNSUPPORTED;
-      if (M * N * (int64_t)sp.nsplit * 4 > 0x7FFFFFFFLL) return AWQ_ERR_UNSUPPORTED;
+      if (sp.ws_bytes - kCounterBytes > 0x7FFFFFFFu) return AWQ_ERR_UNSUPPORTED;  // 32-bit offsets
       ga.counters = (int*)workspace;
       ga.partial = (float*)((char*)workspace + kCounterBytes);
     }
@@ -138,8 +136,6 @@ int awq_w4a16_gemm(const void* a, int64_t lda, const int32_t* qweight, const voi
     return launch_status();
   }
   if ((K % 64) != 0) return AWQ_ERR_SHAPE;
-  ga.nsplit = 1;
-  ga.groups_per_split = (int)(K / group_size);
   if (!launch_prefill(ga, seq, zp, act_dtype, scale_dtype, st)) return AWQ_ERR_UNSUPPORTED;
   return launch_status();
 }
@@ -162,7 +158,7 @@ int awq_w4a16_pack_decode_stream(const int32_t* qweight_kn, int32_t* out, int64_
   if (!qweight_kn || !out) return AWQ_ERR_NULL;
   if (K < 0 || N < 0 || (N % 8) != 0 || (K % 32) != 0) return AWQ_ERR_SHAPE;
   if (decode_stream_bytes(K, N) > 0x7FFFFFFFLL) return AWQ_ERR_UNSUPPORTED;
-  return launch_pack_decode_stream(qweight_kn, out, K, N, (hipStream_t)stream);
+  return launch_pack_decode_stream(qweight_kn, out, K, N, decode_stream_wpl(N), (hipStream_t)stream);
 }
 
 }  // extern "C"

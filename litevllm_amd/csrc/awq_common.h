@@ -21,6 +21,7 @@ typedef __bf16 bf16;
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -145,12 +146,17 @@ struct GemmArgs {
   const uint32_t* qz;
   const void* bias;
   uint16_t* c;
-  float* partial;   // [nsplit, M, N] fp32 (decode kernel with nsplit > 1)
-  int* counters;    // [column tiles]   (zero on entry and on exit)
+  float* partial;   // decode: [tiles, max_contrib, M, tile columns] fp32
+  int* counters;    // decode: [tiles], zero on entry and on exit
   int64_t lda, ldc;
   int M, N, K, G;
-  int nsplit, groups_per_split;
   int bias_dtype;
+};
+
+// Work decomposition of the decode kernel: tiles x ksteps units over `blocks` blocks; a tile
+// has at most max_contrib contributing blocks.
+struct DecodeWork {
+  int tiles, ksteps, blocks, max_contrib;
 };
 
 // Raw per-group constants of one packed word: 8 scales (16 bytes) and the zero word.

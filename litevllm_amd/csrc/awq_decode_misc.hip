@@ -1,0 +1,18 @@
+// Decode kernel instantiations for bf16 scales or bf16 activations (the fp16 ones are in
+// awq_decode.hip).
+#include "awq_decode_kernel.h"
+
+namespace awq_host {
+using namespace awq;
+
+bool launch_decode_misc(const GemmArgs& a, const DecodePlan& s, bool seq, bool zp, int act, int sbf,
+                        hipStream_t st) {
+  if (act == AWQ_DTYPE_F16) {
+    if (seq) return zp ? launch_sel<true, true, f16, false, false>(a, s, sbf, st) : launch_sel<true, false, f16, false, false>(a, s, sbf, st);
+    return zp ? launch_sel<false, true, f16, false, false>(a, s, sbf, st) : launch_sel<false, false, f16, false, false>(a, s, sbf, st);
+  }
+  if (seq) return zp ? launch_sel<true, true, bf16, false, false>(a, s, sbf, st) : launch_sel<true, false, bf16, false, false>(a, s, sbf, st);
+  return zp ? launch_sel<false, true, bf16, false, false>(a, s, sbf, st) : launch_sel<false, false, bf16, false, false>(a, s, sbf, st);
+}
+
+}  // namespace awq_host

@@ -10,13 +10,13 @@
 
 namespace awq_host {
 
-// Workspace layout of the decode kernel's split-K: [0, kCounterBytes) per-tile arrival
-// counters (zero between calls), then fp32 partials [nsplit, M, N].
+// Workspace layout of the decode kernel: [0, kCounterBytes) per-tile arrival counters (zero
+// between calls), then fp32 partials [tiles, max_contrib, M, tile columns].
 constexpr size_t kCounterBytes = 65536;
 
 struct DecodePlan {
-  int wpl, mt, nwv, depth;
-  int tiles, nsplit, groups_per_split;
+  int wpl, mt, nwv, depth, occ;  // words per lane, 16-token tiles, waves/block, ring depth, waves/SIMD
+  int tiles, ksteps, waves, blocks, max_contrib;
   size_t ws_bytes;
 };
 
@@ -33,12 +33,22 @@ inline DecodeMode decode_mode(int layout, int act, int sdt) {
 DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t G, int split_k, DecodeMode mode);
 bool launch_decode(const awq::GemmArgs& a, const DecodePlan& s, DecodeMode mode, bool seq, bool zp,
                    int act, int sdt, hipStream_t st);
+// bf16 scales or bf16 activations (sbf: scales are bf16)
+bool launch_decode_misc(const awq::GemmArgs& a, const DecodePlan& s, bool seq, bool zp, int act, int sbf,
+                        hipStream_t st);
 
-// Decode stream layout: for tile t (64 packed words = 512 columns), k-step s (32 rows),
-// chunk j (0..7) and lane l = 16 q + r, 16 bytes = words 64 t + 4 r .. + 3 of row 32 s + 8 q + j
-// (zero past the last word), stored at byte ((t * K/32 + s) * 8 + j) * 1024 + 16 l.
-inline int64_t decode_stream_bytes(int64_t K, int64_t N) { return awq::cdiv(N / 8, 64) * 64 * K * 4; }
-int launch_pack_decode_stream(const int32_t* qweight_kn, int32_t* out, int64_t K, int64_t N,
+// Decode stream layout with W words per lane (tile = 16 W packed words = 128 W columns): the
+// (tile t, k-step s) run of 2048 W bytes starts at byte (t * K/32 + s) * 2048 W.  Lane
+// l = 16 q + r owns 8 W words of it, u32 number j * W + w being word 16 W t + W r + w of row
+// 32 s + 8 q + j (zero past the last word); its u32 numbers 4 e .. 4 e + 3 (piece e) sit at
+// byte 1024 e + 16 l of the run, so every KiB is one piece of all 64 lanes.  W is fixed by
+// the shape (decode_stream_wpl).
+inline int decode_stream_wpl(int64_t N) { (void)N; return 1; }
+inline int64_t decode_stream_bytes(int64_t K, int64_t N) {
+  const int w = decode_stream_wpl(N);
+  return awq::cdiv(N / 8, 16 * w) * 16 * w * K * 4;
+}
+int launch_pack_decode_stream(const int32_t* qweight_kn, int32_t* out, int64_t K, int64_t N, int wpl,
                               hipStream_t st);
 
 // Prefill GEMM (M > 32 or group sizes the decode kernel does not cover).

@@ -251,15 +251,18 @@ def test_config3_prefill(M, N):
 
 
 # ------------------------------------------------------------------ decode stream layout
-def _stream_layout_numpy(qw_kn):
-    """The decode stream layout restated with numpy gathers: chunk (t, s, j), lane l = 16q + r
-    holds words 64t + 4r .. +3 of row 32s + 8q + j (zero past the last word)."""
+def _stream_layout_numpy(qw_kn, W):
+    """The decode stream layout restated with numpy gathers: in the (tile t, k-step s) run, lane
+    l = 16q + r owns u32 number n = j*W + w = word 16W t + W r + w of row 32s + 8q + j (zero
+    past the last word), stored at byte 1024 (n // 4) + 16 l + 4 (n % 4); runs tile-major."""
     K, NW = qw_kn.shape
-    tiles = -(-NW // 64)
-    pad = np.zeros((K, tiles * 64), dtype=np.int32)
+    tiles = -(-NW // (16 * W))
+    pad = np.zeros((K, tiles * 16 * W), dtype=np.int32)
     pad[:, :NW] = qw_kn
-    v = pad.reshape(K // 32, 4, 8, tiles, 16, 4)          # [s, q, j, t, r, w]
-    return np.ascontiguousarray(v.transpose(3, 0, 2, 1, 4, 5)).reshape(-1)
+    v = pad.reshape(K // 32, 4, 8, tiles, 16, W)              # [s, q, j, t, r, w]
+    lane_words = v.transpose(3, 0, 1, 4, 2, 5).reshape(tiles, K // 32, 64, 8 * W)  # [t, s, l, n]
+    pieces = lane_words.reshape(tiles, K // 32, 64, 2 * W, 4).transpose(0, 1, 3, 2, 4)  # [t, s, e, l, c]
+    return np.ascontiguousarray(pieces).reshape(-1)
 
 
 @pytest.mark.parametrize("K,N", [(256, 4096), (128, 1000), (64, 520)])
@@ -268,7 +271,7 @@ def test_pack_decode_stream_layout(K, N):
     rng = np.random.default_rng(K + N)
     qw = rng.integers(-2**31, 2**31 - 1, size=(K, N // 8), dtype=np.int64).astype(np.int32)
     got = ops.pack_decode_stream(torch.from_numpy(qw).to(DEV)).cpu().numpy()
-    assert np.array_equal(got, _stream_layout_numpy(qw))
+    assert np.array_equal(got, _stream_layout_numpy(qw, ops.DECODE_STREAM_WPL))
 
 
 @pytest.mark.parametrize("M,K,N,G", [(1, 2048, 5632, 128), (4, 4096, 6144, 128), (16, 1024, 1000, 64),
