@@ -48,7 +48,7 @@ extern "C" {
  *                      (n, j) = W[n, 8j + i]; qzeros int32 [N, ceil(K/G/8)] sequential along
  *                      the group axis; scales [N, K/G]  (tensor.py:842-858).
  * AWQ_LAYOUT_DECODE_STREAM : an AUTOAWQ qweight re-ordered by awq_w4a16_pack_decode_stream so
- *                      that the decode kernel reads it as contiguous 8 KiB runs; qzeros and
+ *                      that the decode kernel reads it as contiguous 2 KiB runs; qzeros and
  *                      scales stay in the AUTOAWQ layout.  Accepted by awq_w4a16_gemm for
  *                      M <= 32, group sizes 32/64/128, f16 activations and scales.
  */
@@ -102,7 +102,9 @@ size_t awq_w4a16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t g
 /* C[M, N] = A[M, K] . dequant(W)^T (+ bias), W dequantized exactly as awq_w4a16_dequant
  * does for act_dtype, products accumulated in fp32, one rounding to act_dtype at the end.
  *   a: [M, K] act_dtype (F16 or BF16), row stride lda (elements).
- *   layout: AUTOAWQ or KN_SEQ (qweight [K, N/8]) or NK_SEQ (qweight [N, K/8]).
+ *   layout: AUTOAWQ or KN_SEQ (qweight [K, N/8]), or DECODE_STREAM (M <= 32).  An NK_SEQ
+ *           weight is converted once with awq_w4a16_repack_nk_to_autoawq; passing NK_SEQ
+ *           here returns AWQ_ERR_UNSUPPORTED.
  *   qzeros == NULL: symmetric z = 8.  scales: scale_dtype (F16 or BF16).
  *   bias: NULL or [N] of bias_dtype (F16, BF16 or F32), added once in fp32.
  *   c: [M, N] act_dtype, row stride ldc.
