@@ -15,6 +15,9 @@ Extra measurements on the same JSON line:
     headline M=1 target) -- algorithmic bytes per launch / average launch duration from HIP
     events around back-to-back launches on the launch stream, against 8 TB/s;
   * ``prefill``: configs[3] at M=2048, N=24576 in TFLOP/s against 2.5 PFLOP/s dense fp16;
+  * ``moe``: configs[4] (E=64, top-8, H=2048, I=1024, g=128) at T=16 and T=512: routing +
+    grouped gate_up/activation/down + combine per step, algorithmic bytes (distinct experts
+    touched x expert bytes + x + y) against 8 TB/s and flops against 2.5 PFLOP/s;
   * ``cpu_baseline``: the reference's CPU path (dequant + F.linear, restated in
     ``oracle/ref_cpu.py``) on a bounded sample of the same sweep, timed on the host cores.
 """
@@ -115,6 +118,61 @@ def cpu_baseline(sample_seconds=12.0):
     }
 
 
+MOE_E, MOE_TOPK, MOE_H, MOE_I, MOE_G = 64, 8, 2048, 1024, 128
+
+
+def moe_expert_bytes():
+    """Algorithmic bytes of one expert: gate_up (K=H, N=2I) and down (K=I, N=H) weights,
+    scales and zeros."""
+    w = lambda K, N: K * N // 2 + (K // MOE_G) * N * 2 + (K // MOE_G) * (N // 8) * 4
+    return w(MOE_H, 2 * MOE_I) + w(MOE_I, MOE_H)
+
+
+def _moe_stacks(torch, ops, dev, copies, seed):
+    """`copies` expert sets (AutoAWQ stacks with the benchmark distributions), each with its
+    MoE stream copies built ahead of the timed region."""
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    rnd = lambda *shape: torch.randint(-2**31, 2**31 - 1, shape, dtype=torch.int32, device=dev, generator=gen)
+    scl = lambda *shape: (torch.randn(shape, device=dev, generator=gen).abs() * 0.02 + 1e-4).half()
+    E, H, I, g = MOE_E, MOE_H, MOE_I, MOE_G
+    out = []
+    for _ in range(copies):
+        gq, gz, gs = rnd(E, H, 2 * I // 8), rnd(E, H // g, 2 * I // 8), scl(E, H // g, 2 * I)
+        dq, dz, ds = rnd(E, I, H // 8), rnd(E, I // g, H // 8), scl(E, I // g, H)
+        ops.prepare_moe_stream(gq, True)
+        ops.prepare_moe_stream(dq, False)
+        out.append((gq, gs, gz, dq, ds, dz))
+    return out
+
+
+def _bench_moe(torch, ops, dev, T, copies=3):
+    """configs[4] step: routing (softmax, top-8, renormalise) + grouped gate_up/act/down +
+    combine, graph-replayed over `copies` expert sets (3 x 201 MB, beyond the MALL)."""
+    gen = torch.Generator(device=dev).manual_seed(100 + T)
+    stacks = _moe_stacks(torch, ops, dev, copies, 200 + T)
+    x = torch.randn((T, MOE_H), device=dev, generator=gen).half()
+    logits = torch.randn((T, MOE_E), device=dev, generator=gen).half()
+    y = torch.empty((T, MOE_H), device=dev, dtype=torch.float16)
+    _, tid = ops.moe_route(logits, MOE_TOPK)
+    distinct = int(torch.unique(tid).numel())
+
+    def run():
+        for st in stacks:
+            tw, ids = ops.moe_route(logits, MOE_TOPK)
+            ops.moe(x, tw, ids, *st, MOE_G, out=y)
+    ms, g = _time_graph(torch, run, 10)
+    del g, stacks
+    us = ms * 1e3 / copies
+    nbytes = distinct * moe_expert_bytes() + 2 * T * MOE_H * 2
+    flops = 2.0 * T * MOE_TOPK * (MOE_H * 2 * MOE_I + MOE_I * MOE_H)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    tfl = flops / (us * 1e-6) / 1e12
+    return {"T": T, "E": MOE_E, "top_k": MOE_TOPK, "H": MOE_H, "I": MOE_I, "group": MOE_G,
+            "distinct_experts": distinct, "us": round(us, 2), "bytes": nbytes, "GBps": round(gbs, 1),
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "TFLOPs": round(tfl, 1),
+            "mfma_frac": round(tfl / MFMA_F16_PEAK_TFLOPS, 4)}
+
+
 def _traffic():
     """HBM bytes per launch of the roofline kernel from the committed rocprofv3 PMC summary
     (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-kernel calibration), or None."""
@@ -133,6 +191,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--only", default="", help="profile mode: 'decode-m1n24576', 'prefill' or "
                     "'copy-64MiB' (counter calibration) launches only")
     args = ap.parse_args()
@@ -158,6 +217,17 @@ def main():
         for _ in range(args.steps):
             for qw, qz, sc in W:
                 ops.gemm(x, qw, sc, qz, G, layout="autoawq")
+        torch.cuda.synchronize()
+        return
+    if args.only in ("moe-t16", "moe-t512"):
+        T = 16 if args.only == "moe-t16" else 512
+        stacks = _moe_stacks(torch, ops, dev, 3, 21)
+        x = torch.randn((T, MOE_H), device=dev, generator=gen).half()
+        logits = torch.randn((T, MOE_E), device=dev, generator=gen).half()
+        for _ in range(args.steps):
+            for st in stacks:
+                tw, tid = ops.moe_route(logits, MOE_TOPK)
+                ops.moe(x, tw, tid, *st, MOE_G)
         torch.cuda.synchronize()
         return
     if args.only == "copy-64MiB":
@@ -245,6 +315,11 @@ def main():
                    "mfma_frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "peak_TFLOPs": MFMA_F16_PEAK_TFLOPS}
         del Wp
 
+    # ---- grouped MoE (configs[4]: E=64, top-8, H=2048, I=1024, g=128, zero points) ----
+    moe = None
+    if not args.no_moe:
+        moe = {T: _bench_moe(torch, ops, dev, T) for T in (16, 512)}
+
     line = {
         "metric": "AWQ W4A16 decode GEMV sweep throughput (algorithmic GB/s, M=1-16)",
         "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps_timed,
@@ -257,6 +332,7 @@ def main():
         "roofline": roofline,
         "per_shape": per_shape,
         "prefill": prefill,
+        "moe": moe,
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()

@@ -22,10 +22,14 @@
  *                         (awq_fused_gemm.py:2434-2443), replaced by an fp32 partial buffer
  *   awq_w4a16_repack   <- no kernel in the reference: the lossless layout conversion the
  *                         model loader would need at model_loader/__init__.py:756-797
- *   awq_w4a16_moe_*    <- the dense-expert fused_moe path used for zero-point AWQ experts
- *                         (vllm/model_executor/layers/fused_moe/fused_moe.py:4-77,
- *                         models/gemma4/moe.py:661-751) and the grouped int4 MoE wrapper
- *                         gemma4_moe_int4_prefill_grouped (kernels/triton/gemma4_moe_int4.py:2330-2584)
+ *   awq_w4a16_moe      <- the grouped int4 MoE wrappers gemma4_moe_int4_prefill_grouped(_fused)
+ *                         (vllm/kernels/triton/gemma4_moe_int4.py:2330-2584) and the expert loop
+ *                         of fused_moe (vllm/model_executor/layers/fused_moe/fused_moe.py:17-56)
+ *                         that zero-point AWQ experts take after dequantizing
+ *                         (vllm/model_executor/models/gemma4/moe.py:566-623)
+ *   awq_w4a16_moe_route <- the routing of fused_moe.py:12-15 / gemma4/moe.py:106-116
+ *   awq_w4a16_moe_pack_stream <- no kernel in the reference: the expert-major weight prepack the
+ *                         grouped kernels read (the reference reads its [E, N, K/8] stacks directly)
  */
 #ifndef AWQ_W4A16_H
 #define AWQ_W4A16_H
@@ -138,6 +142,57 @@ int64_t awq_w4a16_decode_stream_bytes(int64_t K, int64_t N);
  * weight so that decode-shaped calls stream the weight contiguously.  K % 32 == 0. */
 int awq_w4a16_pack_decode_stream(const int32_t* qweight_kn, int32_t* out, int64_t K, int64_t N,
                                  void* stream);
+
+/* ---- mixture of experts ------------------------------------------------------------
+ * Experts are stacks of AUTOAWQ matrices: gate_up qweight [E, H, 2I/8] (columns 0..I-1 the
+ * gate projection, I..2I-1 the up projection), scales [E, H/G, 2I], qzeros [E, H/G, 2I/8];
+ * down qweight [E, I, H/8], scales [E, I/G, H], qzeros [E, I/G, H/8].  A route is one
+ * (token t, slot j) pair, numbered r = t * top_k + j.
+ */
+#define AWQ_MOE_ACT_SILU 0      /* silu(gate) * up */
+#define AWQ_MOE_ACT_GELU_TANH 1 /* gelu_pytorch_tanh(gate) * up */
+
+/* Bytes of the MoE stream copy of an expert stack [E, K, N/8] (gate_up != 0: the gate_up
+ * stack, N = 2I, whose tiles pair gate and up columns; 0: the down stack).  0 if K % 32 or
+ * N % 8 (N % 16 for gate_up) fails. */
+int64_t awq_w4a16_moe_stream_bytes(int64_t E, int64_t K, int64_t N, int32_t gate_up);
+
+/* Lossless re-ordering of an AUTOAWQ expert stack [E, K, N/8] into the MoE stream layout read
+ * by awq_w4a16_moe (out holds awq_w4a16_moe_stream_bytes bytes).  Scales and zeros are used
+ * as they are. */
+int awq_w4a16_moe_pack_stream(const int32_t* qweight_ekn, int32_t* out, int64_t E, int64_t K, int64_t N,
+                              int32_t gate_up, void* stream);
+
+/* Routing of T tokens over E <= 256 experts, in fp32: p = softmax(logits[t, :E]); the top_k
+ * largest p in descending order (equal p: lower expert id first); with renormalize,
+ * w = p / max(sum of the selected p, 1e-8).  logits: [T, ld] of logits_dtype (F16, BF16, F32).
+ * topk_weights: [T, top_k] fp32; topk_ids: [T, top_k] int32. */
+int awq_w4a16_moe_route(const void* logits, int64_t ld, int32_t logits_dtype, int64_t T, int32_t E,
+                        int32_t top_k, int32_t renormalize, float* topk_weights, int32_t* topk_ids,
+                        void* stream);
+
+/* Workspace bytes of awq_w4a16_moe (route lists, the intermediate and per-route fp32 rows). */
+size_t awq_w4a16_moe_workspace_bytes(int64_t T, int64_t H, int64_t I, int32_t E, int32_t top_k);
+
+/* out[t] = sum over j of w[t, j] * down_e(act(gate_e(x[t])) * up_e(x[t])), e = ids[t, j]:
+ *   gate/up = x . dequant(W1_e)^T in fp32; h = act(gate) * up * w in fp32, rounded once to
+ *   act_dtype (the intermediate the reference keeps in x.dtype); y = h . dequant(W2_e)^T in
+ *   fp32 per route; out = one rounding of the sum of a token's y in slot order.  Weights are
+ *   dequantized exactly as awq_w4a16_dequant does.  Routes whose id is outside [0, E)
+ *   contribute nothing.  Results are bitwise reproducible.
+ *   x: [T, ldx] act_dtype (F16 or BF16); out: [T, ldo] act_dtype.
+ *   topk_ids: [T, top_k] int32 or int64 (ids_bits 32 / 64); topk_weights: [T, top_k] of
+ *   weights_dtype (F16, BF16 or F32).
+ *   gate_up_stream / down_stream: awq_w4a16_moe_pack_stream outputs; scales of scale_dtype;
+ *   qzeros both NULL (symmetric, z = 8) or both given.
+ *   group_size 32, 64 or 128 dividing H and I; H % 8 == 0, I % 8 == 0.
+ *   workspace: awq_w4a16_moe_workspace_bytes bytes, 256-byte aligned (no zeroing needed). */
+int awq_w4a16_moe(const void* x, int64_t ldx, const void* topk_ids, int32_t ids_bits, const void* topk_weights,
+                  int32_t weights_dtype, const int32_t* gate_up_stream, const void* gate_up_scales,
+                  const int32_t* gate_up_qzeros, const int32_t* down_stream, const void* down_scales,
+                  const int32_t* down_qzeros, void* out, int64_t ldo, int64_t T, int64_t H, int64_t I,
+                  int32_t E, int32_t top_k, int32_t group_size, int32_t activation, int32_t act_dtype,
+                  int32_t scale_dtype, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

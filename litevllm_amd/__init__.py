@@ -14,6 +14,14 @@ from .awq_triton import (  # noqa: F401
     awq_gemm_triton,
     packed_int4_fused_capability_check,
 )
+from .moe import (  # noqa: F401
+    AWQExperts,
+    awq_moe,
+    fused_moe,
+    gemma4_moe_int4_prefill_grouped,
+    gemma4_moe_int4_prefill_grouped_fused,
+    moe_route,
+)
 from .tensor import AWQWeight, PackedInt4Weight  # noqa: F401
 
 __version__ = "0.1.0"

@@ -46,7 +46,18 @@ SIGNATURES = {
                                                       _c_i64, _c_i32, _c_p]),
     "awq_w4a16_decode_stream_bytes": (_c_i64, [_c_i64, _c_i64]),
     "awq_w4a16_pack_decode_stream": (ctypes.c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_p]),
+    "awq_w4a16_moe_stream_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i32]),
+    "awq_w4a16_moe_pack_stream": (ctypes.c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p]),
+    "awq_w4a16_moe_route": (ctypes.c_int, [_c_p, _c_i64, _c_i32, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_p,
+                                           _c_p]),
+    "awq_w4a16_moe_workspace_bytes": (_c_sz, [_c_i64, _c_i64, _c_i64, _c_i32, _c_i32]),
+    "awq_w4a16_moe": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_i32, _c_p, _c_i32, _c_p, _c_p, _c_p, _c_p, _c_p,
+                                     _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32,
+                                     _c_i32, _c_i32, _c_i32, _c_p, _c_sz, _c_p]),
 }
+
+MOE_ACT_SILU = 0
+MOE_ACT_GELU_TANH = 1
 
 _lock = threading.Lock()
 _lib = None

@@ -161,4 +161,96 @@ int awq_w4a16_pack_decode_stream(const int32_t* qweight_kn, int32_t* out, int64_
   return launch_pack_decode_stream(qweight_kn, out, K, N, decode_stream_wpl(N), (hipStream_t)stream);
 }
 
+// ---- mixture of experts ----
+
+int64_t awq_w4a16_moe_stream_bytes(int64_t E, int64_t K, int64_t N, int32_t gate_up) {
+  if (E <= 0 || K <= 0 || N <= 0 || (K % 32) != 0 || (N % (gate_up ? 16 : 8)) != 0) return 0;
+  return moe_stream_bytes(E, K, N, gate_up ? 1 : 0);
+}
+
+int awq_w4a16_moe_pack_stream(const int32_t* qweight_ekn, int32_t* out, int64_t E, int64_t K, int64_t N,
+                              int32_t gate_up, void* stream) {
+  if (!qweight_ekn || !out) return AWQ_ERR_NULL;
+  if (E < 0 || K < 0 || N < 0 || (K % 32) != 0 || (N % (gate_up ? 16 : 8)) != 0) return AWQ_ERR_SHAPE;
+  if (E > 0 && moe_stream_bytes(1, K, N, gate_up ? 1 : 0) > 0x7FFFFFFFLL) return AWQ_ERR_UNSUPPORTED;
+  return launch_moe_pack_stream(qweight_ekn, out, E, K, N, gate_up ? 1 : 0, (hipStream_t)stream);
+}
+
+int awq_w4a16_moe_route(const void* logits, int64_t ld, int32_t logits_dtype, int64_t T, int32_t E,
+                        int32_t top_k, int32_t renormalize, float* topk_weights, int32_t* topk_ids,
+                        void* stream) {
+  if (!logits || !topk_weights || !topk_ids) return AWQ_ERR_NULL;
+  if (logits_dtype != AWQ_DTYPE_F16 && logits_dtype != AWQ_DTYPE_BF16 && logits_dtype != AWQ_DTYPE_F32)
+    return AWQ_ERR_UNSUPPORTED;
+  if (T < 0 || E <= 0 || E > 256 || top_k <= 0 || top_k > E || top_k > 64) return AWQ_ERR_SHAPE;
+  if (ld < E) return AWQ_ERR_STRIDE;
+  return launch_moe_route(logits, ld, logits_dtype, T, E, top_k, renormalize ? 1 : 0, topk_weights, topk_ids,
+                          (hipStream_t)stream);
+}
+
+size_t awq_w4a16_moe_workspace_bytes(int64_t T, int64_t H, int64_t I, int32_t E, int32_t top_k) {
+  if (T <= 0 || H <= 0 || I <= 0 || E <= 0 || top_k <= 0) return 0;
+  return (size_t)moe_workspace(T, H, I, E, top_k, 2).total;
+}
+
+int awq_w4a16_moe(const void* x, int64_t ldx, const void* topk_ids, int32_t ids_bits, const void* topk_weights,
+                  int32_t weights_dtype, const int32_t* gate_up_stream, const void* gate_up_scales,
+                  const int32_t* gate_up_qzeros, const int32_t* down_stream, const void* down_scales,
+                  const int32_t* down_qzeros, void* out, int64_t ldo, int64_t T, int64_t H, int64_t I,
+                  int32_t E, int32_t top_k, int32_t group_size, int32_t activation, int32_t act_dtype,
+                  int32_t scale_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  if (T < 0 || H <= 0 || I <= 0 || E <= 0 || top_k <= 0) return AWQ_ERR_SHAPE;
+  if (T == 0) return AWQ_OK;
+  if (!x || !topk_ids || !topk_weights || !gate_up_stream || !gate_up_scales || !down_stream ||
+      !down_scales || !out)
+    return AWQ_ERR_NULL;
+  if ((gate_up_qzeros == nullptr) != (down_qzeros == nullptr)) return AWQ_ERR_NULL;
+  if (!dtype_16(act_dtype) || !dtype_16(scale_dtype)) return AWQ_ERR_UNSUPPORTED;
+  if (weights_dtype != AWQ_DTYPE_F16 && weights_dtype != AWQ_DTYPE_BF16 && weights_dtype != AWQ_DTYPE_F32)
+    return AWQ_ERR_UNSUPPORTED;
+  if (ids_bits != 32 && ids_bits != 64) return AWQ_ERR_UNSUPPORTED;
+  if (activation != AWQ_MOE_ACT_SILU && activation != AWQ_MOE_ACT_GELU_TANH) return AWQ_ERR_UNSUPPORTED;
+  if (group_size != 32 && group_size != 64 && group_size != 128) return AWQ_ERR_UNSUPPORTED;
+  if ((H % group_size) != 0 || (I % group_size) != 0 || (H % 8) != 0 || (I % 8) != 0) return AWQ_ERR_SHAPE;
+  if (E > 65535) return AWQ_ERR_SHAPE;
+  if (ldx < H || ldo < H || (ldx % 8) != 0 || (ldo % 4) != 0) return AWQ_ERR_STRIDE;
+  if ((((uintptr_t)x) & 15) || (((uintptr_t)out) & 7) || (((uintptr_t)gate_up_scales) & 15) ||
+      (((uintptr_t)down_scales) & 15) || (((uintptr_t)gate_up_stream) & 15) || (((uintptr_t)down_stream) & 15))
+    return AWQ_ERR_STRIDE;
+  // 32-bit buffer offsets: one expert's tensors, the activations and the per-route buffers
+  const int64_t R = T * top_k;
+  if (moe_stream_bytes(1, H, 2 * I, 1) > 0x7FFFFFFFLL || moe_stream_bytes(1, I, H, 0) > 0x7FFFFFFFLL ||
+      T * ldx * 2 > 0x7FFFFFFFLL || R * I * 2 > 0x7FFFFFFFLL || R * H * 4 > 0x7FFFFFFFLL || R > 0x7FFFFFFFLL)
+    return AWQ_ERR_UNSUPPORTED;
+  const MoeWorkspace w = moe_workspace(T, H, I, E, top_k, 2);
+  if (!workspace || workspace_bytes < (size_t)w.total) return AWQ_ERR_WORKSPACE;
+  if (((uintptr_t)workspace) & 255) return AWQ_ERR_WORKSPACE;
+  MoeCall c{};
+  c.x = x;
+  c.ldx = ldx;
+  c.ids = topk_ids;
+  c.id64 = ids_bits == 64 ? 1 : 0;
+  c.rw = topk_weights;
+  c.rw_dtype = weights_dtype;
+  c.gu_qw = gate_up_stream;
+  c.gu_qz = gate_up_qzeros;
+  c.dn_qw = down_stream;
+  c.dn_qz = down_qzeros;
+  c.gu_sc = gate_up_scales;
+  c.dn_sc = down_scales;
+  c.out = out;
+  c.ldo = ldo;
+  c.T = T;
+  c.H = H;
+  c.I = I;
+  c.E = E;
+  c.topk = top_k;
+  c.G = group_size;
+  c.act_kind = activation;
+  c.act_dtype = act_dtype;
+  c.scale_dtype = scale_dtype;
+  c.workspace = workspace;
+  return launch_moe(c, (hipStream_t)stream);
+}
+
 }  // extern "C"

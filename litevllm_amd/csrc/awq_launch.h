@@ -63,4 +63,37 @@ int launch_repack_nk_to_autoawq(const int32_t* qweight_nk, const int32_t* qzeros
                                 void* scales_kn, int64_t N, int64_t K, int32_t group_size,
                                 hipStream_t st);
 
+// ---- mixture of experts ----
+// Stream-packed expert stacks: gate_up (N = 2I) pairs 8 gate words with the 8 up words of the
+// same columns per tile (tiles = ceil(I / 64)); down (gate_up = 0) uses tiles of 16 words.
+int64_t moe_tiles(int64_t N, int gate_up);
+int64_t moe_stream_bytes(int64_t E, int64_t K, int64_t N, int gate_up);
+int launch_moe_pack_stream(const int32_t* in, int32_t* out, int64_t E, int64_t K, int64_t N, int gate_up,
+                           hipStream_t st);
+int launch_moe_route(const void* logits, int64_t ld, int dtype, int64_t T, int E, int topk, int renorm,
+                     float* out_w, int32_t* out_ids, hipStream_t st);
+
+// Workspace of one MoE call (byte offsets): route counts [E] and lists [E][R] (int32), the
+// intermediate [R][I] (activation dtype) and the per-route down outputs [R][H] (fp32).
+struct MoeWorkspace {
+  int64_t counts, lists, tmp, y, total;
+};
+MoeWorkspace moe_workspace(int64_t T, int64_t H, int64_t I, int E, int topk, int act_bytes);
+
+struct MoeCall {
+  const void* x;
+  int64_t ldx;
+  const void* ids;
+  int id64;
+  const void* rw;
+  int rw_dtype;
+  const int32_t *gu_qw, *gu_qz, *dn_qw, *dn_qz;
+  const void *gu_sc, *dn_sc;
+  void* out;
+  int64_t ldo, T, H, I;
+  int E, topk, G, act_kind, act_dtype, scale_dtype;
+  void* workspace;
+};
+int launch_moe(const MoeCall& c, hipStream_t st);
+
 }  // namespace awq_host

@@ -1,0 +1,300 @@
+// Mixture-of-experts: routing (softmax -> top-k -> renormalise), expert-stack stream packing,
+// route lists, the combine, planning, and the f16 instantiations of the grouped GEMM kernels
+// (awq_moe_kernel.h); bf16 ones live in awq_moe_misc.hip.
+#include "awq_moe_kernel.h"
+
+namespace awq {
+
+__device__ __forceinline__ float load_logit(const void* p, int dtype, int64_t i) {
+  if (dtype == AWQ_DTYPE_F16) return h_bits2f(((const uint16_t*)p)[i]);
+  if (dtype == AWQ_DTYPE_BF16) return bf_bits2f(((const uint16_t*)p)[i]);
+  return ((const float*)p)[i];
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// Routing of one token per wave, in fp32 as the Gemma4 router does (models/gemma4/moe.py:106-116):
+// p = softmax(logits); the top_k largest p (ties: lower expert id first) in descending order;
+// with renormalize, w = p / max(sum of the selected p in that order, 1e-8).  E <= 256.
+__global__ void __launch_bounds__(256) moe_route_kernel(const void* logits, int64_t ld, int dtype, int64_t T,
+                                                        int E, int topk, int renorm, float* out_w,
+                                                        int32_t* out_ids) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;  // whole wave
+  float v[4];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = lane + 64 * j;
+    v[j] = e < E ? load_logit(logits, dtype, t * ld + e) : -INFINITY;
+    mx = fmaxf(mx, v[j]);
+  }
+  mx = wave_max(mx);
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = lane + 64 * j;
+    v[j] = e < E ? expf(v[j] - mx) : 0.f;
+    s += v[j];
+  }
+  s = wave_sum(s);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] = (lane + 64 * j) < E ? v[j] / s : -1.f;  // -1: not selectable
+  float mine = 0.f, sel_sum = 0.f;
+  int mine_id = 0;
+  for (int k = 0; k < topk; ++k) {
+    float bv = -1.f;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (v[j] > bv) { bv = v[j]; bi = lane + 64 * j; }  // j ascending: lower id wins ties
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const float ov = __shfl_xor(bv, o);
+      const int oi = __shfl_xor(bi, o);
+      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (lane + 64 * j == bi) v[j] = -1.f;
+    if (lane == k) { mine = bv; mine_id = bi; }
+    sel_sum += bv;
+  }
+  if (lane < topk) {
+    out_w[t * topk + lane] = renorm ? mine / fmaxf(sel_sum, 1e-8f) : mine;
+    out_ids[t * topk + lane] = mine_id;
+  }
+}
+
+// Expert stack [E][K][NW] (AutoAWQ words) -> [E][tiles][K/32] runs of 2048 bytes; lane
+// l = 16q + r's u32 j (row 32s + 8q + j of word moe_word(t, r)) at byte 1024 (j / 4) + 16 l
+// + 4 (j % 4) of its run -- the decode stream layout, tile words chosen by moe_word.
+__global__ void __launch_bounds__(256) moe_pack_stream_kernel(const uint32_t* __restrict__ in,
+                                                              uint32_t* __restrict__ out, int64_t K,
+                                                              int64_t NW, int64_t tiles, int half,
+                                                              int64_t E) {
+  const int64_t KS = K / 32;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= E * tiles * KS * 64) return;
+  const int l = (int)(idx & 63);
+  const int64_t run = idx >> 6;  // (e * tiles + t) * KS + s
+  const int64_t s = run % KS;
+  const int64_t et = run / KS;
+  const int64_t t = et % tiles, e = et / tiles;
+  const int q = l >> 4, r = l & 15;
+  const int w = moe_word((int)t, r, half, (int)NW);
+  const uint32_t* src = in + e * K * NW;
+  uint32_t* dst = out + run * 512;
+  for (int j = 0; j < 8; ++j) {
+    const int64_t row = s * 32 + 8 * q + j;
+    dst[(j >> 2) * 256 + l * 4 + (j & 3)] = w >= 0 ? src[row * NW + w] : 0u;
+  }
+}
+
+// Route lists: block e collects the routes r (in increasing order) whose id is e.
+__global__ void __launch_bounds__(256) moe_align_kernel(const void* ids, int id64, int R, int* lists,
+                                                        int* counts) {
+  __shared__ int s_wcnt[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int e = blockIdx.x;
+  int* list = lists + (int64_t)e * R;
+  int count = 0;
+  for (int base = 0; base < R; base += 256) {
+    const int idx = base + tid;
+    int id = -1;
+    if (idx < R) id = id64 ? (int)((const int64_t*)ids)[idx] : ((const int32_t*)ids)[idx];
+    const bool hit = id == e;
+    const uint64_t m = __ballot(hit);
+    if (lane == 0) s_wcnt[wave] = __popcll(m);
+    __syncthreads();
+    int off = count, tot = count;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      off += w < wave ? s_wcnt[w] : 0;
+      tot += s_wcnt[w];
+    }
+    if (hit) list[off + __popcll(m & ((1ull << lane) - 1ull))] = idx;
+    __syncthreads();  // s_wcnt is read by every wave before the next round writes it
+    count = tot;
+  }
+  if (tid == 0) counts[e] = count;
+}
+
+// out[t, 4c .. 4c+3] = round(sum over j of y[t * topk + j, 4c ..]) in j order; routes whose
+// expert id is outside [0, E) contribute nothing.
+template <typename T>
+__global__ void __launch_bounds__(256) moe_combine_kernel(const float* __restrict__ y, const void* ids, int id64,
+                                                          int E, int64_t T_tok, int64_t H, int topk,
+                                                          uint16_t* __restrict__ out, int64_t ldo) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t hq = H >> 2;
+  if (idx >= T_tok * hq) return;
+  const int64_t t = idx / hq, c = idx - t * hq;
+  f32x4 s = {0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < topk; ++j) {
+    const int64_t rt = t * topk + j;
+    const int id = id64 ? (int)((const int64_t*)ids)[rt] : ((const int32_t*)ids)[rt];
+    if (id < 0 || id >= E) continue;
+    s += *(const f32x4*)(y + rt * H + 4 * c);
+  }
+  u32x2 st;
+  st[0] = pack2<T>(s[0], s[1]);
+  st[1] = pack2<T>(s[2], s[3]);
+  *(u32x2*)(out + t * ldo + 4 * c) = st;
+}
+
+}  // namespace awq
+
+namespace awq_host {
+using namespace awq;
+
+static int launch_status() {
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? AWQ_OK : AWQ_ERR_LAUNCH;
+}
+
+int64_t moe_tiles(int64_t N, int gate_up) {
+  return gate_up ? cdiv(N / 16, 8) : cdiv(N / 8, 16);
+}
+
+int64_t moe_stream_bytes(int64_t E, int64_t K, int64_t N, int gate_up) {
+  return E * moe_tiles(N, gate_up) * (K / 32) * 2048;
+}
+
+int launch_moe_pack_stream(const int32_t* in, int32_t* out, int64_t E, int64_t K, int64_t N, int gate_up,
+                           hipStream_t st) {
+  const int64_t tiles = moe_tiles(N, gate_up);
+  const int64_t n = E * tiles * (K / 32) * 64;
+  if (n == 0) return AWQ_OK;
+  hipLaunchKernelGGL(moe_pack_stream_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st, (const uint32_t*)in,
+                     (uint32_t*)out, K, N / 8, tiles, gate_up ? (int)(N / 16) : 0, E);
+  return launch_status();
+}
+
+int launch_moe_route(const void* logits, int64_t ld, int dtype, int64_t T, int E, int topk, int renorm,
+                     float* out_w, int32_t* out_ids, hipStream_t st) {
+  if (T == 0) return AWQ_OK;
+  hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, st, logits, ld, dtype, T, E, topk,
+                     renorm, out_w, out_ids);
+  return launch_status();
+}
+
+template <int MODE, int MT, bool ZP, typename T, bool FAST>
+static void launch_gemm_t(const MoeArgs& a, int E, int sbf, hipStream_t st) {
+  const dim3 grid((unsigned)a.tiles, (unsigned)E);
+  const int spg = a.G / 32;
+  if (spg == 4)
+    hipLaunchKernelGGL((moe_gemm_kernel<MODE, MT, 2, 4, ZP, T, FAST>), grid, dim3(512), 0, st, a, sbf);
+  else if (spg == 2)
+    hipLaunchKernelGGL((moe_gemm_kernel<MODE, MT, 2, 2, ZP, T, FAST>), grid, dim3(512), 0, st, a, sbf);
+  else
+    hipLaunchKernelGGL((moe_gemm_kernel<MODE, MT, 2, 1, ZP, T, FAST>), grid, dim3(512), 0, st, a, sbf);
+}
+
+template <int MODE>
+static void launch_gemm_f16(const MoeArgs& a, int E, int mt, bool zp, hipStream_t st) {
+  if (mt == 4) zp ? launch_gemm_t<MODE, 4, true, f16, true>(a, E, 0, st) : launch_gemm_t<MODE, 4, false, f16, true>(a, E, 0, st);
+  else if (mt == 2) zp ? launch_gemm_t<MODE, 2, true, f16, true>(a, E, 0, st) : launch_gemm_t<MODE, 2, false, f16, true>(a, E, 0, st);
+  else zp ? launch_gemm_t<MODE, 1, true, f16, true>(a, E, 0, st) : launch_gemm_t<MODE, 1, false, f16, true>(a, E, 0, st);
+}
+
+// 16-token tiles per wave group, from the expected routes per expert
+static int moe_mt(int64_t R, int E) {
+  const int64_t avg = R / (E > 0 ? E : 1);
+  return avg <= 12 ? 1 : (avg <= 28 ? 2 : 4);
+}
+
+MoeWorkspace moe_workspace(int64_t T, int64_t H, int64_t I, int E, int topk, int act_bytes) {
+  MoeWorkspace w{};
+  const int64_t R = T * topk;
+  auto al = [](int64_t x) { return (x + 255) & ~(int64_t)255; };
+  w.counts = 0;
+  w.lists = al(w.counts + (int64_t)E * 4);
+  w.tmp = al(w.lists + (int64_t)E * R * 4);
+  w.y = al(w.tmp + R * I * act_bytes);
+  w.total = al(w.y + R * H * 4);
+  return w;
+}
+
+int launch_moe(const MoeCall& c, hipStream_t st) {
+  const int64_t R = c.T * c.topk;
+  const int act_bytes = 2;
+  const MoeWorkspace w = moe_workspace(c.T, c.H, c.I, c.E, c.topk, act_bytes);
+  char* ws = (char*)c.workspace;
+  int* counts = (int*)(ws + w.counts);
+  int* lists = (int*)(ws + w.lists);
+  uint16_t* tmp = (uint16_t*)(ws + w.tmp);
+  float* y = (float*)(ws + w.y);
+  const bool zp = c.gu_qz != nullptr;
+  const int mt = moe_mt(R, c.E);
+
+  hipLaunchKernelGGL(moe_align_kernel, dim3((unsigned)c.E), dim3(256), 0, st, c.ids, c.id64, (int)R, lists, counts);
+  if (launch_status() != AWQ_OK) return AWQ_ERR_LAUNCH;
+
+  MoeArgs gu{};
+  gu.a = (const uint16_t*)c.x;
+  gu.qw = (const uint32_t*)c.gu_qw;
+  gu.sc = (const uint16_t*)c.gu_sc;
+  gu.qz = (const uint32_t*)c.gu_qz;
+  gu.lists = lists;
+  gu.counts = counts;
+  gu.rw = c.rw;
+  gu.out = tmp;
+  gu.lda = c.ldx;
+  gu.ldo = c.I;
+  gu.R = (int)R;
+  gu.topk = c.topk;
+  gu.K = (int)c.H;
+  gu.N = (int)(2 * c.I);
+  gu.G = c.G;
+  gu.half = (int)(c.I / 8);
+  gu.tiles = (int)moe_tiles(2 * c.I, 1);
+  gu.rows_a = (int)c.T;
+  gu.rw_dtype = c.rw_dtype;
+  gu.act_kind = c.act_kind;
+
+  MoeArgs dn = gu;
+  dn.a = tmp;
+  dn.qw = (const uint32_t*)c.dn_qw;
+  dn.sc = (const uint16_t*)c.dn_sc;
+  dn.qz = (const uint32_t*)c.dn_qz;
+  dn.out = y;
+  dn.lda = c.I;
+  dn.ldo = c.H;
+  dn.K = (int)c.I;
+  dn.N = (int)c.H;
+  dn.half = 0;
+  dn.tiles = (int)moe_tiles(c.H, 0);
+  dn.rows_a = (int)R;
+
+  const int sbf = c.scale_dtype == AWQ_DTYPE_BF16 ? 1 : 0;
+  if (c.act_dtype == AWQ_DTYPE_F16 && !sbf) {
+    launch_gemm_f16<0>(gu, c.E, mt, zp, st);
+    if (launch_status() != AWQ_OK) return AWQ_ERR_LAUNCH;
+    launch_gemm_f16<1>(dn, c.E, mt, zp, st);
+  } else {
+    if (!launch_moe_misc(gu, dn, c.E, zp, c.act_dtype, sbf, st)) return AWQ_ERR_UNSUPPORTED;
+  }
+  if (launch_status() != AWQ_OK) return AWQ_ERR_LAUNCH;
+
+  const int64_t n = c.T * (c.H / 4);
+  if (c.act_dtype == AWQ_DTYPE_BF16)
+    hipLaunchKernelGGL(moe_combine_kernel<bf16>, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st, y, c.ids, c.id64, c.E,
+                       c.T, c.H, c.topk, (uint16_t*)c.out, c.ldo);
+  else
+    hipLaunchKernelGGL(moe_combine_kernel<f16>, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st, y, c.ids, c.id64, c.E,
+                       c.T, c.H, c.topk, (uint16_t*)c.out, c.ldo);
+  return launch_status();
+}
+
+}  // namespace awq_host

@@ -1,0 +1,268 @@
+// Grouped AWQ W4A16 mixture-of-experts kernels for gfx950: the role of
+// gemma4_moe_int4_prefill_grouped / _fused (vllm/kernels/triton/gemma4_moe_int4.py:2330-2584,
+// kernels at 626-760 and 894-1030) and of the expert loop of fused_moe
+// (vllm/model_executor/layers/fused_moe/fused_moe.py:4-77), for zero-point or symmetric int4
+// experts with any group size 32 / 64 / 128.
+//
+//  * route lists (moe_align_kernel): for each expert, the indices r = token * top_k + j of
+//    the routes that chose it, in route order (the stable sort by expert id of the reference
+//    wrapper, gemma4_moe_int4.py:2520-2523), plus the count.
+//  * gate_up (moe_gemm_kernel<0>): grid (column tile, expert).  An expert's gate_up weight
+//    [H, 2I] is read in the stream layout with its tiles pairing 8 gate words with the 8 up
+//    words of the same columns, so one MFMA operand set yields gate and up together.  The
+//    block's 8 waves split K; the sums meet in LDS in a fixed order; the epilogue computes
+//    act(gate) * up * route_weight in fp32 and rounds once to the activation dtype -- the
+//    intermediate the reference keeps in x.dtype (gemma4_moe_int4.py:748-760).
+//  * down (moe_gemm_kernel<1>): the same structure over the intermediate rows, writing one fp32
+//    row per route.
+//  * combine (moe_combine_kernel): out[t] = round(sum_j y[t * top_k + j]) in j order, fp32.
+//
+// Every route row is computed independently of which other rows share its tile, and every sum
+// runs in a fixed order, so results are bitwise reproducible.
+#pragma once
+
+#include "awq_common.h"
+#include "awq_launch.h"
+
+namespace awq {
+
+// Packed word of the expert weight held by lane r of tile t: with gate/up pairing (half =
+// I / 8 > 0) lanes 0-7 hold gate words 8t .. 8t+7 and lanes 8-15 the up words half + 8t ..;
+// without, lanes hold words 16t .. 16t+15.  -1 past the end (zero weights, never stored).
+__host__ __device__ inline int moe_word(int t, int r, int half, int NW) {
+  if (half > 0) {
+    const int w = 8 * t + (r & 7);
+    if (w >= half) return -1;
+    return r < 8 ? w : half + w;
+  }
+  const int w = 16 * t + r;
+  return w < NW ? w : -1;
+}
+
+struct MoeArgs {
+  const uint16_t* a;   // gate_up: x [T, lda]; down: the intermediate [R, lda = I]
+  const uint32_t* qw;  // stream-packed expert stack [E][tiles][K/32][2048 B]
+  const uint16_t* sc;  // scales [E][K/G][N]
+  const uint32_t* qz;  // zeros [E][K/G][N/8] (AutoAWQ order) or null (symmetric, z = 8)
+  const int* lists;    // route lists [E][R]
+  const int* counts;   // routes per expert [E]
+  const void* rw;      // route weights [R] (gate_up only)
+  void* out;           // gate_up: [R][ldo] act dtype; down: [R][ldo] fp32
+  int64_t lda, ldo;
+  int R, topk, K, N, G, half, tiles, rows_a;
+  int rw_dtype, act_kind;
+};
+
+__device__ __forceinline__ float load_route_weight(const void* rw, int dtype, int r) {
+  if (dtype == AWQ_DTYPE_F16) return h_bits2f(((const uint16_t*)rw)[r]);
+  if (dtype == AWQ_DTYPE_BF16) return bf_bits2f(((const uint16_t*)rw)[r]);
+  return ((const float*)rw)[r];
+}
+
+// act(g) of gemma4_moe_int4.py:748-756: silu, or GELU (tanh form) as g * sigmoid(2 * inner)
+__device__ __forceinline__ float moe_act(float g, int kind) {
+  if (kind == 1) {
+    const float inner = 0.7978845608028654f * (g + 0.044715f * g * g * g);
+    return g / (1.0f + expf(-2.0f * inner));
+  }
+  return g / (1.0f + expf(-g));
+}
+
+template <int MODE, int MT, int D, int SPG, bool ZP, typename T, bool FAST>
+__global__ void __launch_bounds__(512) moe_gemm_kernel(const MoeArgs p, int scale_bf16) {
+  constexpr int NWV = 8;
+  constexpr int NACC = 8 * MT;
+  constexpr int CH = NACC < 16 ? NACC : 16;
+  static_assert(NACC % CH == 0, "");
+  __shared__ f32x4 red[(NWV / 2) * CH * 64];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q = lane >> 4, r = lane & 15;
+  const int t = blockIdx.x, e = blockIdx.y;
+  const int count = p.counts[e];
+  if (count == 0) return;  // whole block
+
+  const int KS = p.K >> 5;
+  const int NW = p.N >> 3;
+  const int ngroups = p.K / p.G;
+  const int* list = p.lists + (int64_t)e * p.R;
+  const uint32_t stream_bytes = (uint32_t)p.tiles * (uint32_t)KS * 2048u;
+  const __amdgpu_buffer_rsrc_t wrs = make_rsrc((const char*)p.qw + (int64_t)e * stream_bytes, stream_bytes);
+  const __amdgpu_buffer_rsrc_t srs = make_rsrc(p.sc + (int64_t)e * ngroups * p.N, (uint32_t)ngroups * (uint32_t)p.N * 2u);
+  const __amdgpu_buffer_rsrc_t zrs =
+      make_rsrc(ZP ? (const void*)(p.qz + (int64_t)e * ngroups * NW) : (const void*)p.sc, ZP ? (uint32_t)ngroups * (uint32_t)NW * 4u : 0u);
+  const __amdgpu_buffer_rsrc_t xrs = make_rsrc(p.a, (uint32_t)((uint64_t)p.rows_a * (uint64_t)p.lda * 2u));
+  const int word = moe_word(t, r, p.half, NW);
+  const uint32_t wc = word < 0 ? 0u : (uint32_t)word;  // padding lanes: word 0's constants, zero weights
+  const MagicK mk = magic_consts();
+
+  for (int base = 0; base < count; ) {
+    // wave groups of 16 * MT rows; the waves of a group split K
+    const int left = count - base;
+    int ng = 1;
+    while (ng < NWV && ng * 16 * MT < left) ng <<= 1;
+    const int wpg = NWV / ng;
+    const int gi = wave / wpg, ki = wave - gi * wpg;
+    const int m0 = base + gi * 16 * MT;
+    const bool active = m0 < count;  // wave-uniform
+    const int ks0 = KS * ki / wpg, ks1 = KS * (ki + 1) / wpg;
+    const int nunits = ks1 - ks0;
+
+    f32x4 acc[8][MT];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    int route[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = m0 + mt * 16 + r;
+      route[mt] = m < count ? list[m] : -1;
+    }
+
+    if (active && nunits > 0) {
+      uint32_t x_off[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int arow = MODE == 0 ? route[mt] / p.topk : route[mt];
+        x_off[mt] = route[mt] < 0 ? 0x80000000u : ((uint32_t)arow * (uint32_t)p.lda + 8u * (uint32_t)q) * 2u;
+      }
+      uint32_t raw[D][8];
+      u32x4 xr[D][MT];
+      WordSZ sz[D];
+      ColConst cc[8];
+      int iks = ks0;
+      bool ipast = false;
+      auto issue = [&](int slot) {
+        const int ks = iks;
+        const int kbase = (int)(((uint32_t)t * (uint32_t)KS + (uint32_t)ks) * 2048u);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const u32x4 v = __builtin_bit_cast(
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, (int)((uint32_t)lane * 16u), kbase + 1024 * i, 0));
+#pragma unroll
+          for (int c = 0; c < 4; ++c) raw[slot][4 * i + c] = v[c];
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          xr[slot][mt] = __builtin_bit_cast(
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, ipast ? (int)0x80000000 : (int)x_off[mt], ks * 64, 0));
+        const int g = ks / SPG;
+        sz[slot].s4 = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(srs, (int)(16u * wc), (int)((uint32_t)g * (uint32_t)p.N * 2u), 0));
+        sz[slot].zw = ZP ? __builtin_amdgcn_raw_buffer_load_b32(zrs, (int)(4u * wc), (int)((uint32_t)g * (uint32_t)NW * 4u), 0)
+                         : 0x88888888u;
+        if (iks + 1 < ks1) ++iks; else ipast = true;
+      };
+      int cks = ks0, g_cur = -1;
+      auto step = [&](int done, int slot) {
+        if (done < nunits) {
+          const int g = cks / SPG;
+          if (g != g_cur) {
+            g_cur = g;
+            prep_consts<false, FAST>(sz[slot], scale_bf16 != 0, cc);
+          }
+          ++cks;
+        }
+        uint32_t mlo[4], mhi[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          mlo[v] = pair_lo(raw[slot][2 * v], raw[slot][2 * v + 1]);
+          mhi[v] = pair_hi(raw[slot][2 * v], raw[slot][2 * v + 1]);
+        }
+#define AWQ_MOE_NIB(I)                                                        \
+        {                                                                     \
+          const u32x4 op = rows_operand<I, FAST, T>(mlo, mhi, cc[I], mk);     \
+          _Pragma("unroll") for (int mt = 0; mt < MT; ++mt)                   \
+              acc[I][mt] = MfmaOp<T>::run(op, xr[slot][mt], acc[I][mt]);     \
+        }
+        AWQ_MOE_NIB(0) AWQ_MOE_NIB(1) AWQ_MOE_NIB(2) AWQ_MOE_NIB(3)
+        AWQ_MOE_NIB(4) AWQ_MOE_NIB(5) AWQ_MOE_NIB(6) AWQ_MOE_NIB(7)
+#undef AWQ_MOE_NIB
+      };
+#pragma unroll
+      for (int u = 0; u < D; ++u) issue(u);
+      __builtin_amdgcn_sched_barrier(0);
+      for (int done = 0; done < nunits; done += D) {
+#pragma unroll
+        for (int u = 0; u < D; ++u) {
+          step(done + u, u);
+          __builtin_amdgcn_sched_barrier(0);
+          issue(u);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+
+    // ---- the group's sums meet in LDS, fixed tree order ----
+    const int hslots = wpg >> 1;  // reduction slots per group
+#pragma unroll
+    for (int c0 = 0; c0 < NACC; c0 += CH) {
+      for (int half = hslots; half >= 1; half >>= 1) {
+        if (ki >= half && ki < 2 * half) {
+#pragma unroll
+          for (int c = 0; c < CH; ++c)
+            red[((gi * hslots + ki - half) * CH + c) * 64 + lane] = acc[(c0 + c) / MT][(c0 + c) % MT];
+        }
+        __syncthreads();
+        if (ki < half) {
+#pragma unroll
+          for (int c = 0; c < CH; ++c) acc[(c0 + c) / MT][(c0 + c) % MT] += red[((gi * hslots + ki) * CH + c) * 64 + lane];
+        }
+        __syncthreads();
+      }
+    }
+
+    // ---- epilogue: the group's first wave holds the sums ----
+    // lane (q, r), accumulator [i][mt] element v: row m0 + 16 mt + r, tile word 4q + v, column
+    // nib_col(i) of that word
+    if (ki == 0 && active) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int rt = route[mt];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          float o[8];
+#pragma unroll
+          for (int c = 0; c < 8; ++c) o[c] = acc[col_nib<false>(c)][mt][v];
+          if constexpr (MODE == 0) {
+            // up values of the same columns sit 32 lanes higher (tile words 8 .. 15)
+            float u[8];
+#pragma unroll
+            for (int c = 0; c < 8; ++c) u[c] = __shfl_xor(o[c], 32);
+            const int gw = 8 * t + 4 * q + v;  // gate word
+            if (q < 2 && rt >= 0 && gw < p.half) {
+              const float wgt = load_route_weight(p.rw, p.rw_dtype, rt);
+              float h[8];
+#pragma unroll
+              for (int c = 0; c < 8; ++c) h[c] = moe_act(o[c], p.act_kind) * u[c] * wgt;
+              u32x4 st;
+              st[0] = pack2<T>(h[0], h[1]);
+              st[1] = pack2<T>(h[2], h[3]);
+              st[2] = pack2<T>(h[4], h[5]);
+              st[3] = pack2<T>(h[6], h[7]);
+              *(u32x4*)((uint16_t*)p.out + (int64_t)rt * p.ldo + 8 * gw) = st;
+            }
+          } else {
+            const int w = 16 * t + 4 * q + v;
+            if (rt >= 0 && w < NW) {
+              float* dst = (float*)p.out + (int64_t)rt * p.ldo + 8 * w;
+              *(f32x4*)dst = f32x4{o[0], o[1], o[2], o[3]};
+              *(f32x4*)(dst + 4) = f32x4{o[4], o[5], o[6], o[7]};
+            }
+          }
+        }
+      }
+    }
+    base += ng * 16 * MT;
+  }
+}
+
+}  // namespace awq
+
+namespace awq_host {
+// bf16 activations or bf16 scales (awq_moe_misc.hip); false if the dtype is not provided
+bool launch_moe_misc(const awq::MoeArgs& gu, const awq::MoeArgs& dn, int E, bool zp, int act, int sbf,
+                     hipStream_t st);
+}  // namespace awq_host

@@ -266,3 +266,115 @@ def gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, qzeros: t
         _ptr(ws), ws_bytes if ws is not None else 0, stream)
     L.check("awq_w4a16_gemm", rc)
     return out
+
+
+# ------------------------------------------------------------------ mixture of experts
+MOE_ACTIVATIONS = {"silu": L.MOE_ACT_SILU, "swish": L.MOE_ACT_SILU,
+                   "gelu": L.MOE_ACT_GELU_TANH, "gelu_pytorch_tanh": L.MOE_ACT_GELU_TANH}
+
+
+def moe_route(gating_output: torch.Tensor, topk: int, renormalize: bool = True):
+    """softmax -> top-k -> renormalise in fp32 on the device: ``(weights fp32, ids int32)``,
+    each ``[T, topk]``; equal probabilities select the lower expert id first."""
+    lib = L.load()
+    dev = _require_device(gating_output)
+    if gating_output.dim() != 2:
+        raise ValueError("gating_output must be [T, E]")
+    g = gating_output if gating_output.stride(1) == 1 else gating_output.contiguous()
+    T, E = int(g.shape[0]), int(g.shape[1])
+    w = torch.empty((T, int(topk)), dtype=torch.float32, device=dev)
+    ids = torch.empty((T, int(topk)), dtype=torch.int32, device=dev)
+    rc = lib.awq_w4a16_moe_route(_ptr(g), int(g.stride(0)), dtype_code(g.dtype), T, E, int(topk),
+                                 1 if renormalize else 0, _ptr(w), _ptr(ids), _stream_ptr(dev))
+    L.check("awq_w4a16_moe_route", rc)
+    return w, ids
+
+
+def pack_moe_stream(qweight: torch.Tensor, gate_up: bool) -> torch.Tensor:
+    """AutoAWQ expert stack [E, K, N/8] -> the MoE stream layout (int32, flat).  For the
+    gate_up stack (N = 2I) each tile pairs gate and up columns."""
+    lib = L.load()
+    _require_device(qweight)
+    if qweight.dtype != torch.int32 or qweight.dim() != 3:
+        raise ValueError("expert qweight must be a 3-D int32 tensor [E, K, N/8]")
+    e, k, n = int(qweight.shape[0]), int(qweight.shape[1]), int(qweight.shape[2]) * 8
+    nbytes = int(lib.awq_w4a16_moe_stream_bytes(e, k, n, 1 if gate_up else 0))
+    if nbytes <= 0:
+        raise ValueError(f"no MoE stream layout for E={e}, K={k}, N={n}")
+    qweight = qweight.contiguous()
+    out = torch.empty(nbytes // 4, dtype=torch.int32, device=qweight.device)
+    rc = lib.awq_w4a16_moe_pack_stream(_ptr(qweight), _ptr(out), e, k, n, 1 if gate_up else 0,
+                                       _stream_ptr(qweight.device))
+    L.check("awq_w4a16_moe_pack_stream", rc)
+    return out
+
+
+MOE_STREAM_CACHE = _DerivedCache(pack_moe_stream)
+
+
+def prepare_moe_stream(qweight: torch.Tensor, gate_up: bool) -> torch.Tensor:
+    """Build (and cache) the MoE stream copy of an AutoAWQ expert stack."""
+    return MOE_STREAM_CACHE.get(qweight, args=(bool(gate_up),))
+
+
+def repack_experts_ref_to_autoawq(qweight: torch.Tensor, scales: torch.Tensor,
+                                  qzeros: torch.Tensor | None, group_size: int):
+    """Reference expert stacks [E, N, K/8] -> AutoAWQ stacks [E, K, N/8] (lossless)."""
+    outs = [repack_ref_to_autoawq(qweight[e], scales[e], qzeros[e] if qzeros is not None else None,
+                                  group_size) for e in range(int(qweight.shape[0]))]
+    qw = torch.stack([o[0] for o in outs])
+    sc = torch.stack([o[1] for o in outs])
+    qz = torch.stack([o[2] for o in outs]) if qzeros is not None else None
+    return qw, sc, qz
+
+
+def moe(x: torch.Tensor, topk_weights: torch.Tensor, topk_ids: torch.Tensor,
+        gate_up_qweight: torch.Tensor, gate_up_scales: torch.Tensor, gate_up_qzeros: torch.Tensor | None,
+        down_qweight: torch.Tensor, down_scales: torch.Tensor, down_qzeros: torch.Tensor | None,
+        group_size: int, activation: str = "silu", out: torch.Tensor | None = None) -> torch.Tensor:
+    """Grouped AWQ MoE on AutoAWQ expert stacks: gate_up [E, H, 2I/8], down [E, I, H/8]
+    (scales and zeros in the matching AutoAWQ layouts; zeros None for symmetric z = 8).
+
+    ``out[t] = sum_j w[t, j] * down_e(act(gate_e(x_t)) * up_e(x_t))``, e = ``topk_ids[t, j]``.
+    """
+    lib = L.load()
+    dev = _require_device(x, topk_weights, topk_ids, gate_up_qweight, gate_up_scales, gate_up_qzeros,
+                          down_qweight, down_scales, down_qzeros, out)
+    if x.dim() != 2:
+        raise ValueError("x must be [T, H]")
+    if (gate_up_qzeros is None) != (down_qzeros is None):
+        raise ValueError("gate_up and down zeros must both be given or both be None")
+    try:
+        act = MOE_ACTIVATIONS[str(activation).strip().lower()]
+    except KeyError:
+        raise ValueError(f"unsupported activation {activation!r}") from None
+    T, H = int(x.shape[0]), int(x.shape[1])
+    E = int(gate_up_qweight.shape[0])
+    I = int(gate_up_qweight.shape[2]) * 4
+    if int(gate_up_qweight.shape[1]) != H or tuple(down_qweight.shape) != (E, I, H // 8):
+        raise ValueError(f"expert stacks do not match H={H}, I={I}, E={E}")
+    topk = int(topk_ids.shape[1])
+    if tuple(topk_weights.shape) != (T, topk) or tuple(topk_ids.shape) != (T, topk):
+        raise ValueError("topk_weights / topk_ids must be [T, top_k]")
+    if topk_ids.dtype not in (torch.int32, torch.int64):
+        raise TypeError("topk_ids must be int32 or int64")
+    x = x if x.stride(1) == 1 else x.contiguous()
+    topk_ids, topk_weights = topk_ids.contiguous(), topk_weights.contiguous()
+    gu_sc, dn_sc = gate_up_scales.contiguous(), down_scales.contiguous()
+    gu_qz = gate_up_qzeros.contiguous() if gate_up_qzeros is not None else None
+    dn_qz = down_qzeros.contiguous() if down_qzeros is not None else None
+    gu = prepare_moe_stream(gate_up_qweight, True)
+    dn = prepare_moe_stream(down_qweight, False)
+    if out is None:
+        out = torch.empty((T, H), dtype=x.dtype, device=dev)
+    if T == 0:
+        return out
+    ws_bytes = int(lib.awq_w4a16_moe_workspace_bytes(T, H, I, E, topk))
+    ws = WORKSPACE.get(dev, ws_bytes, key="moe")
+    rc = lib.awq_w4a16_moe(
+        _ptr(x), int(x.stride(0)), _ptr(topk_ids), 64 if topk_ids.dtype == torch.int64 else 32,
+        _ptr(topk_weights), dtype_code(topk_weights.dtype), _ptr(gu), _ptr(gu_sc), _ptr(gu_qz), _ptr(dn),
+        _ptr(dn_sc), _ptr(dn_qz), _ptr(out), int(out.stride(0)), T, H, I, E, topk, int(group_size), act,
+        dtype_code(x.dtype), dtype_code(gu_sc.dtype), _ptr(ws), ws_bytes, _stream_ptr(dev))
+    L.check("awq_w4a16_moe", rc)
+    return out

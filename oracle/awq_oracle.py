@@ -220,3 +220,53 @@ def error_report(y, y_ref, y_exact=None, ulp_floor=1.0):
         e = np.asarray(y_exact, dtype=np.float64)
         rep["max_ulp_vs_exact"] = float((np.abs(y - e) / fp16_ulp(e, ulp_floor)).max()) if d.size else 0.0
     return rep
+
+
+def moe_act(g: np.ndarray, activation: str = "silu") -> np.ndarray:
+    """Gate activation of the grouped MoE kernels in float64
+    (``vllm/kernels/triton/gemma4_moe_int4.py:748-756``): silu ``g / (1 + e^-g)``, or the
+    tanh-form GELU ``g / (1 + e^(-2 * 0.79788456 (g + 0.044715 g^3)))``."""
+    g = np.asarray(g, dtype=np.float64)
+    if str(activation).lower() in ("gelu", "gelu_pytorch_tanh"):
+        inner = 0.7978845608028654 * (g + 0.044715 * g * g * g)
+        return g / (1.0 + np.exp(-2.0 * inner))
+    return g / (1.0 + np.exp(-g))
+
+
+def moe_grouped_exact(x_f16, topk_weights, topk_ids, w1, w2, activation="silu", inter_dtype="float16"):
+    """Grouped MoE with the rounding points of the reference's grouped int4 path
+    (``gemma4_moe_int4.py:686-760``: gate and up summed in fp32, ``act(gate) * up *
+    route_weight`` stored in x.dtype; ``894-1030``: the down products of every route of a
+    token summed in fp32, one cast at the end):
+
+    * ``w1 [E, 2I, H]`` (rows 0..I-1 gate, I..2I-1 up) and ``w2 [E, H, I]`` are the
+      dequantized expert weights (fp16 values);
+    * gate/up and down sums are exact (float64);
+    * the intermediate is rounded once to ``inter_dtype`` (via float32 for bfloat16);
+    * the output is returned unrounded (float64);
+    * routes whose id is outside ``[0, E)`` contribute nothing.
+
+    Pinned by: agreement with the ``fused_moe`` restatement (``ref_cpu.fused_moe_cpu``, the
+    torch path) within its fp16-flow error, expert-relabelling and slot-permutation
+    invariance, and the single-expert case reducing to :func:`linear_exact` compositions.
+    """
+    x = np.asarray(x_f16, dtype=np.float64)
+    w1 = np.asarray(w1)
+    w2 = np.asarray(w2)
+    E, I = w1.shape[0], w2.shape[2]
+    ids = np.asarray(topk_ids).astype(np.int64)
+    tw = np.asarray(topk_weights, dtype=np.float64)
+    out = np.zeros((x.shape[0], w2.shape[1]), dtype=np.float64)
+    for e in np.unique(ids):
+        if e < 0 or e >= E:
+            continue
+        ts, js = np.nonzero(ids == e)
+        gu = x[ts] @ w1[e].astype(np.float64).T
+        h = moe_act(gu[:, :I], activation) * gu[:, I:] * tw[ts, js][:, None]
+        if inter_dtype == "bfloat16":
+            h = bf16_bits_to_f32(f32_to_bf16_bits(h.astype(np.float32))).astype(np.float64)
+        else:
+            h = h.astype(np.float16).astype(np.float64)
+        np.add.at(out, ts, h @ w2[e].astype(np.float64).T)
+    return out
+

@@ -51,9 +51,10 @@ CONFIGS = {
 MOE_CONFIG = dict(E=64, top_k=8, H=2048, I=1024, group_size=128, T=(16, 512))
 
 
-def make_moe_problem(T, E=64, top_k=8, H=2048, I=1024, group_size=128, seed=0):
+def make_moe_problem(T, E=64, top_k=8, H=2048, I=1024, group_size=128, seed=0, zero_point=True):
     """Per-expert AutoAWQ-packed gate_up (K=H, N=2I) and down (K=I, N=H) weights,
-    fp16 activations N(0,1) and fp16 router logits N(0,1)."""
+    fp16 activations N(0,1) and fp16 router logits N(0,1).  ``zero_point=False`` gives
+    symmetric experts (zeros None, z = 8)."""
     rng = np.random.default_rng(seed)
     g = int(group_size)
 
@@ -61,7 +62,7 @@ def make_moe_problem(T, E=64, top_k=8, H=2048, I=1024, group_size=128, seed=0):
         W = rng.integers(0, 16, size=(E, K, N), dtype=np.int32)
         Z = rng.integers(0, 16, size=(E, K // g, N), dtype=np.int32)
         S = (np.abs(rng.standard_normal((E, K // g, N), dtype=np.float32)) * 0.02 + 1e-4).astype(np.float16)
-        return pack_awq(W), pack_awq(Z), S
+        return pack_awq(W), (pack_awq(Z) if zero_point else None), S
 
     gu_q, gu_z, gu_s = expert_stack(H, 2 * I)
     dn_q, dn_z, dn_s = expert_stack(I, H)

@@ -100,3 +100,55 @@ def test_workspace_planning_is_host_only(lib):
     ws8 = lib.awq_w4a16_gemm_workspace_bytes(1, 4096, 12288, 128, 8, 0)
     assert ws1 == 0
     assert ws8 >= 8 * 1 * 4096 * 4
+
+
+def _moe_call(lib, **kw):
+    p = _fake(4096)
+    return lib.awq_w4a16_moe(
+        kw.get("x", p), kw.get("ldx", 64), kw.get("ids", p), kw.get("bits", 32), kw.get("rw", p),
+        kw.get("rw_dtype", L.DTYPE_F32), kw.get("gq", p), kw.get("gs", p), kw.get("gz", None), kw.get("dq", p),
+        kw.get("ds", p), kw.get("dz", None), kw.get("out", p), kw.get("ldo", 64), kw.get("T", 4),
+        kw.get("H", 64), kw.get("I", 32), kw.get("E", 4), kw.get("topk", 2), kw.get("G", 32),
+        kw.get("act", L.MOE_ACT_SILU), kw.get("act_dtype", L.DTYPE_F16), L.DTYPE_F16, kw.get("ws", None),
+        kw.get("ws_bytes", 0), None)
+
+
+def test_moe_rejects_bad_args_before_any_launch(lib):
+    assert _moe_call(lib, x=None) == L.ERR_NULL
+    assert _moe_call(lib, gz=_fake()) == L.ERR_NULL           # zeros for gate_up only
+    assert _moe_call(lib, act=5) == L.ERR_UNSUPPORTED
+    assert _moe_call(lib, G=256) == L.ERR_UNSUPPORTED
+    assert _moe_call(lib, bits=16) == L.ERR_UNSUPPORTED
+    assert _moe_call(lib, act_dtype=L.DTYPE_F32) == L.ERR_UNSUPPORTED
+    assert _moe_call(lib, I=48) == L.ERR_SHAPE                 # I % G
+    assert _moe_call(lib, ldx=32) == L.ERR_STRIDE
+    assert _moe_call(lib, T=-1) == L.ERR_SHAPE
+    assert _moe_call(lib, T=0) == L.OK                         # nothing to do
+    # a real workspace pointer, too small
+    assert _moe_call(lib, ws=_fake(256), ws_bytes=256) == L.ERR_WORKSPACE
+
+
+def test_moe_sizes_are_host_only(lib):
+    # config 4: E = 64, H = 2048, I = 1024 -> 16 tiles per expert for both stacks
+    assert lib.awq_w4a16_moe_stream_bytes(64, 2048, 2048, 1) == 64 * 16 * (2048 // 32) * 2048
+    assert lib.awq_w4a16_moe_stream_bytes(64, 1024, 2048, 0) == 64 * 16 * (1024 // 32) * 2048
+    # the stream copy is exactly the size of the packed stack when the tiles are full
+    assert lib.awq_w4a16_moe_stream_bytes(64, 2048, 2048, 1) == 64 * 2048 * 2048 // 2
+    assert lib.awq_w4a16_moe_stream_bytes(1, 30, 64, 0) == 0   # K % 32
+    R, H, I = 512 * 8, 2048, 1024
+    ws = lib.awq_w4a16_moe_workspace_bytes(512, H, I, 64, 8)
+    assert ws >= R * I * 2 + R * H * 4 + 64 * R * 4
+    assert ws < R * I * 2 + R * H * 4 + 64 * R * 4 + 4096
+
+
+def test_moe_route_rejects_bad_args(lib):
+    p = _fake()
+    r = lambda **kw: lib.awq_w4a16_moe_route(
+        kw.get("lg", p), kw.get("ld", 8), kw.get("dt", L.DTYPE_F16), kw.get("T", 2), kw.get("E", 8),
+        kw.get("k", 2), 1, kw.get("w", p), kw.get("ids", p), None)
+    assert r(lg=None) == L.ERR_NULL
+    assert r(E=300) == L.ERR_SHAPE
+    assert r(k=9) == L.ERR_SHAPE
+    assert r(ld=4) == L.ERR_STRIDE
+    assert r(dt=9) == L.ERR_UNSUPPORTED
+    assert r(T=0) == L.OK

@@ -1,0 +1,202 @@
+"""GPU parity of the grouped AWQ MoE path (routing, gate_up + activation, down, combine)
+against the CPU oracle: ``oracle.awq_oracle.moe_grouped_exact`` (float64 sums, the
+intermediate rounded once, the reference grouped kernel's rounding points) and the
+``fused_moe`` restatement (``oracle.ref_cpu.fused_moe_cpu``).
+
+Bar: the kernel's output within 4 fp16 ulps (ulps at max(|y|, RMS(y))) of the exact oracle
+and mean relative error <= 2e-4; bitwise reproducible across calls.  The intermediate is
+rounded to fp16 (the reference keeps it in x.dtype), so a float32 gate/up sum that differs
+from the exact one in its last bits can land an intermediate value one fp16 ulp away from the
+oracle's; that ulp times its down weight moves an output by up to a few ulps (e.g. h = 9.15
+vs 9.14 with weight 0.593: 2.4 ulps at the RMS scale -- reproduced bit for bit by a float32
+emulation of the kernel's arithmetic on the CPU).  The mean error stays at the output
+rounding's level.
+"""
+import numpy as np
+import pytest
+import torch
+
+from litevllm_amd import moe as MOE
+from litevllm_amd import ops
+from oracle import awq_oracle as O
+from oracle import ref_cpu as R
+from oracle.gen import make_moe_problem
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _dev(a):
+    return None if a is None else torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _problem(T, E, H, I, topk, G, zp=True, seed=0):
+    p = make_moe_problem(T, E=E, top_k=topk, H=H, I=I, group_size=G, seed=seed, zero_point=zp)
+    gq, gz, gs = p["gate_up"]
+    dq, dz, ds = p["down"]
+    return p, dict(gq=_dev(gq), gz=_dev(gz), gs=_dev(gs), dq=_dev(dq), dz=_dev(dz), ds=_dev(ds))
+
+
+def _dense_experts(d, G):
+    """Dequantized stacks in the oracle's orientation, w1 [E, 2I, H], w2 [E, H, I] (fp16), from
+    the device dequant kernel, which is bit-exact against the oracle's dequant."""
+    E = d["gq"].shape[0]
+    w1 = torch.stack([ops.dequant(d["gq"][e], d["gs"][e], None if d["gz"] is None else d["gz"][e], G,
+                                  layout="autoawq").t() for e in range(E)])
+    w2 = torch.stack([ops.dequant(d["dq"][e], d["ds"][e], None if d["dz"] is None else d["dz"][e], G,
+                                  layout="autoawq").t() for e in range(E)])
+    return w1.cpu().numpy(), w2.cpu().numpy()
+
+
+def _route_cpu(logits, topk):
+    p = torch.softmax(logits.float(), dim=-1)
+    w, i = torch.topk(p, topk, dim=-1)
+    return w / w.sum(-1, keepdim=True).clamp_min(1e-8), i
+
+
+def _check(y, exact, what):
+    floor = float(np.sqrt(np.mean(exact ** 2)))
+    rep = O.error_report(y, exact, ulp_floor=floor)
+    print(what, rep, flush=True)
+    assert rep["max_ulp"] <= 4.0 and rep["mean_rel"] <= 2e-4, (what, rep)
+
+
+def test_dequant_matches_oracle_for_expert_slices():
+    # the full-size tests below take the dense experts from the device dequant; pin it here
+    p, d = _problem(2, 3, 256, 128, 2, 64, seed=1)
+    gq, gz, gs = p["gate_up"]
+    for e in range(3):
+        w = ops.dequant(d["gq"][e], d["gs"][e], d["gz"][e], 64, layout="autoawq").cpu().numpy()
+        ref = O.dequant_awq(gq[e], gs[e], gz[e], 64)
+        assert np.array_equal(w.view(np.uint16), ref.view(np.uint16))
+
+
+@pytest.mark.parametrize("T,E,topk", [(1, 8, 2), (37, 64, 8), (300, 16, 4)])
+def test_route_matches_fp32_torch(T, E, topk):
+    g = torch.Generator().manual_seed(T)
+    logits = torch.randn(T, E, generator=g).half()
+    w, ids = ops.moe_route(logits.to(DEV), topk)
+    wr, ir = _route_cpu(logits, topk)
+    assert torch.equal(ids.cpu().long(), ir)
+    assert torch.allclose(w.cpu(), wr, rtol=2e-6, atol=1e-7)
+    # weights of a token sum to one
+    assert torch.allclose(w.sum(-1).cpu(), torch.ones(T), atol=1e-6)
+
+
+def test_route_ties_pick_lower_expert():
+    logits = torch.zeros(3, 16, dtype=torch.float16)
+    w, ids = ops.moe_route(logits.to(DEV), 4)
+    assert ids.cpu().tolist() == [[0, 1, 2, 3]] * 3
+    assert torch.allclose(w.cpu(), torch.full((3, 4), 0.25))
+
+
+CASES = [
+    # T, E, H, I, topk, G, zero point, activation
+    (1, 4, 128, 64, 2, 32, True, "silu"),
+    (6, 8, 256, 128, 2, 64, False, "silu"),
+    (16, 64, 512, 256, 8, 128, True, "silu"),
+    (100, 8, 256, 128, 2, 128, True, "gelu_pytorch_tanh"),   # ~25 routes per expert
+    (200, 4, 256, 160, 2, 32, True, "silu"),                # ~100 routes per expert, I % 64 != 0
+]
+
+
+@pytest.mark.parametrize("T,E,H,I,topk,G,zp,act", CASES)
+def test_moe_vs_exact_oracle(T, E, H, I, topk, G, zp, act):
+    p, d = _problem(T, E, H, I, topk, G, zp, seed=T + E)
+    logits = torch.from_numpy(p["logits"])
+    tw, tid = _route_cpu(logits, topk)
+    x = _dev(p["x"])
+    y = ops.moe(x, tw.to(DEV), tid.to(DEV), d["gq"], d["gs"], d["gz"], d["dq"], d["ds"], d["dz"], G, act)
+    y2 = ops.moe(x, tw.to(DEV), tid.to(DEV), d["gq"], d["gs"], d["gz"], d["dq"], d["ds"], d["dz"], G, act)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2), "not bitwise reproducible"
+    w1, w2 = _dense_experts(d, G)
+    exact = O.moe_grouped_exact(p["x"], tw.numpy(), tid.numpy(), w1, w2, activation=act)
+    _check(y.cpu().numpy(), exact, f"T={T} E={E} H={H} I={I} k={topk} G={G} zp={zp} {act}")
+
+
+def test_moe_skewed_routing_multiple_passes():
+    # every route on two experts: 600 rows per expert -> several wave-group passes
+    T, E, H, I, topk, G = 600, 8, 256, 128, 2, 128
+    p, d = _problem(T, E, H, I, topk, G, seed=5)
+    tid = torch.tensor([[3, 6]] * T, dtype=torch.int64)
+    tw = torch.rand(T, topk, generator=torch.Generator().manual_seed(0))
+    y = ops.moe(_dev(p["x"]), tw.to(DEV), tid.to(DEV), d["gq"], d["gs"], d["gz"], d["dq"], d["ds"], d["dz"], G)
+    w1, w2 = _dense_experts(d, G)
+    exact = O.moe_grouped_exact(p["x"], tw.numpy(), tid.numpy(), w1, w2)
+    _check(y.cpu().numpy(), exact, "skewed")
+
+
+def test_moe_bf16_activations_and_out_of_range_ids():
+    T, E, H, I, topk, G = 20, 8, 256, 128, 3, 64
+    p, d = _problem(T, E, H, I, topk, G, seed=6)
+    tw, tid = _route_cpu(torch.from_numpy(p["logits"]), topk)
+    tid = tid.clone()
+    tid[::4, 1] = E + 3  # ignored routes
+    xb = torch.from_numpy(p["x"]).float().bfloat16()
+    y = ops.moe(xb.to(DEV), tw.to(DEV), tid.to(DEV), d["gq"], d["gs"], d["gz"], d["dq"], d["ds"], d["dz"], G)
+    # bf16 activations: weights dequantized to bf16 (one rounding of (q - z) * s)
+    gq, gz, gs = p["gate_up"]
+    dq, dz, ds = p["down"]
+    bf = lambda q, s, z: O.bf16_bits_to_f32(O.dequant_awq(q, s, z, G, out_dtype="bfloat16")).T
+    w1b = np.stack([bf(gq[e], gs[e], gz[e]) for e in range(E)])
+    w2b = np.stack([bf(dq[e], ds[e], dz[e]) for e in range(E)])
+    xf = xb.float().numpy()
+    exact = O.moe_grouped_exact(xf, tw.numpy(), tid.numpy(), w1b, w2b, inter_dtype="bfloat16")
+    yf = y.float().cpu().numpy()
+    floor = float(np.sqrt(np.mean(exact ** 2)))
+    d_ = np.abs(yf - exact)
+    # bf16 output: one bf16 ulp is 8 fp16 ulps
+    assert np.max(d_ / O.fp16_ulp(exact, floor)) <= 16.0
+    assert d_.sum() / np.abs(exact).sum() <= 2e-3
+
+
+def test_gemma4_grouped_surface_ref_layout_with_zeros():
+    T, E, H, I, topk, G = 24, 8, 256, 256, 2, 32
+    p, d = _problem(T, E, H, I, topk, G, seed=7)
+    tw, tid = _route_cpu(torch.from_numpy(p["logits"]), topk)
+    gq, gz, gs = p["gate_up"]
+    dq, dz, ds = p["down"]
+    ref_gu = [O.repack_awq_to_ref(gq[e], gz[e], gs[e]) for e in range(E)]
+    ref_dn = [O.repack_awq_to_ref(dq[e], dz[e], ds[e]) for e in range(E)]
+    stack = lambda lst, i: _dev(np.stack([t[i] for t in lst]))
+    out, used, reason = MOE.gemma4_moe_int4_prefill_grouped(
+        _dev(p["x"]), tw.to(DEV), tid.to(DEV), stack(ref_gu, 0), stack(ref_gu, 2), stack(ref_dn, 0),
+        stack(ref_dn, 2), intermediate_dim=I, gate_up_qzeros=stack(ref_gu, 1), down_qzeros=stack(ref_dn, 1))
+    assert used and reason == "ok", reason
+    y_awq = ops.moe(_dev(p["x"]), tw.to(DEV), tid.to(DEV), d["gq"], d["gs"], d["gz"], d["dq"], d["ds"], d["dz"], G)
+    assert torch.equal(out, y_awq)  # the repacked reference layout gives the same bits
+    out2, used2, reason2 = MOE.gemma4_moe_int4_prefill_grouped(
+        _dev(p["x"]), tw.to(DEV), tid.to(DEV), stack(ref_gu, 0), stack(ref_gu, 2), stack(ref_dn, 0),
+        stack(ref_dn, 2), intermediate_dim=I, block_i_override=48)
+    assert not used2 and reason2 == "invalid_prefill_grouped_tile"
+
+
+def test_fused_moe_surface_against_reference_port():
+    T, E, H, I, topk, G = 40, 16, 256, 128, 4, 64
+    p, d = _problem(T, E, H, I, topk, G, seed=8)
+    logits = torch.from_numpy(p["logits"])
+    w1 = MOE.AWQExperts(d["gq"], d["gs"], d["gz"], G, layout="autoawq")
+    w2 = MOE.AWQExperts(d["dq"], d["ds"], d["dz"], G, layout="autoawq")
+    y = MOE.fused_moe(_dev(p["x"]), w1, w2, logits.to(DEV), topk).cpu()
+    w1d, w2d = _dense_experts(d, G)
+    tw, tid = _route_cpu(logits, topk)
+    port = R.fused_moe_cpu(torch.from_numpy(p["x"]), torch.from_numpy(w1d), torch.from_numpy(w2d),
+                           topk_weights=tw.half(), topk_ids=tid).double().numpy()
+    exact = O.moe_grouped_exact(p["x"], tw.numpy(), tid.numpy(), w1d, w2d)
+    _check(y.numpy(), exact, "fused_moe")
+    floor = float(np.sqrt(np.mean(exact ** 2)))
+    # the port's fp16 intermediates and accumulation: a few ulps from both
+    assert np.max(np.abs(y.double().numpy() - port) / O.fp16_ulp(exact, floor)) <= 10.0
+
+
+@pytest.mark.parametrize("T", [16, 512])
+def test_config4_full_size(T):
+    """BASELINE config 4 at its real shape: E=64, top-8, H=2048, I=1024, g=128, zero points."""
+    E, H, I, topk, G = 64, 2048, 1024, 8, 128
+    p, d = _problem(T, E, H, I, topk, G, seed=40 + T)
+    tw, tid = _route_cpu(torch.from_numpy(p["logits"]), topk)
+    y = ops.moe(_dev(p["x"]), tw.to(DEV), tid.to(DEV), d["gq"], d["gs"], d["gz"], d["dq"], d["ds"], d["dz"], G)
+    w1, w2 = _dense_experts(d, G)
+    exact = O.moe_grouped_exact(p["x"], tw.numpy(), tid.numpy(), w1, w2)
+    _check(y.cpu().numpy(), exact, f"config4 T={T}")

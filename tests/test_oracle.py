@@ -262,3 +262,63 @@ def test_fused_moe_single_expert_reduces_to_dense_mlp():
     h = torch.nn.functional.linear(x, w1[0])
     want = torch.nn.functional.linear(torch.nn.functional.silu(h[:, :I]) * h[:, I:], w2[0])
     assert torch.equal(y, want)
+
+
+# ---------------------------------------------------------------- grouped MoE oracle
+def test_moe_act_matches_library_routines():
+    g = torch.linspace(-12, 12, 2001, dtype=torch.float64)
+    assert np.allclose(O.moe_act(g.numpy(), "silu"), torch.nn.functional.silu(g).numpy(), rtol=1e-12, atol=1e-15)
+    ref = torch.nn.functional.gelu(g, approximate="tanh").numpy()
+    assert np.allclose(O.moe_act(g.numpy(), "gelu_pytorch_tanh"), ref, rtol=1e-12, atol=1e-15)
+
+
+def test_moe_grouped_exact_against_fused_moe_port():
+    T, E, H, I, topk = 40, 8, 64, 32, 3
+    x, w1, w2, logits = _moe_dense_problem(T, E, H, I, topk, seed=21)
+    tw, tid = R.moe_routing_cpu(logits, topk)
+    ported = R.fused_moe_cpu(x, w1, w2, topk_weights=tw, topk_ids=tid).double().numpy()
+    exact = O.moe_grouped_exact(x.numpy(), tw.float().numpy(), tid.numpy(), w1.numpy(), w2.numpy())
+    floor = float(np.sqrt(np.mean(exact ** 2)))
+    # the port rounds every intermediate to fp16 and accumulates in fp16: a few ulps
+    assert np.max(np.abs(ported - exact) / O.fp16_ulp(exact, floor)) <= 8.0
+    # planted mistake: gate and up halves swapped is far outside that band
+    w1_swapped = torch.cat([w1[:, I:], w1[:, :I]], dim=1)
+    bad = O.moe_grouped_exact(x.numpy(), tw.float().numpy(), tid.numpy(), w1_swapped.numpy(), w2.numpy())
+    assert np.max(np.abs(bad - exact) / O.fp16_ulp(exact, floor)) > 100.0
+
+
+def test_moe_grouped_exact_invariances():
+    T, E, H, I, topk = 24, 6, 64, 32, 3
+    x, w1, w2, logits = _moe_dense_problem(T, E, H, I, topk, seed=22)
+    tw, tid = R.moe_routing_cpu(logits, topk)
+    xs, tws, tids = x.numpy(), tw.float().numpy(), tid.numpy()
+    base = O.moe_grouped_exact(xs, tws, tids, w1.numpy(), w2.numpy())
+    # relabelling experts (ids and stacks together) changes nothing
+    perm = np.random.default_rng(3).permutation(E)
+    inv = np.argsort(perm)
+    relab = O.moe_grouped_exact(xs, tws, perm[tids], w1.numpy()[inv], w2.numpy()[inv])
+    assert np.allclose(relab, base, rtol=1e-12, atol=1e-12)
+    # permuting a token's slots (id and weight together) changes nothing
+    sp = np.random.default_rng(4).permuted(np.tile(np.arange(topk), (T, 1)), axis=1)
+    slot = O.moe_grouped_exact(xs, np.take_along_axis(tws, sp, 1), np.take_along_axis(tids, sp, 1),
+                               w1.numpy(), w2.numpy())
+    assert np.allclose(slot, base, rtol=1e-12, atol=1e-12)
+    # pairing ids with the wrong weights is caught
+    bad = O.moe_grouped_exact(xs, tws[:, ::-1], tids, w1.numpy(), w2.numpy())
+    assert not np.allclose(bad, base, rtol=1e-3)
+    # out-of-range ids contribute nothing
+    tids_oob = tids.copy()
+    tids_oob[:, 0] = E + 5
+    part = O.moe_grouped_exact(xs, tws, tids_oob, w1.numpy(), w2.numpy())
+    only0 = O.moe_grouped_exact(xs, tws[:, :1], tids[:, :1], w1.numpy(), w2.numpy())
+    assert np.allclose(part + only0, base, rtol=1e-9, atol=1e-9)
+
+
+def test_moe_grouped_exact_single_expert_is_a_dense_mlp():
+    T, E, H, I = 7, 1, 64, 32
+    x, w1, w2, _ = _moe_dense_problem(T, E, H, I, 1, seed=23)
+    ones, zeros = np.ones((T, 1), np.float32), np.zeros((T, 1), np.int64)
+    y = O.moe_grouped_exact(x.numpy(), ones, zeros, w1.numpy(), w2.numpy())
+    gu = O.linear_exact(x.numpy(), w1.numpy()[0])
+    h = (torch.nn.functional.silu(torch.from_numpy(gu[:, :I])).numpy() * gu[:, I:]).astype(np.float16)
+    assert np.allclose(y, O.linear_exact(h, w2.numpy()[0]), rtol=1e-12, atol=1e-12)
