@@ -135,7 +135,7 @@ int awq_w4a16_gemm(const void* a, int64_t lda, const int32_t* qweight, const voi
     if (!launch_decode(ga, sp, mode, seq, zp, act_dtype, scale_dtype, st)) return AWQ_ERR_UNSUPPORTED;
     return launch_status();
   }
-  if ((K % 64) != 0) return AWQ_ERR_SHAPE;
+  if ((K % 32) != 0) return AWQ_ERR_SHAPE;
   if (!launch_prefill(ga, seq, zp, act_dtype, scale_dtype, st)) return AWQ_ERR_UNSUPPORTED;
   return launch_status();
 }

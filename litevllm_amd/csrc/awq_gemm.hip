@@ -1,6 +1,18 @@
 // Prefill GEMM (M > 32) for the KN layouts (qweight [K, N/8]) on gfx950: the role of
-// _awq_native_tiled_gemm_autotuned (vllm/kernels/triton/awq_fused_gemm.py:2296-2392) with
-// the weight dequantized once per wave into MFMA operand layout.
+// _awq_native_tiled_gemm_autotuned (vllm/kernels/triton/awq_fused_gemm.py:2296-2392).
+//
+//  * Block tile 256 (M) x 128 (N), k-stages of 32, 4 waves in a 2 x 2 grid, wave tile
+//    128 x 64: 8 x 4 accumulators of v_mfma_f32_16x16x32_{f16,bf16} per wave.
+//  * Each k-stage the block copies its activation tile into LDS and dequantizes its weight
+//    tile once (every thread two packed words of two k-adjacent rows, exact (q - z) * s) into
+//    LDS as [n][k] half values, so every wave reads both MFMA operands with 16-byte LDS loads
+//    and no weight is dequantized twice in a block.
+//  * LDS is double-buffered and the next stage's global loads ride in registers, so one
+//    barrier per stage separates writing stage s + 1 from reading stage s.
+//  * 16-byte LDS chunks are XOR-swizzled by row so that operand reads and the dequant writes
+//    spread over the banks.
+//  * Blocks are dealt to the 8 XCDs so that each XCD works through contiguous tiles (the same
+//    activation row tile stays in its L2).
 #include "awq_common.h"
 #include "awq_launch.h"
 
@@ -14,194 +26,148 @@ __device__ __forceinline__ WordSZ load_sz(const GemmArgs& p, int g, int word) {
   return r;
 }
 
+// chunk swizzle of a 64-byte LDS row (four 16-byte chunks)
+__device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
 
-// Prefill GEMM kernel, KN layouts.  Block tile BM x 256, 4 waves in a 2 x 2 grid, wave tile
-// (BM/2) x 128.  A (activations) goes through LDS in 64-wide k stages (double buffered,
-// 16-byte chunks XOR-swizzled by row); each wave reads its own 16 weight words per row
-// from global memory and dequantizes them into MFMA operands in registers.
-template <int BM, bool SEQ, bool ZP, typename T, bool FAST>
-__global__ void __launch_bounds__(256) gemm_kn_kernel(const GemmArgs p, int scale_bf16,
-                                                      int tiles_m, int tiles_n) {
-  constexpr int BK = 64;
-  constexpr int WM = BM / 2;
-  constexpr int MTL = WM / 16;               // m-tiles per wave
-  constexpr int ACH = BM * BK / 8 / 256;     // 16-byte A chunks per thread per stage
+constexpr int kPBM = 256, kPBN = 128, kPBK = 32;
+
+template <bool SEQ, bool ZP, typename T, bool FAST>
+__global__ void __launch_bounds__(256, 2) prefill_kn_kernel(const GemmArgs p, int scale_bf16, int tiles_m,
+                                                           int tiles_n) {
+  constexpr int BM = kPBM, BN = kPBN, BK = kPBK;
+  constexpr int WM = 128, WN = 64;
+  constexpr int MTL = WM / 16, NTL = WN / 16;
+  constexpr int ACH = BM * BK / 8 / 256;  // 16-byte activation chunks per thread per stage
   __shared__ u32x4 lds_a[2][BM * BK / 8];
+  __shared__ u32x4 lds_b[2][BN * BK / 8];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int q = lane >> 4, r = lane & 15;
   const int wave_m = wave >> 1, wave_n = wave & 1;
 
   // XCD-aware tile order: blocks are dealt round-robin to the 8 XCDs; give each XCD a
-  // contiguous range of tiles (row-tile major) so blocks sharing an A row-tile share an L2.
+  // contiguous range of tiles (row-tile major) so blocks sharing an activation row tile
+  // share an L2.
   const int ntiles = tiles_m * tiles_n;
   int bid = blockIdx.x;
   if ((ntiles & 7) == 0) bid = (bid & 7) * (ntiles >> 3) + (bid >> 3);
   const int tm = bid / tiles_n, tn = bid - tm * tiles_n;
-  const int m0 = tm * BM, n0 = tn * 256;
+  const int m0 = tm * BM, n0 = tn * BN;
 
   const int NW = p.N >> 3;
-  const int word = (n0 >> 3) + wave_n * 16 + r;
-  const bool wvalid = word < NW;
-  const int wld = wvalid ? word : 0;
+  // dequant assignment: packed word bw of the tile, k-rows 2 rp and 2 rp + 1 of the stage
+  const int bw = tid & 15, rp = tid >> 4;
+  const int bword = (n0 >> 3) + bw;
+  const int bwld = bword < NW ? bword : NW - 1;  // columns past N are computed, never stored
 
-  f32x4 acc[MTL][8];
+  f32x4 acc[MTL][NTL];
 #pragma unroll
   for (int mt = 0; mt < MTL; ++mt)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[mt][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int nt = 0; nt < NTL; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int nst = p.K / BK;
-  u32x4 areg[ACH];
-  auto load_a = [&](int st) {
-#pragma unroll
-    for (int i = 0; i < ACH; ++i) {
-      const int c = tid + 256 * i;
-      const int row = c >> 3, ch = c & 7;
-      const int gr = min(m0 + row, p.M - 1);
-      areg[i] = *(const u32x4*)(p.a + (int64_t)gr * p.lda + st * BK + ch * 8);
-    }
-  };
-  auto store_a = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < ACH; ++i) {
-      const int c = tid + 256 * i;
-      const int row = c >> 3, ch = c & 7;
-      lds_a[buf][row * 8 + (ch ^ (row & 7))] = areg[i];
-    }
-  };
-  uint32_t braw[2][8];
-  WordSZ bsz[2];
-  auto load_b = [&](int st, uint32_t (&dst)[2][8], WordSZ (&szd)[2]) {
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        dst[sub][j] = __builtin_nontemporal_load(p.qw + (int64_t)(st * BK + sub * 32 + 8 * q + j) * NW + wld);
-      szd[sub] = load_sz<ZP>(p, (st * BK + sub * 32) / p.G, wld);
-    }
-  };
-
-  ColConst cc[8];
-  int cur_g = -1;
   const MagicK mk = magic_consts();
+  u32x4 areg[ACH];
+  uint32_t b0, b1;
+  WordSZ bsz;
+  auto load = [&](int s) {
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      const int c = tid + 256 * i;
+      const int row = c >> 2, ch = c & 3;
+      const int gr = min(m0 + row, p.M - 1);
+      areg[i] = *(const u32x4*)(p.a + (int64_t)gr * p.lda + s * BK + ch * 8);
+    }
+    const int64_t k = (int64_t)s * BK + 2 * rp;
+    b0 = __builtin_nontemporal_load(p.qw + k * NW + bwld);
+    b1 = __builtin_nontemporal_load(p.qw + (k + 1) * NW + bwld);
+    bsz = load_sz<ZP>(p, (s * BK) / p.G, bwld);
+  };
+  auto write = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < ACH; ++i) {
+      const int c = tid + 256 * i;
+      const int row = c >> 2, ch = c & 3;
+      lds_a[buf][row * 4 + (ch ^ swz(row))] = areg[i];
+    }
+    ColConst cc[8];
+    prep_consts<SEQ, FAST>(bsz, scale_bf16 != 0, cc);
+    const uint32_t lo = pair_lo(b0, b1), hi = pair_hi(b0, b1);
+    uint32_t* const lb = (uint32_t*)lds_b[buf];
+#define AWQ_PF_NIB(I)                                                                      \
+    {                                                                                      \
+      const uint32_t v = deq2<FAST, T>(magic_bits<(I) & 3>((I) < 4 ? lo : hi, mk), cc[I]); \
+      const int n = 8 * bw + nib_col<SEQ>(I);                                              \
+      lb[(n * 4 + ((rp >> 2) ^ swz(n))) * 4 + (rp & 3)] = v;                               \
+    }
+    AWQ_PF_NIB(0) AWQ_PF_NIB(1) AWQ_PF_NIB(2) AWQ_PF_NIB(3)
+    AWQ_PF_NIB(4) AWQ_PF_NIB(5) AWQ_PF_NIB(6) AWQ_PF_NIB(7)
+#undef AWQ_PF_NIB
+  };
+  auto compute = [&](int buf) {
+    u32x4 bf[NTL];
+#pragma unroll
+    for (int nt = 0; nt < NTL; ++nt) {
+      const int n = wave_n * WN + nt * 16 + r;
+      bf[nt] = lds_b[buf][n * 4 + (q ^ swz(n))];
+    }
+#pragma unroll
+    for (int mt = 0; mt < MTL; ++mt) {
+      const int row = wave_m * WM + mt * 16 + r;
+      const u32x4 af = lds_a[buf][row * 4 + (q ^ swz(row))];
+#pragma unroll
+      for (int nt = 0; nt < NTL; ++nt) acc[mt][nt] = MfmaOp<T>::run(af, bf[nt], acc[mt][nt]);
+    }
+  };
 
-  load_a(0);
-  store_a(0);
-  load_b(0, braw, bsz);
+  load(0);
+  write(0);
+  if (nst > 1) load(1);
   __syncthreads();
-
-  for (int st = 0; st < nst; ++st) {
-    const int buf = st & 1;
-    uint32_t bnext[2][8];
-    WordSZ sznext[2];
-    if (st + 1 < nst) {
-      load_a(st + 1);
-      load_b(st + 1, bnext, sznext);
-    }
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      const int g = (st * BK + sub * 32) / p.G;
-      if (g != cur_g) {
-        cur_g = g;
-        prep_consts<SEQ, FAST>(bsz[sub], scale_bf16 != 0, cc);
-      }
-      u32x4 af[MTL];
-#pragma unroll
-      for (int mt = 0; mt < MTL; ++mt) {
-        const int row = wave_m * WM + mt * 16 + r;
-        const int ch = sub * 4 + q;
-        af[mt] = lds_a[buf][row * 8 + (ch ^ (row & 7))];
-      }
-      uint32_t mlo[4], mhi[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        mlo[u] = pair_lo(braw[sub][2 * u], braw[sub][2 * u + 1]);
-        mhi[u] = pair_hi(braw[sub][2 * u], braw[sub][2 * u + 1]);
-      }
-#define AWQ_GEMM_NIB(I)                                                          \
-      {                                                                          \
-        const u32x4 bop = rows_operand<I, FAST, T>(mlo, mhi, cc[I], mk);         \
-        _Pragma("unroll") for (int mt = 0; mt < MTL; ++mt)                       \
-            acc[mt][I] = MfmaOp<T>::run(af[mt], bop, acc[mt][I]);                \
-      }
-      AWQ_GEMM_NIB(0) AWQ_GEMM_NIB(1) AWQ_GEMM_NIB(2) AWQ_GEMM_NIB(3)
-      AWQ_GEMM_NIB(4) AWQ_GEMM_NIB(5) AWQ_GEMM_NIB(6) AWQ_GEMM_NIB(7)
-#undef AWQ_GEMM_NIB
-    }
-    if (st + 1 < nst) {
-      store_a(buf ^ 1);
-#pragma unroll
-      for (int sub = 0; sub < 2; ++sub) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) braw[sub][j] = bnext[sub][j];
-        bsz[sub] = sznext[sub];
-      }
-    }
+  for (int s = 0; s < nst; ++s) {
+    compute(s & 1);
+    if (s + 1 < nst) write((s + 1) & 1);
+    if (s + 2 < nst) load(s + 2);
     __syncthreads();
   }
 
-  // lane (q, r) holds acc[mt][i][v] = C[row m0 + wave_m*WM + mt*16 + 4q + v][8*word + nib_col(i)]
-  if (!wvalid) return;
-  float bv[8];
+  // lane (q, r) holds acc[mt][nt][v] = C[m0 + wave_m*WM + mt*16 + 4q + v][n0 + wave_n*WN + nt*16 + r]
 #pragma unroll
-  for (int c = 0; c < 8; ++c) bv[c] = p.bias ? load_bias(p.bias, p.bias_dtype, 8 * word + c) : 0.0f;
+  for (int nt = 0; nt < NTL; ++nt) {
+    const int col = n0 + wave_n * WN + nt * 16 + r;
+    if (col >= p.N) continue;
+    const float bv = p.bias ? load_bias(p.bias, p.bias_dtype, col) : 0.0f;
 #pragma unroll
-  for (int mt = 0; mt < MTL; ++mt) {
+    for (int mt = 0; mt < MTL; ++mt) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int row = m0 + wave_m * WM + mt * 16 + 4 * q + v;
-      if (row >= p.M) continue;
-      float o[8];
-#pragma unroll
-      for (int c = 0; c < 8; ++c) o[c] = acc[mt][col_nib<SEQ>(c)][v] + bv[c];
-      u32x4 st;
-      st[0] = pack2<T>(o[0], o[1]);
-      st[1] = pack2<T>(o[2], o[3]);
-      st[2] = pack2<T>(o[4], o[5]);
-      st[3] = pack2<T>(o[6], o[7]);
-      *(u32x4*)(p.c + (int64_t)row * p.ldc + 8 * word) = st;
+      for (int v = 0; v < 4; ++v) {
+        const int row = m0 + wave_m * WM + mt * 16 + 4 * q + v;
+        if (row < p.M) p.c[(int64_t)row * p.ldc + col] = to_bits<T>(acc[mt][nt][v] + bv);
+      }
     }
   }
 }
-
 
 }  // namespace awq
 
 namespace awq_host {
 using namespace awq;
 
-template <int BM, bool SEQ, bool ZP, typename T, bool FAST>
-static void launch_gemm_t(const GemmArgs& a, int sbf, hipStream_t st) {
-  const int tm = (int)cdiv(a.M, BM), tn = (int)cdiv(a.N, 256);
-  hipLaunchKernelGGL((gemm_kn_kernel<BM, SEQ, ZP, T, FAST>), dim3(tm * tn), dim3(256), 0, st, a,
-                     sbf, tm, tn);
-}
-
-static int pick_bm(int64_t M, int64_t N) {
-  const int64_t slots = num_cus();
-  auto fill = [&](int64_t bm) {
-    const int64_t blocks = cdiv(M, bm) * cdiv(N, 256);
-    return (double)blocks / ((double)cdiv(blocks, slots) * (double)slots);
-  };
-  if (M >= 256 && fill(256) >= 0.99 * fill(128)) return 256;
-  return 128;
-}
-
 template <bool SEQ, bool ZP, typename T, bool FAST>
-static void launch_gemm_sel(const GemmArgs& a, int sbf, hipStream_t st) {
-  if (pick_bm(a.M, a.N) == 256) launch_gemm_t<256, SEQ, ZP, T, FAST>(a, sbf, st);
-  else launch_gemm_t<128, SEQ, ZP, T, FAST>(a, sbf, st);
+static void launch_prefill_t(const GemmArgs& a, int sbf, hipStream_t st) {
+  const int tm = (int)cdiv(a.M, kPBM), tn = (int)cdiv(a.N, kPBN);
+  hipLaunchKernelGGL((prefill_kn_kernel<SEQ, ZP, T, FAST>), dim3(tm * tn), dim3(256), 0, st, a, sbf, tm, tn);
 }
 
 template <bool SEQ, bool ZP>
 static void dispatch(const GemmArgs& a, int act, int sdt, hipStream_t st) {
   const int sbf = (sdt == AWQ_DTYPE_BF16) ? 1 : 0;
   if (act == AWQ_DTYPE_F16) {
-    if (sdt == AWQ_DTYPE_F16) launch_gemm_sel<SEQ, ZP, f16, true>(a, sbf, st);
-    else launch_gemm_sel<SEQ, ZP, f16, false>(a, sbf, st);
+    if (sdt == AWQ_DTYPE_F16) launch_prefill_t<SEQ, ZP, f16, true>(a, sbf, st);
+    else launch_prefill_t<SEQ, ZP, f16, false>(a, sbf, st);
   } else {
-    launch_gemm_sel<SEQ, ZP, bf16, false>(a, sbf, st);
+    launch_prefill_t<SEQ, ZP, bf16, false>(a, sbf, st);
   }
 }
 
