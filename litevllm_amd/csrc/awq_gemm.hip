@@ -1,8 +1,9 @@
 // Prefill GEMM (M > 32) for the KN layouts (qweight [K, N/8]) on gfx950: the role of
 // _awq_native_tiled_gemm_autotuned (vllm/kernels/triton/awq_fused_gemm.py:2296-2392).
 //
-//  * Block tile 256 (M) x 128 (N), k-stages of 32, 4 waves in a 2 x 2 grid, wave tile
-//    128 x 64: 8 x 4 accumulators of v_mfma_f32_16x16x32_{f16,bf16} per wave.
+//  * Block tile 256 (M) x 64 NWN (N), k-stages of 32, 2 x NWN waves, wave tile 128 x 64:
+//    8 x 4 accumulators of v_mfma_f32_16x16x32_{f16,bf16} per wave.  NWN = 4 (256 columns,
+//    one 512-thread block per CU) halves the activation traffic per flop of NWN = 2.
 //  * Each k-stage the block copies its activation tile into LDS and dequantizes its weight
 //    tile once (every thread two packed words of two k-adjacent rows, exact (q - z) * s) into
 //    LDS as [n][k] half values, so every wave reads both MFMA operands with 16-byte LDS loads
@@ -29,21 +30,23 @@ __device__ __forceinline__ WordSZ load_sz(const GemmArgs& p, int g, int word) {
 // chunk swizzle of a 64-byte LDS row (four 16-byte chunks)
 __device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
 
-constexpr int kPBM = 256, kPBN = 128, kPBK = 32;
+constexpr int kPBM = 256, kPBK = 32;
 
-template <bool SEQ, bool ZP, typename T, bool FAST>
-__global__ void __launch_bounds__(256, 2) prefill_kn_kernel(const GemmArgs p, int scale_bf16, int tiles_m,
-                                                           int tiles_n) {
-  constexpr int BM = kPBM, BN = kPBN, BK = kPBK;
+template <int NWN, bool SEQ, bool ZP, typename T, bool FAST>
+__global__ void __launch_bounds__(128 * NWN, 2) prefill_kn_kernel(const GemmArgs p, int scale_bf16, int tiles_m,
+                                                               int tiles_n) {
+  constexpr int NT = 128 * NWN;  // threads
+  constexpr int BM = kPBM, BN = 64 * NWN, BK = kPBK;
   constexpr int WM = 128, WN = 64;
   constexpr int MTL = WM / 16, NTL = WN / 16;
-  constexpr int ACH = BM * BK / 8 / 256;  // 16-byte activation chunks per thread per stage
+  constexpr int ACH = BM * BK / 8 / NT;  // 16-byte activation chunks per thread per stage
+  constexpr int BW = BN / 8;             // packed words per row of the tile
   __shared__ u32x4 lds_a[2][BM * BK / 8];
   __shared__ u32x4 lds_b[2][BN * BK / 8];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int q = lane >> 4, r = lane & 15;
-  const int wave_m = wave >> 1, wave_n = wave & 1;
+  const int wave_m = wave / NWN, wave_n = wave % NWN;
 
   // XCD-aware tile order: blocks are dealt round-robin to the 8 XCDs; give each XCD a
   // contiguous range of tiles (row-tile major) so blocks sharing an activation row tile
@@ -56,7 +59,7 @@ __global__ void __launch_bounds__(256, 2) prefill_kn_kernel(const GemmArgs p, in
 
   const int NW = p.N >> 3;
   // dequant assignment: packed word bw of the tile, k-rows 2 rp and 2 rp + 1 of the stage
-  const int bw = tid & 15, rp = tid >> 4;
+  const int bw = tid % BW, rp = tid / BW;
   const int bword = (n0 >> 3) + bw;
   const int bwld = bword < NW ? bword : NW - 1;  // columns past N are computed, never stored
 
@@ -74,7 +77,7 @@ __global__ void __launch_bounds__(256, 2) prefill_kn_kernel(const GemmArgs p, in
   auto load = [&](int s) {
 #pragma unroll
     for (int i = 0; i < ACH; ++i) {
-      const int c = tid + 256 * i;
+      const int c = tid + NT * i;
       const int row = c >> 2, ch = c & 3;
       const int gr = min(m0 + row, p.M - 1);
       areg[i] = *(const u32x4*)(p.a + (int64_t)gr * p.lda + s * BK + ch * 8);
@@ -87,7 +90,7 @@ __global__ void __launch_bounds__(256, 2) prefill_kn_kernel(const GemmArgs p, in
   auto write = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < ACH; ++i) {
-      const int c = tid + 256 * i;
+      const int c = tid + NT * i;
       const int row = c >> 2, ch = c & 3;
       lds_a[buf][row * 4 + (ch ^ swz(row))] = areg[i];
     }
@@ -154,10 +157,17 @@ __global__ void __launch_bounds__(256, 2) prefill_kn_kernel(const GemmArgs p, in
 namespace awq_host {
 using namespace awq;
 
+// 256-column tiles unless that leaves a CU without a block
 template <bool SEQ, bool ZP, typename T, bool FAST>
 static void launch_prefill_t(const GemmArgs& a, int sbf, hipStream_t st) {
-  const int tm = (int)cdiv(a.M, kPBM), tn = (int)cdiv(a.N, kPBN);
-  hipLaunchKernelGGL((prefill_kn_kernel<SEQ, ZP, T, FAST>), dim3(tm * tn), dim3(256), 0, st, a, sbf, tm, tn);
+  const int tm = (int)cdiv(a.M, kPBM);
+  const int tn4 = (int)cdiv(a.N, 256);
+  if ((int64_t)tm * tn4 >= num_cus()) {
+    hipLaunchKernelGGL((prefill_kn_kernel<4, SEQ, ZP, T, FAST>), dim3(tm * tn4), dim3(512), 0, st, a, sbf, tm, tn4);
+  } else {
+    const int tn2 = (int)cdiv(a.N, 128);
+    hipLaunchKernelGGL((prefill_kn_kernel<2, SEQ, ZP, T, FAST>), dim3(tm * tn2), dim3(256), 0, st, a, sbf, tm, tn2);
+  }
 }
 
 template <bool SEQ, bool ZP>
