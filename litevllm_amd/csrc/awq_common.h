@@ -183,6 +183,23 @@ __device__ __forceinline__ void prep_consts(const WordSZ& sz, bool scale_bf16, C
   }
 }
 
+// Constants of nibble I alone (as prep_consts computes them for all eight).
+template <int I, bool SEQ, bool FAST>
+__device__ __forceinline__ ColConst prep_const(const WordSZ& sz, bool scale_bf16) {
+  constexpr int c = nib_col<SEQ>(I);
+  const uint32_t sbits = (sz.s4[c >> 1] >> (16 * (c & 1))) & 0xFFFFu;
+  ColConst cc;
+  cc.zm = zero_magic(I & 1, (sz.zw >> (4 * I)) & 0xF);
+  if constexpr (FAST) {
+    cc.sc = sbits * 0x00010001u;
+    cc.scf = 0.0f;
+  } else {
+    cc.sc = 0;
+    cc.scf = scale_bf16 ? bf_bits2f((uint16_t)sbits) : h_bits2f((uint16_t)sbits);
+  }
+  return cc;
+}
+
 // Row pairing with one byte permute: lo16(w0) | lo16(w1) << 16 and hi16(w0) | hi16(w1) << 16.
 // (v_perm_b32 selects bytes 0-3 from its second operand and 4-7 from its first.)
 __device__ __forceinline__ uint32_t pair_lo(uint32_t w0, uint32_t w1) {

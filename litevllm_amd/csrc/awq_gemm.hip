@@ -1,7 +1,7 @@
 // Prefill GEMM (M > 32) for the KN layouts (qweight [K, N/8]) on gfx950: the role of
 // _awq_native_tiled_gemm_autotuned (vllm/kernels/triton/awq_fused_gemm.py:2296-2392).
 //
-//  * Block tile 256 (M) x 64 NWN (N), k-stages of 32, 2 x NWN waves, wave tile 128 x 64:
+//  * Block tile 256 (M) x 64 NWN (N), k-stages of 64, 2 x NWN waves, wave tile 128 x 64:
 //    8 x 4 accumulators of v_mfma_f32_16x16x32_{f16,bf16} per wave.  NWN = 4 (256 columns,
 //    one 512-thread block per CU) halves the activation traffic per flop of NWN = 2.
 //  * Each k-stage the block copies its activation tile into LDS and dequantizes its weight
@@ -27,22 +27,29 @@ __device__ __forceinline__ WordSZ load_sz(const GemmArgs& p, int g, int word) {
   return r;
 }
 
-// chunk swizzle of a 64-byte LDS row (four 16-byte chunks)
-__device__ __forceinline__ int swz(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+// 16-byte chunk swizzles of 128-byte LDS rows (eight chunks).  Operand reads take 16
+// consecutive rows; activation rows are stored whole, weight rows n = 8 w + c by lanes of
+// neighbouring words w.  swz_a depends on the row's low bits only, so the A fragments of a
+// wave sit at constant offsets from one lane address; swz_b also mixes in the word index so
+// the dequant stores spread over the banks.
+__device__ __forceinline__ int swz_a(int row) { return row & 7; }
+__device__ __forceinline__ int swz_b(int n) { return (n ^ (n >> 4)) & 7; }
 
-constexpr int kPBM = 256, kPBK = 32;
+constexpr int kPBM = 256, kPBK = 64;
 
 template <int NWN, bool SEQ, bool ZP, typename T, bool FAST>
 __global__ void __launch_bounds__(128 * NWN, 2) prefill_kn_kernel(const GemmArgs p, int scale_bf16, int tiles_m,
-                                                               int tiles_n) {
+                                                                  int tiles_n) {
   constexpr int NT = 128 * NWN;  // threads
   constexpr int BM = kPBM, BN = 64 * NWN, BK = kPBK;
   constexpr int WM = 128, WN = 64;
   constexpr int MTL = WM / 16, NTL = WN / 16;
-  constexpr int ACH = BM * BK / 8 / NT;  // 16-byte activation chunks per thread per stage
+  constexpr int CPR = BK / 8;            // 16-byte chunks per LDS row
+  constexpr int ACH = BM * CPR / NT;     // activation chunks per thread per stage
   constexpr int BW = BN / 8;             // packed words per row of the tile
-  __shared__ u32x4 lds_a[2][BM * BK / 8];
-  __shared__ u32x4 lds_b[2][BN * BK / 8];
+  static_assert(BW * (BK / 4) == NT, "one packed word x 4 k-rows per thread");
+  __shared__ u32x4 lds_a[2][BM * CPR];
+  __shared__ u32x4 lds_b[2][BN * CPR];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int q = lane >> 4, r = lane & 15;
@@ -58,8 +65,9 @@ __global__ void __launch_bounds__(128 * NWN, 2) prefill_kn_kernel(const GemmArgs
   const int m0 = tm * BM, n0 = tn * BN;
 
   const int NW = p.N >> 3;
-  // dequant assignment: packed word bw of the tile, k-rows 2 rp and 2 rp + 1 of the stage
-  const int bw = tid % BW, rp = tid / BW;
+  // dequant assignment: packed word bw of the tile, k-rows 4 kq .. 4 kq + 3 of the stage
+  // (neighbouring lanes take neighbouring words: full 128-byte global row segments)
+  const int bw = tid % BW, kq = tid / BW;
   const int bword = (n0 >> 3) + bw;
   const int bwld = bword < NW ? bword : NW - 1;  // columns past N are computed, never stored
 
@@ -72,66 +80,124 @@ __global__ void __launch_bounds__(128 * NWN, 2) prefill_kn_kernel(const GemmArgs
   const int nst = p.K / BK;
   const MagicK mk = magic_consts();
   u32x4 areg[ACH];
-  uint32_t b0, b1;
+  uint32_t braw[4];
   WordSZ bsz;
   auto load = [&](int s) {
 #pragma unroll
     for (int i = 0; i < ACH; ++i) {
       const int c = tid + NT * i;
-      const int row = c >> 2, ch = c & 3;
+      const int row = c / CPR, ch = c % CPR;
       const int gr = min(m0 + row, p.M - 1);
       areg[i] = *(const u32x4*)(p.a + (int64_t)gr * p.lda + s * BK + ch * 8);
     }
-    const int64_t k = (int64_t)s * BK + 2 * rp;
-    b0 = __builtin_nontemporal_load(p.qw + k * NW + bwld);
-    b1 = __builtin_nontemporal_load(p.qw + (k + 1) * NW + bwld);
+    const int64_t k = (int64_t)s * BK + 4 * kq;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) braw[j] = __builtin_nontemporal_load(p.qw + (k + j) * NW + bwld);
     bsz = load_sz<ZP>(p, (s * BK) / p.G, bwld);
   };
-  auto write = [&](int buf) {
+  auto write_a = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < ACH; ++i) {
       const int c = tid + NT * i;
-      const int row = c >> 2, ch = c & 3;
-      lds_a[buf][row * 4 + (ch ^ swz(row))] = areg[i];
+      const int row = c / CPR, ch = c % CPR;
+      lds_a[buf][row * CPR + (ch ^ swz_a(row))] = areg[i];
     }
-    ColConst cc[8];
-    prep_consts<SEQ, FAST>(bsz, scale_bf16 != 0, cc);
-    const uint32_t lo = pair_lo(b0, b1), hi = pair_hi(b0, b1);
-    uint32_t* const lb = (uint32_t*)lds_b[buf];
-#define AWQ_PF_NIB(I)                                                                      \
-    {                                                                                      \
-      const uint32_t v = deq2<FAST, T>(magic_bits<(I) & 3>((I) < 4 ? lo : hi, mk), cc[I]); \
-      const int n = 8 * bw + nib_col<SEQ>(I);                                              \
-      lb[(n * 4 + ((rp >> 2) ^ swz(n))) * 4 + (rp & 3)] = v;                               \
-    }
-    AWQ_PF_NIB(0) AWQ_PF_NIB(1) AWQ_PF_NIB(2) AWQ_PF_NIB(3)
-    AWQ_PF_NIB(4) AWQ_PF_NIB(5) AWQ_PF_NIB(6) AWQ_PF_NIB(7)
-#undef AWQ_PF_NIB
   };
-  auto compute = [&](int buf) {
-    u32x4 bf[NTL];
+  // nibble I of the thread's word over its 4 k-rows -> 8 bytes of LDS row n = 8 bw + col(I);
+  // the nibble's constants are derived right here so only the raw group words stay live
+  auto write_b_nib = [&](int buf, int I, const uint32_t (&lo)[2], const uint32_t (&hi)[2]) {
+    u32x2 v;
+    const bool sb = scale_bf16 != 0;
+#define AWQ_PF_CASE(II, SRC, P)                                            \
+    case II: {                                                             \
+      const ColConst c_ = prep_const<II, SEQ, FAST>(bsz, sb);              \
+      v[0] = deq2<FAST, T>(magic_bits<P>(SRC[0], mk), c_);                 \
+      v[1] = deq2<FAST, T>(magic_bits<P>(SRC[1], mk), c_);                 \
+      break;                                                               \
+    }
+    switch (I) {  // I is a constant after unrolling
+      AWQ_PF_CASE(0, lo, 0) AWQ_PF_CASE(1, lo, 1) AWQ_PF_CASE(2, lo, 2) AWQ_PF_CASE(3, lo, 3)
+      AWQ_PF_CASE(4, hi, 0) AWQ_PF_CASE(5, hi, 1) AWQ_PF_CASE(6, hi, 2)
+      default: AWQ_PF_CASE(7, hi, 3)
+    }
+#undef AWQ_PF_CASE
+    const int n = 8 * bw + nib_col<SEQ>(I);
+    ((u32x2*)lds_b[buf])[(n * CPR + ((kq >> 1) ^ swz_b(n))) * 2 + (kq & 1)] = v;
+  };
+  auto mfma_sub = [&](int cb, int sub, int mt, const u32x4 (&bf)[NTL], const u32x4& af) {
+    (void)cb; (void)sub;
+#pragma unroll
+    for (int nt = 0; nt < NTL; ++nt) acc[mt][nt] = MfmaOp<T>::run(af, bf[nt], acc[mt][nt]);
+  };
+  auto read_b = [&](int cb, int sub, u32x4 (&bf)[NTL]) {
 #pragma unroll
     for (int nt = 0; nt < NTL; ++nt) {
       const int n = wave_n * WN + nt * 16 + r;
-      bf[nt] = lds_b[buf][n * 4 + (q ^ swz(n))];
+      bf[nt] = lds_b[cb][n * CPR + ((sub * 4 + q) ^ swz_b(n))];
     }
+  };
+  auto read_a = [&](int cb, int sub, int mt) {
+    const int row = wave_m * WM + mt * 16 + r;
+    return lds_a[cb][row * CPR + ((sub * 4 + q) ^ swz_a(row))];
+  };
+  // stage from buffer cb; the next stage's global data (already requested) is written to
+  // buffer wb during the second 32-k half, one nibble of the dequant per A fragment
+  auto step = [&](int cb, int wb) {
+    u32x4 bf[NTL];
+    u32x4 af[2];
+    read_b(cb, 0, bf);
+    af[0] = read_a(cb, 0, 0);
 #pragma unroll
     for (int mt = 0; mt < MTL; ++mt) {
-      const int row = wave_m * WM + mt * 16 + r;
-      const u32x4 af = lds_a[buf][row * 4 + (q ^ swz(row))];
+      if (mt + 1 < MTL) af[(mt + 1) & 1] = read_a(cb, 0, mt + 1);
+      mfma_sub(cb, 0, mt, bf, af[mt & 1]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    read_b(cb, 1, bf);
+    af[0] = read_a(cb, 1, 0);
+    write_a(wb);
+    uint32_t lo[2], hi[2];
+    lo[0] = pair_lo(braw[0], braw[1]);
+    hi[0] = pair_hi(braw[0], braw[1]);
+    lo[1] = pair_lo(braw[2], braw[3]);
+    hi[1] = pair_hi(braw[2], braw[3]);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int nt = 0; nt < NTL; ++nt) acc[mt][nt] = MfmaOp<T>::run(af, bf[nt], acc[mt][nt]);
+    for (int mt = 0; mt < MTL; ++mt) {
+      if (mt + 1 < MTL) af[(mt + 1) & 1] = read_a(cb, 1, mt + 1);
+      mfma_sub(cb, 1, mt, bf, af[mt & 1]);
+      write_b_nib(wb, mt & 7, lo, hi);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
+  // prologue: stage 0 into buffer 0
   load(0);
-  write(0);
-  if (nst > 1) load(1);
+  {
+    write_a(0);
+    uint32_t lo[2], hi[2];
+    lo[0] = pair_lo(braw[0], braw[1]);
+    hi[0] = pair_hi(braw[0], braw[1]);
+    lo[1] = pair_lo(braw[2], braw[3]);
+    hi[1] = pair_hi(braw[2], braw[3]);
+#pragma unroll
+    for (int I = 0; I < 8; ++I) write_b_nib(0, I, lo, hi);
+  }
   __syncthreads();
+  // iteration s: request stage s + 1 (the last stage re-requests itself), compute stage s
+  // from buffer s & 1 and, in its second half, write stage s + 1 into the other buffer (after
+  // the last stage into a buffer nobody reads); one barrier per 64-k stage
   for (int s = 0; s < nst; ++s) {
-    compute(s & 1);
-    if (s + 1 < nst) write((s + 1) & 1);
-    if (s + 2 < nst) load(s + 2);
+    load(min(s + 1, nst - 1));
+    step(s & 1, (s & 1) ^ 1);
     __syncthreads();
   }
 
