@@ -14,6 +14,7 @@ from .awq_triton import (  # noqa: F401
     awq_gemm_triton,
     packed_int4_fused_capability_check,
 )
+from .fused_pair import try_fused_awq_pair_matmul  # noqa: F401
 from .moe import (  # noqa: F401
     AWQExperts,
     awq_moe,
