@@ -208,6 +208,9 @@ static void launch_gemm_f16(const MoeArgs& a, int E, int mt, bool zp, hipStream_
   else zp ? launch_gemm_t<MODE, 1, true, f16, true>(a, E, 0, st) : launch_gemm_t<MODE, 1, false, f16, true>(a, E, 0, st);
 }
 
+// expected routes per expert from which the grouped MFMA kernels take over
+constexpr int kMoeMfmaMinRoutes = 16;
+
 // 16-token tiles per wave group, from the expected routes per expert
 static int moe_mt(int64_t R, int E) {
   const int64_t avg = R / (E > 0 ? E : 1);
@@ -278,7 +281,10 @@ int launch_moe(const MoeCall& c, hipStream_t st) {
   dn.rows_a = (int)R;
 
   const int sbf = c.scale_dtype == AWQ_DTYPE_BF16 ? 1 : 0;
-  if (c.act_dtype == AWQ_DTYPE_F16 && !sbf) {
+  if (R >= (int64_t)kMoeMfmaMinRoutes * c.E && (c.H % 64) == 0 && (c.I % 64) == 0) {
+    // many routes per expert: weights dequantized once per 64-route tile into LDS
+    launch_moe_mfma(gu, dn, c.E, zp, c.act_dtype, sbf, st);
+  } else if (c.act_dtype == AWQ_DTYPE_F16 && !sbf) {
     launch_gemm_f16<0>(gu, c.E, mt, zp, st);
     if (launch_status() != AWQ_OK) return AWQ_ERR_LAUNCH;
     launch_gemm_f16<1>(dn, c.E, mt, zp, st);

@@ -262,6 +262,9 @@ __global__ void __launch_bounds__(512) moe_gemm_kernel(const MoeArgs p, int scal
 }  // namespace awq
 
 namespace awq_host {
+// grouped MFMA kernels for many routes per expert (awq_moe_mfma.hip); both K dims % 64 == 0
+void launch_moe_mfma(const awq::MoeArgs& gu, const awq::MoeArgs& dn, int E, bool zp, int act, int sbf,
+                     hipStream_t st);
 // bf16 activations or bf16 scales (awq_moe_misc.hip); false if the dtype is not provided
 bool launch_moe_misc(const awq::MoeArgs& gu, const awq::MoeArgs& dn, int E, bool zp, int act, int sbf,
                      hipStream_t st);

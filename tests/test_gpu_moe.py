@@ -97,6 +97,10 @@ CASES = [
     (16, 64, 512, 256, 8, 128, True, "silu"),
     (100, 8, 256, 128, 2, 128, True, "gelu_pytorch_tanh"),   # ~25 routes per expert
     (200, 4, 256, 160, 2, 32, True, "silu"),                # ~100 routes per expert, I % 64 != 0
+    # >= 16 routes per expert with H, I % 64 == 0: the grouped MFMA kernels
+    (64, 4, 256, 128, 2, 32, False, "silu"),                # 32 routes/expert, 2 groups per k-stage
+    (128, 8, 512, 192, 4, 64, True, "gelu_pytorch_tanh"),   # partial gate tile (I = 192)
+    (300, 16, 256, 256, 4, 128, True, "silu"),              # ~75 routes/expert: 2 row tiles
 ]
 
 
@@ -200,3 +204,23 @@ def test_config4_full_size(T):
     w1, w2 = _dense_experts(d, G)
     exact = O.moe_grouped_exact(p["x"], tw.numpy(), tid.numpy(), w1, w2)
     _check(y.cpu().numpy(), exact, f"config4 T={T}")
+
+
+def test_moe_mfma_path_bf16():
+    T, E, H, I, topk, G = 96, 4, 256, 128, 2, 64   # 48 routes per expert
+    p, d = _problem(T, E, H, I, topk, G, seed=9)
+    tw, tid = _route_cpu(torch.from_numpy(p["logits"]), topk)
+    xb = torch.from_numpy(p["x"]).float().bfloat16()
+    y = ops.moe(xb.to(DEV), tw.to(DEV), tid.to(DEV), d["gq"], d["gs"], d["gz"], d["dq"], d["ds"], d["dz"], G)
+    gq, gz, gs = p["gate_up"]
+    dq, dz, ds = p["down"]
+    bf = lambda q, s, z: O.bf16_bits_to_f32(O.dequant_awq(q, s, z, G, out_dtype="bfloat16")).T
+    w1b = np.stack([bf(gq[e], gs[e], gz[e]) for e in range(E)])
+    w2b = np.stack([bf(dq[e], ds[e], dz[e]) for e in range(E)])
+    exact = O.moe_grouped_exact(xb.float().numpy(), tw.numpy(), tid.numpy(), w1b, w2b, inter_dtype="bfloat16")
+    yf = y.float().cpu().numpy()
+    floor = float(np.sqrt(np.mean(exact ** 2)))
+    d_ = np.abs(yf - exact)
+    assert np.max(d_ / O.fp16_ulp(exact, floor)) <= 16.0
+    assert d_.sum() / np.abs(exact).sum() <= 2e-3
+
