@@ -24,7 +24,7 @@ constexpr int kGBM = 64, kGBN = 256, kGBK = 64;
 
 // MODE 0: gate_up (paired stream tiles, activation epilogue into the intermediate)
 // MODE 1: down (plain stream tiles, fp32 per-route rows)
-template <int MODE, bool ZP, typename T, bool FAST>
+template <int MODE, int PD, bool ZP, typename T, bool FAST>
 __global__ void __launch_bounds__(512, 1) moe_mfma_kernel(const MoeArgs p, int scale_bf16, int E, int tiles_n) {
   constexpr int NT = 512, BM = kGBM, BN = kGBN, BK = kGBK;
   constexpr int WM = 32, WN = 64, MTL = WM / 16, NTL = WN / 16;
@@ -55,9 +55,12 @@ __global__ void __launch_bounds__(512, 1) moe_mfma_kernel(const MoeArgs p, int s
   const int KS = p.K >> 5;
   const int NW = p.N >> 3;
   const int ngroups = p.K / p.G;
-  const uint32_t* qw = p.qw + (int64_t)e * p.tiles * KS * 512;
-  const uint16_t* sc = p.sc + (int64_t)e * ngroups * p.N;
-  const uint32_t* qz = ZP ? p.qz + (int64_t)e * ngroups * NW : nullptr;
+  const uint32_t stream_bytes = (uint32_t)p.tiles * (uint32_t)KS * 2048u;
+  const __amdgpu_buffer_rsrc_t wrs = make_rsrc((const char*)p.qw + (int64_t)e * stream_bytes, stream_bytes);
+  const __amdgpu_buffer_rsrc_t srs = make_rsrc(p.sc + (int64_t)e * ngroups * p.N, (uint32_t)ngroups * (uint32_t)p.N * 2u);
+  const __amdgpu_buffer_rsrc_t zrs =
+      make_rsrc(ZP ? (const void*)(p.qz + (int64_t)e * ngroups * NW) : (const void*)p.sc, ZP ? (uint32_t)ngroups * (uint32_t)NW * 4u : 0u);
+  const __amdgpu_buffer_rsrc_t xrs = make_rsrc(p.a, (uint32_t)((uint64_t)p.rows_a * (uint64_t)p.lda * 2u));
 
   // ---- activation row gathered by this thread (one 16-byte chunk per stage) ----
   const int arow = tid >> 3, ach = tid & 7;
@@ -69,7 +72,8 @@ __global__ void __launch_bounds__(512, 1) moe_mfma_kernel(const MoeArgs p, int s
       src = MODE == 0 ? rt / p.topk : rt;
     }
   }
-  const uint16_t* arow_ptr = p.a + (int64_t)src * p.lda + ach * 8;
+  // per-lane byte offsets are fixed; each stage adds a wave-uniform offset (SGPR)
+  const uint32_t a_voff = ((uint32_t)src * (uint32_t)p.lda + 8u * (uint32_t)ach) * 2u;
 
   // ---- weight word of this thread: stream tile, lane, LDS row of each nibble column ----
   const int bw = tid & 31, kq = tid >> 5;  // word of the block, k-rows 4 kq .. 4 kq + 3
@@ -92,6 +96,13 @@ __global__ void __launch_bounds__(512, 1) moe_mfma_kernel(const MoeArgs p, int s
   }
   const int stld = stile < p.tiles ? stile : p.tiles - 1;  // in-range reads for padding words
   const uint32_t wc = gword < 0 ? 0u : (uint32_t)gword;
+  // k-step 2 s + kq / 8, rows 4 (kq % 8) .. + 3 of it: lane piece (kq & 1) of lane 16 q' + r
+  const uint32_t b_voff = ((uint32_t)stld * (uint32_t)KS + (uint32_t)(kq >> 3)) * 2048u + (uint32_t)(kq & 1) * 1024u +
+                          (uint32_t)(16 * ((kq & 7) >> 1) + slane) * 16u;
+  // group of the thread's rows: (64 s + 4 kq) / G = 64 s / G + (G == 32 ? kq / 8 : 0)
+  const int g_lane = p.G == 32 ? (kq >> 3) : 0;
+  const uint32_t s_voff = 16u * wc + (uint32_t)g_lane * (uint32_t)p.N * 2u;
+  const uint32_t z_voff = 4u * wc + (uint32_t)g_lane * (uint32_t)NW * 4u;
 
   f32x4 acc[MTL][NTL];
 #pragma unroll
@@ -99,18 +110,28 @@ __global__ void __launch_bounds__(512, 1) moe_mfma_kernel(const MoeArgs p, int s
 #pragma unroll
     for (int nt = 0; nt < NTL; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int nst = p.K / BK;
+  const int nst = p.K / BK;  // a multiple of PD (the launcher picks PD so)
   const MagicK mk = magic_consts();
+  // ring of PD stages of global data in registers: stage s + 1 + PD is requested right after
+  // stage s + 1 went to LDS, so PD stages of MFMA work cover its latency
+  u32x4 aring[PD], bring[PD];
+  WordSZ szring[PD];
   u32x4 areg, braw;
   WordSZ bsz;
-  auto load = [&](int s) {
-    areg = *(const u32x4*)(arow_ptr + s * BK);
-    // k-step 2 s + kq / 8, rows 4 (kq % 8) .. + 3 of it: lane piece (kq & 1) of lane 16 q' + r
-    const int ks = 2 * s + (kq >> 3), qq = (kq & 7) >> 1;
-    braw = *(const u32x4*)(qw + ((int64_t)stld * KS + ks) * 512 + (kq & 1) * 256 + (16 * qq + slane) * 4);
-    const int g = (s * BK + 4 * kq) / p.G;  // the thread's 4 rows lie in one group (G % 32 == 0)
-    bsz.s4 = *(const u32x4*)(sc + (int64_t)g * p.N + 8 * wc);
-    bsz.zw = ZP ? qz[(int64_t)g * NW + wc] : 0x88888888u;
+  auto load = [&](int s, int slot) {
+    s = min(s, nst - 1);  // past the end: re-request the last stage (never written)
+    aring[slot] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)a_voff, s * BK * 2, 0));
+    bring[slot] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, (int)b_voff, s * 4096, 0));
+    const int gu = (s * BK) / p.G;  // wave-uniform part of the group
+    szring[slot].s4 = __builtin_bit_cast(
+        u32x4, __builtin_amdgcn_raw_buffer_load_b128(srs, (int)s_voff, (int)((uint32_t)gu * (uint32_t)p.N * 2u), 0));
+    szring[slot].zw = ZP ? __builtin_amdgcn_raw_buffer_load_b32(zrs, (int)z_voff, (int)((uint32_t)gu * (uint32_t)NW * 4u), 0)
+                         : 0x88888888u;
+  };
+  auto take = [&](int slot) {
+    areg = aring[slot];
+    braw = bring[slot];
+    bsz = szring[slot];
   };
   auto write_a = [&](int buf) { lds_a[buf][arow * CPR + (ach ^ gswz_a(arow))] = areg; };
   auto write_b_nib = [&](int buf, int I, const uint32_t (&lo)[2], const uint32_t (&hi)[2]) {
@@ -171,7 +192,9 @@ __global__ void __launch_bounds__(512, 1) moe_mfma_kernel(const MoeArgs p, int s
     }
   };
 
-  load(0);
+#pragma unroll
+  for (int u = 0; u < PD; ++u) load(u, u);
+  take(0);
   {
     write_a(0);
     uint32_t lo[2], hi[2];
@@ -179,11 +202,17 @@ __global__ void __launch_bounds__(512, 1) moe_mfma_kernel(const MoeArgs p, int s
 #pragma unroll
     for (int I = 0; I < 8; ++I) write_b_nib(0, I, lo, hi);
   }
+  load(PD, 0);
   __syncthreads();
-  for (int s = 0; s < nst; ++s) {
-    load(min(s + 1, nst - 1));  // the last stage re-requests itself; its write goes unread
-    step(s & 1, (s & 1) ^ 1);
-    __syncthreads();
+  for (int s0 = 0; s0 < nst; s0 += PD) {
+#pragma unroll
+    for (int u = 0; u < PD; ++u) {
+      const int s = s0 + u;
+      take((u + 1) % PD);  // stage s + 1 (after the last stage: unread data)
+      step(s & 1, (s & 1) ^ 1);
+      load(s + 1 + PD, (u + 1) % PD);
+      __syncthreads();
+    }
   }
 
   // ---- epilogue: lane (q, r), acc[mt][nt][v] = row m0 + wave_m*WM + mt*16 + 4q + v,
@@ -224,8 +253,14 @@ template <int MODE, bool ZP, typename T, bool FAST>
 static void launch_mfma_t(const MoeArgs& a, int E, int sbf, hipStream_t st) {
   const int tiles_n = MODE == 0 ? (int)cdiv(a.half, 16) : (int)cdiv(a.N / 8, 32);
   const int64_t tiles_m = cdiv(a.R, kGBM) + E;  // each expert adds at most one partial tile
-  hipLaunchKernelGGL((moe_mfma_kernel<MODE, ZP, T, FAST>), dim3((unsigned)(tiles_m * tiles_n)), dim3(512), 0, st,
-                     a, sbf, E, tiles_n);
+  const dim3 grid((unsigned)(tiles_m * tiles_n));
+  const int nst = a.K / kGBK;
+  if (nst % 4 == 0)
+    hipLaunchKernelGGL((moe_mfma_kernel<MODE, 4, ZP, T, FAST>), grid, dim3(512), 0, st, a, sbf, E, tiles_n);
+  else if (nst % 2 == 0)
+    hipLaunchKernelGGL((moe_mfma_kernel<MODE, 2, ZP, T, FAST>), grid, dim3(512), 0, st, a, sbf, E, tiles_n);
+  else
+    hipLaunchKernelGGL((moe_mfma_kernel<MODE, 1, ZP, T, FAST>), grid, dim3(512), 0, st, a, sbf, E, tiles_n);
 }
 
 template <int MODE>
