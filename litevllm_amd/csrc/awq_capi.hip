@@ -158,7 +158,7 @@ int awq_w4a16_pack_decode_stream(const int32_t* qweight_kn, int32_t* out, int64_
   if (!qweight_kn || !out) return AWQ_ERR_NULL;
   if (K < 0 || N < 0 || (N % 8) != 0 || (K % 32) != 0) return AWQ_ERR_SHAPE;
   if (decode_stream_bytes(K, N) > 0x7FFFFFFFLL) return AWQ_ERR_UNSUPPORTED;
-  return launch_pack_decode_stream(qweight_kn, out, K, N, decode_stream_wpl(N), (hipStream_t)stream);
+  return launch_pack_decode_stream(qweight_kn, out, K, N, (hipStream_t)stream);
 }
 
 // ---- mixture of experts ----

@@ -153,10 +153,10 @@ struct GemmArgs {
   int bias_dtype;
 };
 
-// Work decomposition of the decode kernel: tiles x ksteps units over `blocks` blocks; a tile
-// has at most max_contrib contributing blocks.
+// Work decomposition of the decode kernel: tiles x ksteps units; each tile's k-steps are cut
+// into `splits` ranges, one block each (block b: tile b / splits, range b % splits).
 struct DecodeWork {
-  int tiles, ksteps, blocks, max_contrib;
+  int tiles, ksteps, splits;
 };
 
 // Raw per-group constants of one packed word: 8 scales (16 bytes) and the zero word.
@@ -200,6 +200,19 @@ __device__ __forceinline__ ColConst prep_const(const WordSZ& sz, bool scale_bf16
   return cc;
 }
 
+// Decode constants of nibble i: the biased zero and the fp32 scale (the decode kernel feeds
+// the MFMA the integers q - z and scales each group's sum).
+template <bool SEQ, bool SBF>
+__device__ __forceinline__ ColConst prep_const_int(const WordSZ& sz, int i) {
+  const int c = nib_col<SEQ>(i);
+  const uint32_t sbits = (sz.s4[c >> 1] >> (16 * (c & 1))) & 0xFFFFu;
+  ColConst cc;
+  cc.zm = zero_magic(i & 1, (sz.zw >> (4 * i)) & 0xF);
+  cc.sc = 0;
+  cc.scf = SBF ? bf_bits2f((uint16_t)sbits) : h_bits2f((uint16_t)sbits);
+  return cc;
+}
+
 // Row pairing with one byte permute: lo16(w0) | lo16(w1) << 16 and hi16(w0) | hi16(w1) << 16.
 // (v_perm_b32 selects bytes 0-3 from its second operand and 4-7 from its first.)
 __device__ __forceinline__ uint32_t pair_lo(uint32_t w0, uint32_t w1) {
@@ -217,6 +230,21 @@ __device__ __forceinline__ u32x4 rows_operand(const uint32_t (&mlo)[4], const ui
   u32x4 r;
 #pragma unroll
   for (int u = 0; u < 4; ++u) r[u] = deq2<FAST, T>(magic_bits<I & 3>(I < 4 ? mlo[u] : mhi[u], k), cc);
+  return r;
+}
+
+// Eight rows (k .. k+7) of nibble I as the exact integers q - z in T: the subtraction of the
+// biased zero is exact in fp16, and integers up to 15 in magnitude are exact in bf16.
+template <int I, typename T>
+__device__ __forceinline__ u32x4 int_operand(const uint32_t (&mlo)[4], const uint32_t (&mhi)[4], uint32_t zm,
+                                             const MagicK& k) {
+  u32x4 r;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const f16x2 d = as_h2(magic_bits<I & 3>(I < 4 ? mlo[u] : mhi[u], k)) - as_h2(zm);
+    if constexpr (std::is_same<T, f16>::value) r[u] = as_u(d);
+    else r[u] = pack2<bf16>((float)d.x, (float)d.y);
+  }
   return r;
 }
 

@@ -7,12 +7,16 @@ using namespace awq;
 
 bool launch_decode_misc(const GemmArgs& a, const DecodePlan& s, bool seq, bool zp, int act, int sbf,
                         hipStream_t st) {
-  if (act == AWQ_DTYPE_F16) {
-    if (seq) return zp ? launch_sel<true, true, f16, false, false>(a, s, sbf, st) : launch_sel<true, false, f16, false, false>(a, s, sbf, st);
-    return zp ? launch_sel<false, true, f16, false, false>(a, s, sbf, st) : launch_sel<false, false, f16, false, false>(a, s, sbf, st);
+  if (act == AWQ_DTYPE_F16) {  // bf16 scales
+    if (seq) return zp ? launch_sel<true, true, f16, true, false, false>(a, s, st) : launch_sel<true, false, f16, true, false, false>(a, s, st);
+    return zp ? launch_sel<false, true, f16, true, false, false>(a, s, st) : launch_sel<false, false, f16, true, false, false>(a, s, st);
   }
-  if (seq) return zp ? launch_sel<true, true, bf16, false, false>(a, s, sbf, st) : launch_sel<true, false, bf16, false, false>(a, s, sbf, st);
-  return zp ? launch_sel<false, true, bf16, false, false>(a, s, sbf, st) : launch_sel<false, false, bf16, false, false>(a, s, sbf, st);
+  if (sbf) {
+    if (seq) return zp ? launch_sel<true, true, bf16, true, false, false>(a, s, st) : launch_sel<true, false, bf16, true, false, false>(a, s, st);
+    return zp ? launch_sel<false, true, bf16, true, false, false>(a, s, st) : launch_sel<false, false, bf16, true, false, false>(a, s, st);
+  }
+  if (seq) return zp ? launch_sel<true, true, bf16, false, false, false>(a, s, st) : launch_sel<true, false, bf16, false, false, false>(a, s, st);
+  return zp ? launch_sel<false, true, bf16, false, false, false>(a, s, st) : launch_sel<false, false, bf16, false, false, false>(a, s, st);
 }
 
 }  // namespace awq_host

@@ -130,11 +130,11 @@ __global__ void __launch_bounds__(256) repack_s_kernel(const uint16_t* __restric
   out[idx] = in[n * NG + g];
 }
 
-// Decode stream pack (layout documented at decode_stream_bytes): thread = one lane's 8 W
-// words of one (tile, k-step) run.
+// Decode stream pack (layout documented at decode_stream_bytes): thread = one lane's 8 words
+// of one (tile, k-step) run, rows paired as the decode kernel unpacks them.
 __global__ void __launch_bounds__(256) pack_stream_kernel(const uint32_t* __restrict__ in,
                                                           uint32_t* __restrict__ out, int64_t K,
-                                                          int64_t NW, int64_t tiles, int W) {
+                                                          int64_t NW, int64_t tiles) {
   const int64_t KS = K / 32;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= tiles * KS * 64) return;
@@ -142,14 +142,13 @@ __global__ void __launch_bounds__(256) pack_stream_kernel(const uint32_t* __rest
   const int64_t ts = idx >> 6;  // t * KS + s
   const int64_t t = ts / KS, s = ts - t * KS;
   const int q = l >> 4, r = l & 15;
-  const int64_t w0 = t * 16 * W + (int64_t)r * W;
-  uint32_t* run = out + ts * 512 * W;  // 2048 W bytes per (tile, k-step)
-  for (int j = 0; j < 8; ++j) {
-    const int64_t row = s * 32 + 8 * q + j;
-    for (int w = 0; w < W; ++w) {
-      const int n = j * W + w;  // the lane's u32 number: piece n / 4 at byte 1024 (n / 4) + 16 l
-      run[(n >> 2) * 256 + l * 4 + (n & 3)] = (w0 + w < NW) ? in[row * NW + w0 + w] : 0u;
-    }
+  const int64_t w = t * 16 + r;
+  uint32_t rows[8];
+  for (int j = 0; j < 8; ++j) rows[j] = (w < NW) ? in[(s * 32 + 8 * q + j) * NW + w] : 0u;
+  uint32_t* run = out + ts * 512;  // 2048 bytes per (tile, k-step)
+  for (int v = 0; v < 4; ++v) {
+    run[l * 4 + v] = pair_lo(rows[2 * v], rows[2 * v + 1]);        // piece 0
+    run[256 + l * 4 + v] = pair_hi(rows[2 * v], rows[2 * v + 1]);  // piece 1
   }
 }
 
@@ -250,14 +249,12 @@ int launch_repack_nk_to_autoawq(const int32_t* qweight_nk, const int32_t* qzeros
   return launch_status();
 }
 
-int launch_pack_decode_stream(const int32_t* qweight_kn, int32_t* out, int64_t K, int64_t N, int wpl,
-                              hipStream_t st) {
-  if (wpl != 1 && wpl != 2 && wpl != 4) return AWQ_ERR_UNSUPPORTED;
-  const int64_t NW = N / 8, tiles = cdiv(NW, 16 * wpl);
+int launch_pack_decode_stream(const int32_t* qweight_kn, int32_t* out, int64_t K, int64_t N, hipStream_t st) {
+  const int64_t NW = N / 8, tiles = cdiv(NW, 16);
   const int64_t n = tiles * (K / 32) * 64;
   if (n > 0)
     hipLaunchKernelGGL(pack_stream_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st,
-                       (const uint32_t*)qweight_kn, (uint32_t*)out, K, NW, tiles, wpl);
+                       (const uint32_t*)qweight_kn, (uint32_t*)out, K, NW, tiles);
   return launch_status();
 }
 

@@ -11,12 +11,12 @@
 namespace awq_host {
 
 // Workspace layout of the decode kernel: [0, kCounterBytes) per-tile arrival counters (zero
-// between calls), then fp32 partials [tiles, max_contrib, M, tile columns].
+// between calls), then fp32 partials [tiles, splits, M, 128].
 constexpr size_t kCounterBytes = 65536;
 
 struct DecodePlan {
-  int wpl, mt, nwv, depth, occ;  // words per lane, 16-token tiles, waves/block, ring depth, waves/SIMD
-  int tiles, ksteps, waves, blocks, max_contrib;
+  int mt;  // 16-token MFMA tiles
+  int tiles, ksteps, splits, blocks;
   size_t ws_bytes;
 };
 
@@ -37,19 +37,14 @@ bool launch_decode(const awq::GemmArgs& a, const DecodePlan& s, DecodeMode mode,
 bool launch_decode_misc(const awq::GemmArgs& a, const DecodePlan& s, bool seq, bool zp, int act, int sbf,
                         hipStream_t st);
 
-// Decode stream layout with W words per lane (tile = 16 W packed words = 128 W columns): the
-// (tile t, k-step s) run of 2048 W bytes starts at byte (t * K/32 + s) * 2048 W.  Lane
-// l = 16 q + r owns 8 W words of it, u32 number j * W + w being word 16 W t + W r + w of row
-// 32 s + 8 q + j (zero past the last word); its u32 numbers 4 e .. 4 e + 3 (piece e) sit at
-// byte 1024 e + 16 l of the run, so every KiB is one piece of all 64 lanes.  W is fixed by
-// the shape (decode_stream_wpl).
-inline int decode_stream_wpl(int64_t N) { (void)N; return 1; }
-inline int64_t decode_stream_bytes(int64_t K, int64_t N) {
-  const int w = decode_stream_wpl(N);
-  return awq::cdiv(N / 8, 16 * w) * 16 * w * K * 4;
-}
-int launch_pack_decode_stream(const int32_t* qweight_kn, int32_t* out, int64_t K, int64_t N, int wpl,
-                              hipStream_t st);
+// Decode stream layout (tile = 16 packed words = 128 columns): the (tile t, k-step s) run of
+// 2048 bytes starts at byte (t * K/32 + s) * 2048.  Lane l = 16 q + r owns word 16 t + r
+// (zero past the last word) of rows 32 s + 8 q + j, j < 8, stored pre-paired for the
+// kernel's magic-exponent unpack: its u32 number v < 4 is lo16(row 2v) | lo16(row 2v+1) << 16
+// and number 4 + v is hi16(row 2v) | hi16(row 2v+1) << 16.  Numbers 4 e .. 4 e + 3 (piece e)
+// sit at byte 1024 e + 16 l of the run, so every KiB is one piece of all 64 lanes.
+inline int64_t decode_stream_bytes(int64_t K, int64_t N) { return awq::cdiv(N / 8, 16) * 16 * K * 4; }
+int launch_pack_decode_stream(const int32_t* qweight_kn, int32_t* out, int64_t K, int64_t N, hipStream_t st);
 
 // Prefill GEMM (M > 32 or group sizes the decode kernel does not cover).
 bool launch_prefill(const awq::GemmArgs& a, bool seq, bool zp, int act, int sdt, hipStream_t st);

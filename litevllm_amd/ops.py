@@ -207,8 +207,6 @@ WORKSPACE = _Workspace()
 
 # ------------------------------------------------------------------ GEMM
 DECODE_MAX_M = 32
-# packed words per lane of the library's decode stream layout (decode_stream_wpl in csrc)
-DECODE_STREAM_WPL = 1
 DECODE_GROUPS = (32, 64, 128)
 
 

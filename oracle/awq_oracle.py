@@ -112,6 +112,10 @@ def repack_ref_to_awq(qweight_ref, qzeros_ref, scales_ref):
 
 
 def _round_out(res_f32: np.ndarray, out_dtype: str) -> np.ndarray:
+    if out_dtype == "float32":
+        # unrounded: the fused kernel's M = 1 operand b (awq_fused_gemm.py:1966-1971); exact,
+        # since |q - z| <= 15 and a fp16/bf16 scale carry at most 4 + 11 significant bits
+        return res_f32.astype(np.float32)
     if out_dtype == "float16":
         return res_f32.astype(np.float16)
     if out_dtype == "bfloat16":
@@ -141,7 +145,9 @@ def dequant_ref(qweight, scales, qzeros, group_size, out_dtype="float16", zero_p
     ``(qs - zs) * scales``, one cast) and, for ``zero_point=False``,
     ``dequantize_symmetric_packed_int4_pytorch`` (``tensor.py:863-901``: z = 8).
     ``out_dtype="bfloat16"`` follows the fused Triton path's single rounding of the
-    float32 product (``awq_fused_gemm.py:1966, 1976``) and returns bf16 bit patterns.
+    float32 product (``awq_fused_gemm.py:1966, 1976``) and returns bf16 bit patterns;
+    ``out_dtype="float32"`` returns the product unrounded, the operand the fused path's
+    M = 1 branch accumulates (``awq_fused_gemm.py:1966-1971``).
     Pinned by: exhaustive (q, z) x scale sweep against float64-exact products
     rounded once, the symmetric known-answer words, and the ``q == z -> +0.0`` case.
     """

@@ -65,8 +65,10 @@ def test_fused_pair_matches_oracle_and_separate_calls(M, zeros):
     assert torch.equal(y, y2)
     za = pa["qzeros"] if zeros else None
     zb = pb["qzeros"] if zeros else None
-    wa = O.dequant_awq(pa["qweight"], pa["scales"], za, G, zero_point=zeros)
-    wb = O.dequant_awq(pb["qweight"], pb["scales"], zb, G, zero_point=zeros)
+    # the skinny kernel (M <= 32) multiplies unrounded weights, the prefill one fp16 ones
+    wdt = "float32" if M <= 32 else "float16"
+    wa = O.dequant_awq(pa["qweight"], pa["scales"], za, G, out_dtype=wdt, zero_point=zeros)
+    wb = O.dequant_awq(pb["qweight"], pb["scales"], zb, G, out_dtype=wdt, zero_point=zeros)
     w = np.concatenate([wa, wb], axis=1).T                       # [2N, K]
     exact = O.linear_exact(pa["x"], w, np.concatenate([ba.numpy(), bb.numpy()]))
     rep = O.error_report(y.cpu().numpy(), exact)

@@ -2,9 +2,10 @@
 
 Bars (stated per test):
   * dequantized weights: bit-exact (uint16 patterns / fp32 values equal);
-  * GEMM outputs vs the exact oracle (float64 sum of exact fp16 products): every
-    element within 1 fp16 ulp of the exact value (ulp taken at max(|y|, 1), see
-    ``oracle.awq_oracle.fp16_ulp``), i.e. fp32 accumulation plus one final rounding;
+  * GEMM outputs vs the exact oracle (float64 sum of exact products with the weights the
+    serving kernel uses, see ``_w_used``): every element within 1 fp16 ulp of the exact
+    value (ulp taken at max(|y|, 1), see ``oracle.awq_oracle.fp16_ulp``), i.e. fp32
+    accumulation plus one final rounding;
   * GEMM outputs vs the reference's own CPU path (dequant + F.linear): elementwise
     |d| <= max(2e-2, 1 ulp(|ref|)) and mean relative error sum|d|/sum|ref| <= 1e-3.
     The 2e-2 bound alone is below one fp16 ulp for |y| >= 32 (one rounding flip
@@ -34,6 +35,22 @@ def _to_dev(p):
 
 def _note(msg):
     print(msg, flush=True)
+
+
+def _decode_path(M, G):
+    """Calls the skinny kernel serves (M <= 32, G in {32, 64, 128}).  It feeds the MFMA the
+    exact integers q - z and scales each group's fp32 sum, so its weights enter unrounded, as
+    in the reference's M = 1 branch (awq_fused_gemm.py:1966-1971); the prefill kernel rounds
+    them to the activation dtype first, as the reference's tl.dot branch does (1973-1976)."""
+    return M <= 32 and G in (32, 64, 128)
+
+
+def _w_used(p, M, G, zp=True, half="float16"):
+    """Dequantized [K, N] weights as the kernel serving (M, G) multiplies them: float32
+    unrounded on the decode path, else rounded once to ``half``."""
+    out = "float32" if _decode_path(M, G) else half
+    w = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"] if zp else None, G, out_dtype=out, zero_point=zp)
+    return O.bf16_bits_to_f32(w) if out == "bfloat16" else w
 
 
 def _check_vs_exact(y, ye, what):
@@ -125,7 +142,7 @@ def test_gemm_autoawq_vs_oracle(M, K, N, G, stream):
     t = _to_dev(p)
     y = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, layout="autoawq",
                  decode_stream=stream).cpu().numpy()
-    w = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"], G)       # [K, N]
+    w = _w_used(p, M, G)                                                 # [K, N]
     _check_vs_exact(y, O.linear_exact(p["x"], w.T), f"M={M} K={K} N={N}")
     qr, zr, sr = O.repack_awq_to_ref(p["qweight"], p["qzeros"], p["scales"]) if (K // G) % 8 == 0 else (None,) * 3
     if qr is not None:
@@ -144,7 +161,7 @@ def test_gemm_bias(M, bias_dtype):
     t = _to_dev(p)
     b = torch.randn(N, generator=torch.Generator().manual_seed(3)).to(bias_dtype)
     y = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, bias=b.to(DEV), layout="autoawq").cpu().numpy()
-    w = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"], G)
+    w = _w_used(p, M, G)
     _check_vs_exact(y, O.linear_exact(p["x"], w.T, b.double().numpy()), f"bias M={M}")
 
 
@@ -157,8 +174,9 @@ def test_gemm_bf16_activations(M, K, N):
     t = _to_dev(p)
     xb = torch.from_numpy(p["x"]).to(torch.bfloat16)
     y = ops.gemm(xb.to(DEV), t["qweight"], t["scales"], t["qzeros"], G, layout="autoawq").float().cpu().numpy()
-    # weights rounded once to bf16 from the exact product (fused path, awq_fused_gemm.py:1966-1976)
-    wb = O.bf16_bits_to_f32(O.dequant_awq(p["qweight"], p["scales"], p["qzeros"], G, out_dtype="bfloat16"))
+    # decode path: unrounded weights; prefill: rounded once to bf16 from the exact product
+    # (fused path, awq_fused_gemm.py:1966-1976)
+    wb = _w_used(p, M, G, half="bfloat16")
     ye = xb.double().numpy() @ wb.astype(np.float64)
     # one bf16 rounding of the fp32 sum: |d| <= 1 bf16 ulp of max(|y|, 1)
     ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(ye), 1.0))) - 7)
@@ -172,7 +190,7 @@ def test_gemm_symmetric(M, K, N, G):
     p = make_awq_problem(M=M, K=K, N=N, group_size=G, seed=13)
     t = _to_dev(p)
     y = ops.gemm(t["x"], t["qweight"], t["scales"], None, G, layout="autoawq").cpu().numpy()
-    w = O.dequant_awq(p["qweight"], p["scales"], None, G, zero_point=False)
+    w = _w_used(p, M, G, zp=False)
     _check_vs_exact(y, O.linear_exact(p["x"], w.T), "symmetric")
 
 
@@ -186,7 +204,7 @@ def test_gemm_kn_seq_layout():
     y = ops.gemm(torch.from_numpy(p["x"]).to(DEV), torch.from_numpy(qw).to(DEV),
                  torch.from_numpy(p["scales"]).to(DEV), torch.from_numpy(qz).to(DEV), G,
                  layout="kn_seq").cpu().numpy()
-    w = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"], G)
+    w = _w_used(p, M, G)
     _check_vs_exact(y, O.linear_exact(p["x"], w.T), "kn_seq")
 
 
@@ -199,8 +217,7 @@ def test_split_k_config2_bit_stable(M):
     K, N, G = 12288, 4096, 128
     p = make_awq_problem(M=M, K=K, N=N, group_size=G, seed=2)
     t = _to_dev(p)
-    w = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"], G)
-    ye = O.linear_exact(p["x"], w.T)
+    ye = O.linear_exact(p["x"], _w_used(p, M, G).T)
     for sk in (1, 4, 8):
         _note(f"split-K M={M} split={sk} (AutoAWQ layout read directly)")
         y1 = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, split_k=sk, layout="autoawq", decode_stream=False)
@@ -220,7 +237,7 @@ def test_config1_decode_sweep(M, N, stream):
     t = _to_dev(p)
     y = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, layout="autoawq",
                  decode_stream=stream).cpu().numpy()
-    w = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"], G)
+    w = _w_used(p, M, G)
     _check_vs_exact(y, O.linear_exact(p["x"], w.T), f"config1 M={M} N={N}")
     qr, zr, sr = O.repack_awq_to_ref(p["qweight"], p["qzeros"], p["scales"])
     yr = R.awq_linear_cpu(torch.from_numpy(p["x"]), torch.from_numpy(qr), torch.from_numpy(sr),
@@ -251,18 +268,22 @@ def test_config3_prefill(M, N):
 
 
 # ------------------------------------------------------------------ decode stream layout
-def _stream_layout_numpy(qw_kn, W):
+def _stream_layout_numpy(qw_kn):
     """The decode stream layout restated with numpy gathers: in the (tile t, k-step s) run, lane
-    l = 16q + r owns u32 number n = j*W + w = word 16W t + W r + w of row 32s + 8q + j (zero
-    past the last word), stored at byte 1024 (n // 4) + 16 l + 4 (n % 4); runs tile-major."""
+    l = 16q + r owns word 16 t + r (zero past the last word) of rows 32 s + 8 q + j; its u32
+    number v < 4 is lo16(row 2v) | lo16(row 2v+1) << 16 and number 4 + v the same of the high
+    halves, stored at byte 1024 (n // 4) + 16 l + 4 (n % 4); runs tile-major."""
     K, NW = qw_kn.shape
-    tiles = -(-NW // (16 * W))
-    pad = np.zeros((K, tiles * 16 * W), dtype=np.int32)
-    pad[:, :NW] = qw_kn
-    v = pad.reshape(K // 32, 4, 8, tiles, 16, W)              # [s, q, j, t, r, w]
-    lane_words = v.transpose(3, 0, 1, 4, 2, 5).reshape(tiles, K // 32, 64, 8 * W)  # [t, s, l, n]
-    pieces = lane_words.reshape(tiles, K // 32, 64, 2 * W, 4).transpose(0, 1, 3, 2, 4)  # [t, s, e, l, c]
-    return np.ascontiguousarray(pieces).reshape(-1)
+    tiles = -(-NW // 16)
+    pad = np.zeros((K, tiles * 16), dtype=np.uint32)
+    pad[:, :NW] = qw_kn.view(np.uint32)
+    v = pad.reshape(K // 32, 4, 4, 2, tiles, 16)            # [s, q, v, row parity, t, r]
+    lo, hi = v & 0xFFFF, v >> 16
+    plo = lo[:, :, :, 0] | (lo[:, :, :, 1] << 16)           # [s, q, v, t, r]
+    phi = hi[:, :, :, 0] | (hi[:, :, :, 1] << 16)
+    n = np.stack([plo, phi], axis=2)                         # [s, q, e, v, t, r]
+    lane = n.transpose(4, 0, 2, 1, 5, 3)                     # [t, s, e, q, r, v]
+    return np.ascontiguousarray(lane).reshape(-1).view(np.int32)
 
 
 @pytest.mark.parametrize("K,N", [(256, 4096), (128, 1000), (64, 520)])
@@ -271,7 +292,7 @@ def test_pack_decode_stream_layout(K, N):
     rng = np.random.default_rng(K + N)
     qw = rng.integers(-2**31, 2**31 - 1, size=(K, N // 8), dtype=np.int64).astype(np.int32)
     got = ops.pack_decode_stream(torch.from_numpy(qw).to(DEV)).cpu().numpy()
-    assert np.array_equal(got, _stream_layout_numpy(qw, ops.DECODE_STREAM_WPL))
+    assert np.array_equal(got, _stream_layout_numpy(qw))
 
 
 @pytest.mark.parametrize("M,K,N,G", [(1, 2048, 5632, 128), (4, 4096, 6144, 128), (16, 1024, 1000, 64),
@@ -288,7 +309,7 @@ def test_gemm_decode_stream_vs_oracle(M, K, N, G, zp):
     y = ops.gemm(t["x"], t["qweight"], t["scales"], qz, G, layout="autoawq", decode_stream=True)
     y2 = ops.gemm(t["x"], t["qweight"], t["scales"], qz, G, layout="autoawq")
     assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
-    w = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"] if zp else None, G, zero_point=zp)
+    w = _w_used(p, M, G, zp=zp)
     _check_vs_exact(y.cpu().numpy(), O.linear_exact(p["x"], w.T), f"stream M={M} N={N}")
 
 
@@ -298,8 +319,7 @@ def test_decode_stream_split_k_bit_stable(M):
     K, N, G = 12288, 4096, 128
     p = make_awq_problem(M=M, K=K, N=N, group_size=G, seed=21)
     t = _to_dev(p)
-    w = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"], G)
-    ye = O.linear_exact(p["x"], w.T)
+    ye = O.linear_exact(p["x"], _w_used(p, M, G).T)
     for sk in (1, 4, 8):
         _note(f"stream split-K M={M} split={sk}")
         y1 = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, split_k=sk, layout="autoawq", decode_stream=True)

@@ -143,6 +143,31 @@ def test_dequant_single_rounding_exhaustive_q_z():
     assert not np.signbit(W.reshape(16, n_groups, G)[zero_mask]).any()
 
 
+def test_dequant_float32_is_the_exact_product():
+    """The unrounded operand (the fused path's M = 1 ``b``): every (q, z) pair against many
+    scales equals the float64 product exactly, and one fp16 rounding of it reproduces the
+    fp16 dequant bit for bit."""
+    scales = _scale_set()
+    G, n_groups = 16, 16
+    K = G * n_groups
+    Q = np.broadcast_to(np.tile(np.arange(16, dtype=np.int32), K // 16), (16, K)).copy()
+    Z = (np.arange(16)[:, None] + np.arange(n_groups)[None, :]) % 16
+    qw, qz = O.pack_ref(Q), O.pack_ref(Z.astype(np.int32))
+    for start in range(0, scales.size - 256 + 1, 256):
+        S = scales[start:start + 256].reshape(16, 16)
+        W32 = O.dequant_ref(qw, S, qz, G, out_dtype="float32")
+        exact = ((Q.reshape(16, n_groups, G) - Z[..., None]).astype(np.float64)
+                 * S.astype(np.float64)[..., None]).reshape(16, K)
+        assert W32.dtype == np.float32 and np.array_equal(W32.astype(np.float64), exact)
+        W16 = O.dequant_ref(qw, S, qz, G)
+        assert np.array_equal(W32.astype(np.float16).view(np.uint16), W16.view(np.uint16))
+    # the AutoAWQ unpack agrees with the reference one on the unrounded values too
+    p = make_awq_problem(M=1, K=256, N=64, group_size=32, seed=4)
+    qr, zr, sr = O.repack_awq_to_ref(p["qweight"], p["qzeros"], p["scales"])
+    assert np.array_equal(O.dequant_awq(p["qweight"], p["scales"], p["qzeros"], 32, out_dtype="float32"),
+                          O.dequant_ref(qr, sr, zr, 32, out_dtype="float32").T)
+
+
 def test_prescaled_zero_variant_is_caught():
     """Plants the classic mistake (q*s - z*s in fp16) and shows the exhaustive
     check above would reject it."""
