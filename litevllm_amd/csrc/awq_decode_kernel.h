@@ -5,8 +5,8 @@
 // (vllm/kernels/triton/awq_fused_gemm.py:1754-1990), built for HBM streaming on MI355X:
 //
 //  * Work unit = (column tile, k-step): a tile is 16 packed words (128 columns), a k-step 32
-//    rows.  Each tile's k-steps are cut into `splits` equal ranges, one per block, and a
-//    block's 8 waves take contiguous shares of its range, so a block never leaves its tile.
+//    rows.  Each tile's k-steps are cut into `splits` equal ranges, one per block, and the
+//    block's waves take contiguous shares of its range, so a block never leaves its tile.
 //  * Lane (q = lane / 16, r = lane % 16) owns word tile*16 + r and, per k-step, rows
 //    8q .. 8q+7.  For each nibble i the lane builds one 32 k x 16 column operand of
 //    v_mfma_f32_16x16x32_{f16,bf16} and multiplies the activations (16 tokens x 32 k) by it,
@@ -333,17 +333,20 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
 namespace awq_host {
 using namespace awq;
 
+// Blocks of 8 waves at two waves per SIMD; the M == 1 instantiation needs few enough
+// registers to run 16 waves at four per SIMD, which hides more of the memory latency.
 template <int MT, bool SEQ, bool ZP, typename T, bool SBF, bool STREAM, bool ONE>
 inline void launch_t(const GemmArgs& a, const DecodePlan& s, hipStream_t st) {
   const DecodeWork wk{s.tiles, s.ksteps, s.splits};
-  const dim3 grid((unsigned)s.blocks), block(8 * 64);
+  constexpr int NWV = ONE ? 16 : 8, OCC = ONE ? 4 : 2;
+  const dim3 grid((unsigned)s.blocks), block(NWV * 64);
   const int spg = a.G / 32;
   if (spg == 4)
-    hipLaunchKernelGGL((decode_kn_kernel<MT, 8, 2, 4, SEQ, ZP, T, SBF, STREAM, ONE, 2>), grid, block, 0, st, a, wk);
+    hipLaunchKernelGGL((decode_kn_kernel<MT, NWV, 2, 4, SEQ, ZP, T, SBF, STREAM, ONE, OCC>), grid, block, 0, st, a, wk);
   else if (spg == 2)
-    hipLaunchKernelGGL((decode_kn_kernel<MT, 8, 2, 2, SEQ, ZP, T, SBF, STREAM, ONE, 2>), grid, block, 0, st, a, wk);
+    hipLaunchKernelGGL((decode_kn_kernel<MT, NWV, 2, 2, SEQ, ZP, T, SBF, STREAM, ONE, OCC>), grid, block, 0, st, a, wk);
   else
-    hipLaunchKernelGGL((decode_kn_kernel<MT, 8, 2, 1, SEQ, ZP, T, SBF, STREAM, ONE, 2>), grid, block, 0, st, a, wk);
+    hipLaunchKernelGGL((decode_kn_kernel<MT, NWV, 2, 1, SEQ, ZP, T, SBF, STREAM, ONE, OCC>), grid, block, 0, st, a, wk);
 }
 
 // ONE selects the M == 1 instantiation (the f16 paths only; the others use the general one)
