@@ -46,9 +46,8 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
   static_assert(NWV >= 2 && (NWV & (NWV - 1)) == 0, "power-of-two waves per block");
   static_assert(!ONE || MT == 1, "");
   constexpr int NACC = 8 * MT;             // f32x4 accumulators per lane
-  constexpr int RED = (NWV / 2) * NACC * 64;  // floats (ONE) or f32x4 of the cross-wave tree
-  __shared__ f32x4 red4[ONE ? 1 : RED];
-  __shared__ float red1[ONE ? RED : 1];
+  __shared__ f32x4 red4[ONE ? 1 : (NWV / 2) * NACC * 64];  // the cross-wave tree
+  __shared__ float red1[ONE ? NWV * 128 : 1];              // M == 1: every wave's column sums
   __shared__ int s_last;
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -98,20 +97,23 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
     uint32_t zm[8];  // biased zeros of the current group
     float scf[8];    // scales of the current group
 
-    // Issue cursor over the wave's units, advanced one unit per issue.  After the last unit it
-    // keeps re-loading that unit with zero activations (their products add exact zeros), so
-    // every ring turn is a full one.  All per-unit index math is 32-bit scalar arithmetic.
+    // Issue cursor over the wave's units, advanced one unit per issue.  Past the last unit the
+    // ring's refills read out of the buffers' ranges (zeros, no memory traffic), so every ring
+    // turn is a whole one; all per-unit index math is 32-bit scalar arithmetic.
     int iks = w0, ileft = nunits;
-    bool ipast = false;
     auto issue = [&](int slot) {
       const int ks = iks;  // wave-uniform
+      const bool past = ileft <= 0;
+      ++iks;
+      --ileft;
+      const int oob = (int)0x80000000;  // a VGPR offset past every range
       if constexpr (STREAM) {
         // the unit's 2 KiB run; lane l's 16-byte piece e at byte 1024 e + 16 l
         const int kbase = (int)(((uint32_t)t * (uint32_t)KS + (uint32_t)ks) * 2048u);
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           const u32x4 v = __builtin_bit_cast(
-              u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, (int)w_lane_off, kbase + 1024 * e, 0));
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, past ? oob : (int)w_lane_off, kbase + 1024 * e, 0));
 #pragma unroll
           for (int c = 0; c < 4; ++c) raw[slot][4 * e + c] = v[c];
         }
@@ -120,23 +122,16 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
         const uint32_t kbase = (uint32_t)ks * 32u * row_bytes;
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-          raw[slot][j] = __builtin_amdgcn_raw_buffer_load_b32(wrs, (int)w_lane_off, (int)(kbase + (uint32_t)j * row_bytes), 0);
+          raw[slot][j] = __builtin_amdgcn_raw_buffer_load_b32(wrs, past ? oob : (int)w_lane_off, (int)(kbase + (uint32_t)j * row_bytes), 0);
       }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
-        xr[slot][mt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                     xrs, ipast ? (int)0x80000000 : (int)x_lane_off[mt], ks * 64, 0));
+        xr[slot][mt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, past ? oob : (int)x_lane_off[mt], ks * 64, 0));
       const int g = ks / SPG;
       sz[slot].s4 = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(srs, (int)(16u * wc), (int)((uint32_t)g * (uint32_t)p.N * 2u), 0));
-      sz[slot].zw = ZP ? __builtin_amdgcn_raw_buffer_load_b32(zrs, (int)(4u * wc), (int)((uint32_t)g * (uint32_t)NW * 4u), 0)
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(srs, past ? oob : (int)(16u * wc), (int)((uint32_t)g * (uint32_t)p.N * 2u), 0));
+      sz[slot].zw = ZP ? __builtin_amdgcn_raw_buffer_load_b32(zrs, past ? oob : (int)(4u * wc), (int)((uint32_t)g * (uint32_t)NW * 4u), 0)
                        : 0x88888888u;
-      if (ileft > 1) {
-        --ileft;
-        ++iks;
-      } else {
-        ipast = true;
-      }
     };
     auto compute = [&](int slot) {
       uint32_t mlo[4], mhi[4];
@@ -175,9 +170,6 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
     // bookkeeping of the unit being computed: its k-step and the group acc holds
     int cks = w0;
     int g_cur = -1;
-    // With one k-step per group every unit is a whole group: its constants are prepared, its
-    // MFMAs start from zero and its sum is scaled at once, with no state kept between units
-    // (the ring's zero-activation turns then add exact zeros).
     auto prep = [&](int slot) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -186,20 +178,19 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
         scf[i] = cc.scf;
       }
     };
-    auto step = [&](int done, int slot) {
+    // With one k-step per group every unit is a whole group: its constants are prepared, its
+    // MFMAs start from zero and its sum is scaled at once, with no state kept between units.
+    auto step = [&](int slot) {
       if constexpr (SPG == 1) {
         prep(slot);
         compute(slot);
         flush();
       } else {
-        if (done < nunits) {  // wave-uniform bookkeeping of real units
-          const int g = cks / SPG;
-          if (g != g_cur) {
-            if (g_cur >= 0) flush();
-            g_cur = g;
-            prep(slot);
-          }
-          ++cks;
+        const int g = cks++ / SPG;  // wave-uniform
+        if (g != g_cur) {
+          if (g_cur >= 0) flush();
+          g_cur = g;
+          prep(slot);
         }
         compute(slot);
       }
@@ -211,89 +202,116 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
     for (int done = 0; done < nunits; done += D) {
 #pragma unroll
       for (int u = 0; u < D; ++u) {
-        step(done + u, u);
+        if (done + u < nunits) step(u);  // wave-uniform: the last turn may hold fewer units
         __builtin_amdgcn_sched_barrier(0);
         issue(u);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    if constexpr (SPG > 1) flush();  // the last group (the ring's zero-activation turns added exact zeros)
+    if constexpr (SPG > 1) flush();  // the last group
   }
 
-  // ---- the waves' sums meet in LDS, fixed tree order: ((w0 + w4) + (w2 + w6)) + ... ----
-#pragma unroll
-  for (int half = NWV / 2; half >= 1; half >>= 1) {
-    if (wave >= half && wave < 2 * half) {
-#pragma unroll
-      for (int c = 0; c < NACC; ++c) {
-        if constexpr (ONE) red1[((wave - half) * NACC + c) * 64 + lane] = tot1[c];
-        else red4[((wave - half) * NACC + c) * 64 + lane] = tot[c / MT][c % MT];
-      }
-    }
-    __syncthreads();
-    if (wave < half) {
-#pragma unroll
-      for (int c = 0; c < NACC; ++c) {
-        if constexpr (ONE) tot1[c] += red1[(wave * NACC + c) * 64 + lane];
-        else tot[c / MT][c % MT] += red4[(wave * NACC + c) * 64 + lane];
-      }
-    }
-    __syncthreads();
-  }
-
-  // ---- outputs ----
-  // lane (q, r) of wave 0 holds, for accumulator [i][mt] element v, token mt*16 + 4q + v and
-  // column 8 * word + nib_col(i).
-  constexpr int NV = ONE ? 1 : 4;
   const int M = p.M;
   const int tile_floats = M * 128;  // one partial: [M, 128] fp32
-  auto cols_of = [&](int mt, int v, float (&o)[8]) {
-#pragma unroll
-    for (int c = 0; c < 8; ++c) o[c] = ONE ? tot1[col_nib<SEQ>(c)] : tot[col_nib<SEQ>(c)][mt][v];
-  };
-  if (S == 1) {
-    if (wave != 0 || word >= NW) return;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int v = 0; v < NV; ++v) {
-        const int m = mt * 16 + 4 * q + v;
-        if (m >= M) continue;
-        float o[8];
-        cols_of(mt, v, o);
-        if (p.bias) {
-#pragma unroll
-          for (int c = 0; c < 8; ++c) o[c] += load_bias(p.bias, p.bias_dtype, 8 * word + c);
-        }
-        u32x4 st;
-        st[0] = pack2<T>(o[0], o[1]);
-        st[1] = pack2<T>(o[2], o[3]);
-        st[2] = pack2<T>(o[4], o[5]);
-        st[3] = pack2<T>(o[6], o[7]);
-        *(u32x4*)(p.c + (int64_t)m * p.ldc + 8 * word) = st;
-      }
-    return;
-  }
   // partial (t, part): [M][128] floats, columns relative to the tile
   const __amdgpu_buffer_rsrc_t prs = make_rsrc(p.partial, (uint32_t)wk.tiles * (uint32_t)S * (uint32_t)tile_floats * 4u);
   const uint32_t tbase = (uint32_t)t * (uint32_t)S * (uint32_t)tile_floats * 4u;
-  if (wave == 0) {
-    const uint32_t base = tbase + (uint32_t)part * (uint32_t)tile_floats * 4u;
+  const uint32_t pbase = tbase + (uint32_t)part * (uint32_t)tile_floats * 4u;
+
+  if constexpr (ONE) {
+    // ---- M == 1: lanes q = 0 hold the token.  Every wave parks its 128 column sums in LDS
+    // and wave 0 adds them in wave order (fixed), lane l taking columns 2l and 2l + 1. ----
+    if (q == 0) {
+      float o[8];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+      for (int c = 0; c < 8; ++c) o[c] = tot1[col_nib<SEQ>(c)];
+      *(f32x4*)&red1[wave * 128 + 8 * r] = f32x4{o[0], o[1], o[2], o[3]};
+      *(f32x4*)&red1[wave * 128 + 8 * r + 4] = f32x4{o[4], o[5], o[6], o[7]};
+    }
+    __syncthreads();
+    if (wave == 0) {
+      f32x2 sum = *(const f32x2*)&red1[2 * lane];
 #pragma unroll
-      for (int v = 0; v < NV; ++v) {
-        const int m = mt * 16 + 4 * q + v;
-        if (m >= M) continue;
-        float o[8];
-        cols_of(mt, v, o);
-        const uint32_t off = base + ((uint32_t)m * 128u + 8u * (uint32_t)r) * 4u;
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, f32x4{o[0], o[1], o[2], o[3]}), prs, (int)off, 0, kDeviceCoherent);
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, f32x4{o[4], o[5], o[6], o[7]}), prs, (int)(off + 16u), 0, kDeviceCoherent);
+      for (int w = 1; w < NWV; ++w) sum += *(const f32x2*)&red1[w * 128 + 2 * lane];
+      const int col = t * 128 + 2 * lane;
+      if (S == 1) {
+        if (col < p.N) {
+          if (p.bias) {
+            sum[0] += load_bias(p.bias, p.bias_dtype, col);
+            sum[1] += load_bias(p.bias, p.bias_dtype, col + 1);
+          }
+          *(uint32_t*)(p.c + col) = pack2<T>(sum[0], sum[1]);
+        }
+      } else {
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, sum), prs, (int)(pbase + 8u * (uint32_t)lane), 0,
+                                              kDeviceCoherent);
+        __builtin_amdgcn_s_waitcnt(0);  // the partial stores have completed (device scope)
+        if (lane == 0)
+          s_last = __hip_atomic_fetch_add(&p.counters[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
       }
-    __builtin_amdgcn_s_waitcnt(0);  // the partial stores have completed (device scope)
-    if (lane == 0)
-      s_last = __hip_atomic_fetch_add(&p.counters[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+    }
+    if (S == 1) return;
+  } else {
+    // ---- the waves' sums meet in LDS, fixed tree order: ((w0 + w4) + (w2 + w6)) + ... ----
+#pragma unroll
+    for (int half = NWV / 2; half >= 1; half >>= 1) {
+      if (wave >= half && wave < 2 * half) {
+#pragma unroll
+        for (int c = 0; c < NACC; ++c) red4[((wave - half) * NACC + c) * 64 + lane] = tot[c / MT][c % MT];
+      }
+      __syncthreads();
+      if (wave < half) {
+#pragma unroll
+        for (int c = 0; c < NACC; ++c) tot[c / MT][c % MT] += red4[(wave * NACC + c) * 64 + lane];
+      }
+      __syncthreads();
+    }
+    // lane (q, r) of wave 0 holds, for accumulator [i][mt] element v, token mt*16 + 4q + v and
+    // column 8 * word + nib_col(i).
+    auto cols_of = [&](int mt, int v, float (&o)[8]) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) o[c] = tot[col_nib<SEQ>(c)][mt][v];
+    };
+    if (S == 1) {
+      if (wave != 0 || word >= NW) return;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int m = mt * 16 + 4 * q + v;
+          if (m >= M) continue;
+          float o[8];
+          cols_of(mt, v, o);
+          if (p.bias) {
+#pragma unroll
+            for (int c = 0; c < 8; ++c) o[c] += load_bias(p.bias, p.bias_dtype, 8 * word + c);
+          }
+          u32x4 st;
+          st[0] = pack2<T>(o[0], o[1]);
+          st[1] = pack2<T>(o[2], o[3]);
+          st[2] = pack2<T>(o[4], o[5]);
+          st[3] = pack2<T>(o[6], o[7]);
+          *(u32x4*)(p.c + (int64_t)m * p.ldc + 8 * word) = st;
+        }
+      return;
+    }
+    if (wave == 0) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int m = mt * 16 + 4 * q + v;
+          if (m >= M) continue;
+          float o[8];
+          cols_of(mt, v, o);
+          const uint32_t off = pbase + ((uint32_t)m * 128u + 8u * (uint32_t)r) * 4u;
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, f32x4{o[0], o[1], o[2], o[3]}), prs, (int)off, 0, kDeviceCoherent);
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, f32x4{o[4], o[5], o[6], o[7]}), prs, (int)(off + 16u), 0, kDeviceCoherent);
+        }
+      __builtin_amdgcn_s_waitcnt(0);  // the partial stores have completed (device scope)
+      if (lane == 0)
+        s_last = __hip_atomic_fetch_add(&p.counters[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+    }
   }
   __syncthreads();
   if (!s_last) return;
