@@ -7,8 +7,8 @@ namespace awq_host {
 using namespace awq;
 
 // ---- planning ----
-// Each tile's K/32 k-steps are cut into `splits` equal ranges, one block each (8 waves at two
-// per SIMD, or 16 at four per SIMD when M == 1; a two-deep ring).  By default splits = CUs / tiles (at least 1), so one round of
+// Each tile's K/32 k-steps are cut into `splits` equal ranges, one block each (16 waves at
+// four per SIMD for M <= 16, 8 at two per SIMD above; a two-deep ring).  By default splits = CUs / tiles (at least 1), so one round of
 // blocks covers the chip and no block leaves its tile; split_k > 0 asks for that many
 // ranges (capped at the k-step count).
 DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t G, int split_k, DecodeMode mode) {

@@ -45,9 +45,8 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
   static_assert((SPG & (SPG - 1)) == 0, "");
   static_assert(NWV >= 2 && (NWV & (NWV - 1)) == 0, "power-of-two waves per block");
   static_assert(!ONE || MT == 1, "");
-  constexpr int NACC = 8 * MT;             // f32x4 accumulators per lane
-  __shared__ f32x4 red4[ONE ? 1 : (NWV / 2) * NACC * 64];  // the cross-wave tree
-  __shared__ float red1[ONE ? NWV * 128 : 1];              // M == 1: every wave's column sums
+  constexpr int MROWS = ONE ? 1 : 16 * MT;  // token rows a wave can hold
+  __shared__ float red[NWV * MROWS * 128];  // every wave's sums: [wave][token][tile column]
   __shared__ int s_last;
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -95,7 +94,7 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
     u32x4 xr[D][MT];
     WordSZ sz[D];    // raw constants of each slot's group (used when the group changes)
     uint32_t zm[8];  // biased zeros of the current group
-    float scf[8];    // scales of the current group
+    u32x4 s4;        // scales of the current group (the word's 8 columns, raw 16-bit values)
 
     // Issue cursor over the wave's units, advanced one unit per issue.  Past the last unit the
     // ring's refills read out of the buffers' ranges (zeros, no memory traffic), so every ring
@@ -162,8 +161,11 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
       for (int i = 0; i < 8; ++i)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          if constexpr (ONE) tot1[i] += acc[i][mt][0] * scf[i];
-          else tot[i][mt] += acc[i][mt] * scf[i];
+          const int c = nib_col<SEQ>(i);
+          const uint16_t sb = (uint16_t)(s4[c >> 1] >> (16 * (c & 1)));
+          const float sf = SBF ? bf_bits2f(sb) : h_bits2f(sb);
+          if constexpr (ONE) tot1[i] += acc[i][mt][0] * sf;
+          else tot[i][mt] += acc[i][mt] * sf;
           if constexpr (SPG > 1) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
     };
@@ -172,11 +174,8 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
     int g_cur = -1;
     auto prep = [&](int slot) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const ColConst cc = prep_const_int<SEQ, SBF>(sz[slot], i);
-        zm[i] = cc.zm;
-        scf[i] = cc.scf;
-      }
+      for (int i = 0; i < 8; ++i) zm[i] = zero_magic(i & 1, (sz[slot].zw >> (4 * i)) & 0xF);
+      s4 = sz[slot].s4;
     };
     // With one k-step per group every unit is a whole group: its constants are prepared, its
     // MFMAs start from zero and its sum is scaled at once, with no state kept between units.
@@ -218,107 +217,49 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
   const uint32_t tbase = (uint32_t)t * (uint32_t)S * (uint32_t)tile_floats * 4u;
   const uint32_t pbase = tbase + (uint32_t)part * (uint32_t)tile_floats * 4u;
 
-  if constexpr (ONE) {
-    // ---- M == 1: lanes q = 0 hold the token.  Every wave parks its 128 column sums in LDS
-    // and wave 0 adds them in wave order (fixed), lane l taking columns 2l and 2l + 1. ----
-    if (q == 0) {
+  // ---- the waves' sums meet in LDS: lane (q, r) holds, for accumulator [i][mt] element v,
+  // token mt*16 + 4q + v of column 8 r + nib_col(i); every wave parks its real tokens, then
+  // each output is summed over the waves in wave order (fixed, so results are reproducible).
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int v = 0; v < (ONE ? 1 : 4); ++v) {
+      const int m = mt * 16 + 4 * q + v;
+      if (m >= M) continue;
       float o[8];
 #pragma unroll
-      for (int c = 0; c < 8; ++c) o[c] = tot1[col_nib<SEQ>(c)];
-      *(f32x4*)&red1[wave * 128 + 8 * r] = f32x4{o[0], o[1], o[2], o[3]};
-      *(f32x4*)&red1[wave * 128 + 8 * r + 4] = f32x4{o[4], o[5], o[6], o[7]};
+      for (int c = 0; c < 8; ++c) o[c] = ONE ? tot1[col_nib<SEQ>(c)] : tot[col_nib<SEQ>(c)][mt][v];
+      float* dst = &red[(wave * MROWS + m) * 128 + 8 * r];
+      *(f32x4*)dst = f32x4{o[0], o[1], o[2], o[3]};
+      *(f32x4*)(dst + 4) = f32x4{o[4], o[5], o[6], o[7]};
     }
-    __syncthreads();
-    if (wave == 0) {
-      f32x2 sum = *(const f32x2*)&red1[2 * lane];
+  __syncthreads();
+  const int ncols = min(128, p.N - t * 128);
+  for (int o = tid; o < M * 128; o += NWV * 64) {
+    const int m = o >> 7, col = o & 127;
+    float sum = red[m * 128 + col];
 #pragma unroll
-      for (int w = 1; w < NWV; ++w) sum += *(const f32x2*)&red1[w * 128 + 2 * lane];
-      const int col = t * 128 + 2 * lane;
-      if (S == 1) {
-        if (col < p.N) {
-          if (p.bias) {
-            sum[0] += load_bias(p.bias, p.bias_dtype, col);
-            sum[1] += load_bias(p.bias, p.bias_dtype, col + 1);
-          }
-          *(uint32_t*)(p.c + col) = pack2<T>(sum[0], sum[1]);
-        }
-      } else {
-        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, sum), prs, (int)(pbase + 8u * (uint32_t)lane), 0,
-                                              kDeviceCoherent);
-        __builtin_amdgcn_s_waitcnt(0);  // the partial stores have completed (device scope)
-        if (lane == 0)
-          s_last = __hip_atomic_fetch_add(&p.counters[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
-      }
-    }
-    if (S == 1) return;
-  } else {
-    // ---- the waves' sums meet in LDS, fixed tree order: ((w0 + w4) + (w2 + w6)) + ... ----
-#pragma unroll
-    for (int half = NWV / 2; half >= 1; half >>= 1) {
-      if (wave >= half && wave < 2 * half) {
-#pragma unroll
-        for (int c = 0; c < NACC; ++c) red4[((wave - half) * NACC + c) * 64 + lane] = tot[c / MT][c % MT];
-      }
-      __syncthreads();
-      if (wave < half) {
-#pragma unroll
-        for (int c = 0; c < NACC; ++c) tot[c / MT][c % MT] += red4[(wave * NACC + c) * 64 + lane];
-      }
-      __syncthreads();
-    }
-    // lane (q, r) of wave 0 holds, for accumulator [i][mt] element v, token mt*16 + 4q + v and
-    // column 8 * word + nib_col(i).
-    auto cols_of = [&](int mt, int v, float (&o)[8]) {
-#pragma unroll
-      for (int c = 0; c < 8; ++c) o[c] = tot[col_nib<SEQ>(c)][mt][v];
-    };
+    for (int w = 1; w < NWV; ++w) sum += red[(w * MROWS + m) * 128 + col];
     if (S == 1) {
-      if (wave != 0 || word >= NW) return;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int m = mt * 16 + 4 * q + v;
-          if (m >= M) continue;
-          float o[8];
-          cols_of(mt, v, o);
-          if (p.bias) {
-#pragma unroll
-            for (int c = 0; c < 8; ++c) o[c] += load_bias(p.bias, p.bias_dtype, 8 * word + c);
-          }
-          u32x4 st;
-          st[0] = pack2<T>(o[0], o[1]);
-          st[1] = pack2<T>(o[2], o[3]);
-          st[2] = pack2<T>(o[4], o[5]);
-          st[3] = pack2<T>(o[6], o[7]);
-          *(u32x4*)(p.c + (int64_t)m * p.ldc + 8 * word) = st;
-        }
-      return;
-    }
-    if (wave == 0) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int m = mt * 16 + 4 * q + v;
-          if (m >= M) continue;
-          float o[8];
-          cols_of(mt, v, o);
-          const uint32_t off = pbase + ((uint32_t)m * 128u + 8u * (uint32_t)r) * 4u;
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, f32x4{o[0], o[1], o[2], o[3]}), prs, (int)off, 0, kDeviceCoherent);
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, f32x4{o[4], o[5], o[6], o[7]}), prs, (int)(off + 16u), 0, kDeviceCoherent);
-        }
-      __builtin_amdgcn_s_waitcnt(0);  // the partial stores have completed (device scope)
-      if (lane == 0)
-        s_last = __hip_atomic_fetch_add(&p.counters[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+      if (col < ncols) {
+        if (p.bias) sum += load_bias(p.bias, p.bias_dtype, t * 128 + col);
+        p.c[(int64_t)m * p.ldc + t * 128 + col] = to_bits<T>(sum);
+      }
+    } else {
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, sum), prs, (int)(pbase + 4u * (uint32_t)o), 0,
+                                            kDeviceCoherent);
     }
   }
+  if (S == 1) return;
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed (device scope)
+  __syncthreads();                // ... and every thread's
+  if (tid == 0)
+    s_last = __hip_atomic_fetch_add(&p.counters[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
   __syncthreads();
   if (!s_last) return;
   // the last of the S blocks of tile t sums the partials in split (k) order, adds the bias
   // and writes the output (all threads of the block)
   const uint32_t pstride = (uint32_t)tile_floats * 4u;  // bytes between splits
-  const int ncols = min(128, p.N - t * 128);
   const int nh = ncols >> 1;  // float2 chunks per row
   for (int idx = tid; idx < M * nh; idx += NWV * 64) {
     const int m = idx / nh, ch = idx - m * nh;
@@ -351,12 +292,12 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
 namespace awq_host {
 using namespace awq;
 
-// Blocks of 8 waves at two waves per SIMD; the M == 1 instantiation needs few enough
-// registers to run 16 waves at four per SIMD, which hides more of the memory latency.
+// One 16-token tile (M <= 16) needs few enough registers to run blocks of 16 waves at four
+// per SIMD, which hides more of the memory latency; two tiles run 8 waves at two per SIMD.
 template <int MT, bool SEQ, bool ZP, typename T, bool SBF, bool STREAM, bool ONE>
 inline void launch_t(const GemmArgs& a, const DecodePlan& s, hipStream_t st) {
   const DecodeWork wk{s.tiles, s.ksteps, s.splits};
-  constexpr int NWV = ONE ? 16 : 8, OCC = ONE ? 4 : 2;
+  constexpr int NWV = MT == 1 ? 16 : 8, OCC = MT == 1 ? 4 : 2;
   const dim3 grid((unsigned)s.blocks), block(NWV * 64);
   const int spg = a.G / 32;
   if (spg == 4)
