@@ -76,15 +76,14 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
   const uint32_t row_bytes = (uint32_t)NW * 4u;
   if (nunits > 0) {
     const uint32_t w_bytes = STREAM ? (uint32_t)wk.tiles * (uint32_t)KS * 2048u : (uint32_t)p.K * row_bytes;
-    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(p.qw, w_bytes);
-    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(p.a, (uint32_t)((uint64_t)p.M * (uint64_t)p.lda * 2u));
+    const uint32_t x_bytes = (uint32_t)((uint64_t)p.M * (uint64_t)p.lda * 2u);
+    const uint32_t s_bytes = (uint32_t)((uint64_t)ngroups * p.N * 2u);
+    const uint32_t z_bytes = ZP ? (uint32_t)((uint64_t)ngroups * NW * 4u) : 0u;
     // the whole activation row offset rides in the VGPR offset, so rows >= M read as zero
     uint32_t x_lane_off[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
       x_lane_off[mt] = ((uint32_t)(mt * 16 + r) * (uint32_t)p.lda + 8u * (uint32_t)q) * 2u;
-    const __amdgpu_buffer_rsrc_t srs = make_rsrc(p.sc, (uint32_t)((uint64_t)ngroups * p.N * 2u));
-    const __amdgpu_buffer_rsrc_t zrs = make_rsrc(p.qz, ZP ? (uint32_t)((uint64_t)ngroups * NW * 4u) : 0u);
     const MagicK mk = magic_consts();
     // per-column clamp (columns past N are computed, never stored)
     const uint32_t wc = (uint32_t)min(word, NW - 1);
@@ -97,22 +96,25 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
     u32x4 s4;        // scales of the current group (the word's 8 columns, raw 16-bit values)
 
     // Issue cursor over the wave's units, advanced one unit per issue.  Past the last unit the
-    // ring's refills read out of the buffers' ranges (zeros, no memory traffic), so every ring
-    // turn is a whole one; all per-unit index math is 32-bit scalar arithmetic.
+    // ring's refills go through empty buffer descriptors (zeros, no memory traffic), so every
+    // ring turn is a whole one; all per-unit index math is 32-bit scalar arithmetic.
     int iks = w0, ileft = nunits;
     auto issue = [&](int slot) {
       const int ks = iks;  // wave-uniform
       const bool past = ileft <= 0;
       ++iks;
       --ileft;
-      const int oob = (int)0x80000000;  // a VGPR offset past every range
+      const __amdgpu_buffer_rsrc_t wrs = make_rsrc(p.qw, past ? 0u : w_bytes);
+      const __amdgpu_buffer_rsrc_t xrs = make_rsrc(p.a, past ? 0u : x_bytes);
+      const __amdgpu_buffer_rsrc_t srs = make_rsrc(p.sc, past ? 0u : s_bytes);
+      const __amdgpu_buffer_rsrc_t zrs = make_rsrc(p.qz, past ? 0u : z_bytes);
       if constexpr (STREAM) {
         // the unit's 2 KiB run; lane l's 16-byte piece e at byte 1024 e + 16 l
         const int kbase = (int)(((uint32_t)t * (uint32_t)KS + (uint32_t)ks) * 2048u);
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           const u32x4 v = __builtin_bit_cast(
-              u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, past ? oob : (int)w_lane_off, kbase + 1024 * e, 0));
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, (int)w_lane_off, kbase + 1024 * e, 0));
 #pragma unroll
           for (int c = 0; c < 4; ++c) raw[slot][4 * e + c] = v[c];
         }
@@ -121,18 +123,20 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
         const uint32_t kbase = (uint32_t)ks * 32u * row_bytes;
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-          raw[slot][j] = __builtin_amdgcn_raw_buffer_load_b32(wrs, past ? oob : (int)w_lane_off, (int)(kbase + (uint32_t)j * row_bytes), 0);
+          raw[slot][j] = __builtin_amdgcn_raw_buffer_load_b32(wrs, (int)w_lane_off, (int)(kbase + (uint32_t)j * row_bytes), 0);
       }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
-        xr[slot][mt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, past ? oob : (int)x_lane_off[mt], ks * 64, 0));
+        xr[slot][mt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)x_lane_off[mt], ks * 64, 0));
       const int g = ks / SPG;
       sz[slot].s4 = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(srs, past ? oob : (int)(16u * wc), (int)((uint32_t)g * (uint32_t)p.N * 2u), 0));
-      sz[slot].zw = ZP ? __builtin_amdgcn_raw_buffer_load_b32(zrs, past ? oob : (int)(4u * wc), (int)((uint32_t)g * (uint32_t)NW * 4u), 0)
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(srs, (int)(16u * wc), (int)((uint32_t)g * (uint32_t)p.N * 2u), 0));
+      sz[slot].zw = ZP ? __builtin_amdgcn_raw_buffer_load_b32(zrs, (int)(4u * wc), (int)((uint32_t)g * (uint32_t)NW * 4u), 0)
                        : 0x88888888u;
     };
-    auto compute = [&](int slot) {
+    // FRESH: the group's first unit (its MFMAs start from zero)
+    auto compute = [&](int slot, auto fresh) {
+      constexpr bool FRESH = decltype(fresh)::value;
       uint32_t mlo[4], mhi[4];
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
@@ -148,15 +152,14 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
       {                                                                                        \
         const u32x4 op = int_operand<I, T>(mlo, mhi, zm[I], mk);                               \
         _Pragma("unroll") for (int mt = 0; mt < MT; ++mt)                                      \
-            acc[I][mt] = MfmaOp<T>::run(xr[slot][mt], op, SPG == 1 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[I][mt]); \
+            acc[I][mt] = MfmaOp<T>::run(xr[slot][mt], op, FRESH ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[I][mt]); \
       }
       AWQ_DECODE_NIB(0) AWQ_DECODE_NIB(1) AWQ_DECODE_NIB(2) AWQ_DECODE_NIB(3)
       AWQ_DECODE_NIB(4) AWQ_DECODE_NIB(5) AWQ_DECODE_NIB(6) AWQ_DECODE_NIB(7)
 #undef AWQ_DECODE_NIB
     };
-    // tot += acc * scale of the group just finished; acc restarts from zero (with one k-step
-    // per group every unit's MFMAs start from zero instead)
-    auto flush = [&]() {
+    // tot += acc * scale of the group just finished (ZERO: acc restarts from zero)
+    auto flush = [&](auto zero) {
 #pragma unroll
       for (int i = 0; i < 8; ++i)
 #pragma unroll
@@ -166,48 +169,66 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
           const float sf = SBF ? bf_bits2f(sb) : h_bits2f(sb);
           if constexpr (ONE) tot1[i] += acc[i][mt][0] * sf;
           else tot[i][mt] += acc[i][mt] * sf;
-          if constexpr (SPG > 1) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+          if constexpr (decltype(zero)::value) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
     };
-    // bookkeeping of the unit being computed: its k-step and the group acc holds
-    int cks = w0;
-    int g_cur = -1;
     auto prep = [&](int slot) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) zm[i] = zero_magic(i & 1, (sz[slot].zw >> (4 * i)) & 0xF);
       s4 = sz[slot].s4;
     };
-    // With one k-step per group every unit is a whole group: its constants are prepared, its
-    // MFMAs start from zero and its sum is scaled at once, with no state kept between units.
-    auto step = [&](int slot) {
-      if constexpr (SPG == 1) {
-        prep(slot);
-        compute(slot);
-        flush();
-      } else {
-        const int g = cks++ / SPG;  // wave-uniform
-        if (g != g_cur) {
-          if (g_cur >= 0) flush();
-          g_cur = g;
-          prep(slot);
-        }
-        compute(slot);
-      }
-    };
 
 #pragma unroll
     for (int u = 0; u < D; ++u) issue(u);
     __builtin_amdgcn_sched_barrier(0);
-    for (int done = 0; done < nunits; done += D) {
+    static_assert(D == 2 && (SPG == 1 || SPG % D == 0), "");
+    // (one tile of 16 tokens at four waves per SIMD has no registers to spare for it)
+    constexpr bool kGroupLoop = SPG > 1 && (ONE || MT > 1);
+    if (kGroupLoop && (w0 % SPG) == 0 && (nunits % SPG) == 0) {
+      // whole groups (the usual case): one group per iteration, its first unit in slot 0, so
+      // the MFMAs of that unit start from zero and nothing but tot is carried between groups
+      for (int done = 0; done < nunits; done += SPG) {
+        prep(0);
 #pragma unroll
-      for (int u = 0; u < D; ++u) {
-        if (done + u < nunits) step(u);  // wave-uniform: the last turn may hold fewer units
-        __builtin_amdgcn_sched_barrier(0);
-        issue(u);
-        __builtin_amdgcn_sched_barrier(0);
+        for (int u = 0; u < SPG; ++u) {
+          if (u == 0) compute(0, std::true_type{});
+          else compute(u % D, std::false_type{});
+          __builtin_amdgcn_sched_barrier(0);
+          issue(u % D);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        flush(std::false_type{});
       }
+    } else {
+      // shares that start or end inside a group; with one k-step per group every unit is a
+      // whole group (prepared, started from zero and scaled at once)
+      int cks = w0;
+      int g_cur = -1;
+      for (int done = 0; done < nunits; done += D) {
+#pragma unroll
+        for (int u = 0; u < D; ++u) {
+          if (done + u < nunits) {  // wave-uniform: the last turn may hold fewer units
+            if constexpr (SPG == 1) {
+              prep(u);
+              compute(u, std::true_type{});
+              flush(std::false_type{});
+            } else {
+              const int g = cks++ / SPG;
+              if (g != g_cur) {
+                if (g_cur >= 0) flush(std::true_type{});
+                g_cur = g;
+                prep(u);
+              }
+              compute(u, std::false_type{});
+            }
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          issue(u);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      if (SPG > 1 && g_cur >= 0) flush(std::false_type{});  // the last group
     }
-    if constexpr (SPG > 1) flush();  // the last group
   }
 
   const int M = p.M;
