@@ -103,8 +103,11 @@ int awq_w4a16_dequant(const int32_t* qweight, const void* scales, const int32_t*
 size_t awq_w4a16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_size,
                                       int32_t split_k, int32_t layout);
 
-/* C[M, N] = A[M, K] . dequant(W)^T (+ bias), W dequantized exactly as awq_w4a16_dequant
- * does for act_dtype, products accumulated in fp32, one rounding to act_dtype at the end.
+/* C[M, N] = A[M, K] . dequant(W)^T (+ bias), products accumulated in fp32, one rounding to
+ * act_dtype at the end.  M <= 32 with group_size 32, 64 or 128 (the decode kernel): the
+ * weights enter unrounded, (q - z) * s in fp32 -- the reference's M = 1 formulation,
+ * awq_fused_gemm.py:1966-1971.  Otherwise (the prefill kernel): W rounded once to act_dtype,
+ * as awq_w4a16_dequant computes it (the reference's tl.dot branch, 1973-1976).
  *   a: [M, K] act_dtype (F16 or BF16), row stride lda (elements).
  *   layout: AUTOAWQ or KN_SEQ (qweight [K, N/8]), or DECODE_STREAM (M <= 32).  An NK_SEQ
  *           weight is converted once with awq_w4a16_repack_nk_to_autoawq; passing NK_SEQ
@@ -112,10 +115,11 @@ size_t awq_w4a16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t g
  *   qzeros == NULL: symmetric z = 8.  scales: scale_dtype (F16 or BF16).
  *   bias: NULL or [N] of bias_dtype (F16, BF16 or F32), added once in fp32.
  *   c: [M, N] act_dtype, row stride ldc.
- *   split_k: number of contiguous K partitions whose fp32 partial sums are added in a fixed
- *            order (0 = choose automatically).  For a given (M, N, K, split_k) the result is
- *            bitwise reproducible.  Partition s covers k-steps [s*I, (s+1)*I) with
- *            I = ceil(steps / split_k), as in awq_fused_gemm.py:1799-1801.
+ *   split_k: number of contiguous K partitions of the decode kernel whose fp32 partial sums
+ *            are added in a fixed order (0 = choose automatically; the prefill kernel does
+ *            not split K).  For a given (M, N, K, split_k) the result is bitwise
+ *            reproducible.  Partition s covers rows [64 s I, min(64 (s+1) I, K)) with
+ *            I = ceil(ceil(K / 64) / split_k), as in awq_fused_gemm.py:1798-1800.
  *   Requirements: N % 8 == 0, group_size % 32 == 0, K % group_size == 0.
  */
 int awq_w4a16_gemm(const void* a, int64_t lda, const int32_t* qweight, const void* scales,

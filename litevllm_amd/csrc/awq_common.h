@@ -154,9 +154,10 @@ struct GemmArgs {
 };
 
 // Work decomposition of the decode kernel: tiles x ksteps units; each tile's k-steps are cut
-// into `splits` ranges, one block each (block b: tile b / splits, range b % splits).
+// into `splits` ranges of `per` k-steps (the last ones shorter or empty), one block each
+// (block b: tile b / splits, range b % splits).
 struct DecodeWork {
-  int tiles, ksteps, splits;
+  int tiles, ksteps, splits, per;
 };
 
 // Raw per-group constants of one packed word: 8 scales (16 bytes) and the zero word.

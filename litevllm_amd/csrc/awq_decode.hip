@@ -7,10 +7,12 @@ namespace awq_host {
 using namespace awq;
 
 // ---- planning ----
-// Each tile's K/32 k-steps are cut into `splits` equal ranges, one block each (16 waves at
-// four per SIMD for M <= 16, 8 at two per SIMD above; a two-deep ring).  By default splits = CUs / tiles (at least 1), so one round of
-// blocks covers the chip and no block leaves its tile; split_k > 0 asks for that many
-// ranges (capped at the k-step count).
+// Each tile's K is cut into `splits` ranges by the reference's split-K rule
+// (awq_fused_gemm.py:1798-1800, BLOCK_K = 64): ceil(ceil(K / 64) / splits) blocks of 64 rows
+// per range, the last ones shorter or empty, one block of waves each (16 waves at four per
+// SIMD for M <= 16, 8 at two per SIMD above; a two-deep ring).  By default splits = CUs /
+// tiles (at least 1, at most one 64-row block each), so one round of blocks covers the chip;
+// split_k > 0 asks for that many ranges.
 DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t G, int split_k, DecodeMode mode) {
   (void)G;
   (void)mode;
@@ -18,10 +20,12 @@ DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t G, int split_k, 
   s.mt = (M > 16) ? 2 : 1;
   s.tiles = (int)cdiv(N / 8, 16);
   s.ksteps = (int)(K / 32);
-  const int64_t KS = s.ksteps;
-  const int64_t splits = split_k > 0 ? std::min<int64_t>(split_k, KS)
-                                     : std::min<int64_t>(KS, std::max<int64_t>(1, (int64_t)num_cus() / s.tiles));
+  const int64_t kb = cdiv(K, 64);  // 64-row blocks
+  // past one 64-row block per range the reference's extra ranges are empty: not launched
+  const int64_t splits = std::min<int64_t>(kb, split_k > 0 ? (int64_t)split_k
+                                                           : std::max<int64_t>(1, (int64_t)num_cus() / s.tiles));
   s.splits = (int)splits;
+  s.per = (int)(2 * cdiv(kb, splits));
   s.blocks = (int)((int64_t)s.tiles * splits);
   s.ws_bytes = splits > 1 ? kCounterBytes + (size_t)s.tiles * (size_t)splits * (size_t)M * 128 * sizeof(float) : 0;
   return s;

@@ -5,8 +5,9 @@
 // (vllm/kernels/triton/awq_fused_gemm.py:1754-1990), built for HBM streaming on MI355X:
 //
 //  * Work unit = (column tile, k-step): a tile is 16 packed words (128 columns), a k-step 32
-//    rows.  Each tile's k-steps are cut into `splits` equal ranges, one per block, and the
-//    block's waves take contiguous shares of its range, so a block never leaves its tile.
+//    rows.  Each tile's k-steps are cut into `splits` ranges (the reference's split-K rule),
+//    one per block, and the block's waves take contiguous shares of its range, so a block
+//    never leaves its tile.
 //  * Lane (q = lane / 16, r = lane % 16) owns word tile*16 + r and, per k-step, rows
 //    8q .. 8q+7.  For each nibble i the lane builds one 32 k x 16 column operand of
 //    v_mfma_f32_16x16x32_{f16,bf16} and multiplies the activations (16 tokens x 32 k) by it,
@@ -56,7 +57,7 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
   const int KS = wk.ksteps, S = wk.splits;
   const int t = (int)blockIdx.x / S, part = (int)blockIdx.x - t * S;
   // the block's k-step range of tile t, then this wave's contiguous share of it
-  const int k0 = (int)((int64_t)KS * part / S), k1 = (int)((int64_t)KS * (part + 1) / S);
+  const int k0 = min(part * wk.per, KS), k1 = min(k0 + wk.per, KS);
   const int len = k1 - k0;
   const int w0 = k0 + len * wave / NWV;
   const int nunits = k0 + len * (wave + 1) / NWV - w0;
@@ -317,7 +318,7 @@ using namespace awq;
 // per SIMD, which hides more of the memory latency; two tiles run 8 waves at two per SIMD.
 template <int MT, bool SEQ, bool ZP, typename T, bool SBF, bool STREAM, bool ONE>
 inline void launch_t(const GemmArgs& a, const DecodePlan& s, hipStream_t st) {
-  const DecodeWork wk{s.tiles, s.ksteps, s.splits};
+  const DecodeWork wk{s.tiles, s.ksteps, s.splits, s.per};
   constexpr int NWV = MT == 1 ? 16 : 8, OCC = MT == 1 ? 4 : 2;
   const dim3 grid((unsigned)s.blocks), block(NWV * 64);
   const int spg = a.G / 32;

@@ -16,7 +16,7 @@ constexpr size_t kCounterBytes = 65536;
 
 struct DecodePlan {
   int mt;  // 16-token MFMA tiles
-  int tiles, ksteps, splits, blocks;
+  int tiles, ksteps, splits, per, blocks;  // per: k-steps of 32 rows in each split's range
   size_t ws_bytes;
 };
 

@@ -226,6 +226,23 @@ def test_split_k_config2_bit_stable(M):
         _check_vs_exact(y1.cpu().numpy(), ye, f"split {sk}")
 
 
+@pytest.mark.parametrize("M,K,sk", [(1, 4096, 3), (4, 2080, 5), (16, 1024, 200)])
+@pytest.mark.parametrize("stream", [True, False])
+def test_split_k_uneven_ranges(M, K, sk, stream):
+    """split_k follows the reference's ranges (ceil(ceil(K/64)/split_k) blocks of 64 rows each,
+    awq_fused_gemm.py:1798-1800): uneven, a K that is not a multiple of 64, and more splits
+    than 64-row blocks (the extra ranges are empty).  Bit-stable and within the oracle bar."""
+    ops = _lib()
+    N, G = 1024, 32
+    _note(f"split-K uneven M={M} K={K} split={sk} stream={stream}")
+    p = make_awq_problem(M=M, K=K, N=N, group_size=G, seed=K + sk)
+    t = _to_dev(p)
+    y1 = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, split_k=sk, layout="autoawq", decode_stream=stream)
+    y2 = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, split_k=sk, layout="autoawq", decode_stream=stream)
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+    _check_vs_exact(y1.cpu().numpy(), O.linear_exact(p["x"], _w_used(p, M, G).T), f"split {sk}")
+
+
 # ------------------------------------------------------------------ benchmark configs
 @pytest.mark.parametrize("M,N", [(m, n) for m in (1, 4, 16) for n in (4096, 6144, 24576)])
 @pytest.mark.parametrize("stream", [None, False])
