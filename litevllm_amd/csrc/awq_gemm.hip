@@ -4,12 +4,15 @@
 //  * Block tile 256 (M) x 64 NWN (N), k-stages of 64, 2 x NWN waves, wave tile 128 x 64:
 //    8 x 4 accumulators of v_mfma_f32_16x16x32_{f16,bf16} per wave.  NWN = 4 (256 columns,
 //    one 512-thread block per CU) halves the activation traffic per flop of NWN = 2.
-//  * Each k-stage the block copies its activation tile into LDS and dequantizes its weight
-//    tile once (every thread two packed words of two k-adjacent rows, exact (q - z) * s) into
-//    LDS as [n][k] half values, so every wave reads both MFMA operands with 16-byte LDS loads
-//    and no weight is dequantized twice in a block.
-//  * LDS is double-buffered and the next stage's global loads ride in registers, so one
-//    barrier per stage separates writing stage s + 1 from reading stage s.
+//  * Each k-stage the block dequantizes its weight tile once (every thread one packed word
+//    over 4 k-rows, exact (q - z) * s) into LDS as [n][k] half values, so every wave reads
+//    both MFMA operands with 16-byte LDS loads and no weight is dequantized twice in a block.
+//  * The activation tile goes straight from memory to LDS (buffer loads with the LDS
+//    modifier), one stage ahead; the packed weights, scales and zeros of stage s + 2 are
+//    requested while stage s computes and wait in registers, so every global load has a
+//    whole stage of MFMAs to arrive in.
+//  * LDS is double-buffered: one barrier per stage separates writing stage s + 1 from
+//    reading stage s.
 //  * 16-byte LDS chunks are XOR-swizzled by row so that operand reads and the dequant writes
 //    spread over the banks.
 //  * Blocks are dealt to the 8 XCDs so that each XCD works through contiguous tiles (the same
@@ -26,6 +29,26 @@ __device__ __forceinline__ WordSZ load_sz(const GemmArgs& p, int g, int word) {
   r.zw = ZP ? p.qz[(int64_t)g * (p.N >> 3) + word] : 0x88888888u;
   return r;
 }
+
+// waits until no vector-memory operation of this wave is outstanding (gfx9 s_waitcnt
+// encoding, expcnt and lgkmcnt unconstrained); as an intrinsic the compiler's own wait
+// bookkeeping sees it
+#define AWQ_WAIT_VMCNT0() __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8))
+
+// 16 bytes per lane from a buffer straight into LDS: lane l's bytes land at lds + 16 l.
+// Written as assembly so the compiler does not pair it with the LDS reads of the other
+// buffer (it cannot tell the two buffers apart and would wait for every load in flight
+// before each of them); the kernel waits for these loads itself before its barrier.  M0
+// carries the LDS address and nothing else in these kernels uses M0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16(const u32x4& rsrc, uint32_t lds, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
 
 // 16-byte chunk swizzles of 128-byte LDS rows (eight chunks).  Operand reads take 16
 // consecutive rows; activation rows are stored whole, weight rows n = 8 w + c by lanes of
@@ -77,31 +100,44 @@ __global__ void __launch_bounds__(128 * NWN, 2) prefill_kn_kernel(const GemmArgs
 #pragma unroll
     for (int nt = 0; nt < NTL; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int nst = p.K / BK;
+  // K % 64 may be 32 (group size 32): the last stage's upper half reads zero activations
+  const int nst = (p.K + BK - 1) / BK;
+  const int ngroups = p.K / p.G;
   const MagicK mk = magic_consts();
-  u32x4 areg[ACH];
-  uint32_t braw[4];
-  WordSZ bsz;
-  auto load = [&](int s) {
+
+  // activations: DMA instruction i of wave w fills 16-byte chunks c = (w ACH + i) 64 + lane of
+  // the stage buffer, i.e. row c / 8, slot c % 8, which holds global chunk slot ^ swz_a(row);
+  // rows past M read as zero (the descriptor's range check)
+  const uint64_t abase = (uint64_t)(uintptr_t)p.a;
+  const u32x4 ars = {(uint32_t)abase, (uint32_t)(abase >> 32) & 0xFFFFu,
+                     (uint32_t)((uint64_t)p.M * (uint64_t)p.lda * 2u), 0x00020000u};  // raw, bounds-checked
+  uint32_t a_voff[ACH];
+  int a_k[ACH];  // the chunk's first k within a stage
+#pragma unroll
+  for (int i = 0; i < ACH; ++i) {
+    const int c = (wave * ACH + i) * 64 + lane;
+    const int row = c / CPR, ch = (c % CPR) ^ swz_a(row);
+    a_k[i] = ch * 8;
+    a_voff[i] = ((uint32_t)(m0 + row) * (uint32_t)p.lda + (uint32_t)(ch * 8)) * 2u;
+  }
+  auto dma_a = [&](int s, int buf) {
 #pragma unroll
     for (int i = 0; i < ACH; ++i) {
-      const int c = tid + NT * i;
-      const int row = c / CPR, ch = c % CPR;
-      const int gr = min(m0 + row, p.M - 1);
-      areg[i] = *(const u32x4*)(p.a + (int64_t)gr * p.lda + s * BK + ch * 8);
+      const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) u32x4*)&lds_a[buf][(wave * ACH + i) * 64];
+      lds_dma16(ars, __builtin_amdgcn_readfirstlane(lds), s * BK + a_k[i] < p.K ? a_voff[i] : 0x80000000u,
+                (uint32_t)(s * BK * 2));
     }
-    const int64_t k = (int64_t)s * BK + 4 * kq;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) braw[j] = __builtin_nontemporal_load(p.qw + (k + j) * NW + bwld);
-    bsz = load_sz<ZP>(p, (s * BK) / p.G, bwld);
   };
-  auto write_a = [&](int buf) {
+  // packed weights: rows past K (the tail and the prefetch past the last stage) read as zero
+  const __amdgpu_buffer_rsrc_t wrs = make_rsrc(p.qw, (uint32_t)((uint64_t)p.K * (uint64_t)NW * 4u));
+  uint32_t braw[4], bnext[4];
+  WordSZ bsz, bsznext;
+  auto load_b = [&](int s) {
 #pragma unroll
-    for (int i = 0; i < ACH; ++i) {
-      const int c = tid + NT * i;
-      const int row = c / CPR, ch = c % CPR;
-      lds_a[buf][row * CPR + (ch ^ swz_a(row))] = areg[i];
-    }
+    for (int j = 0; j < 4; ++j)
+      bnext[j] = __builtin_amdgcn_raw_buffer_load_b32(
+          wrs, (int)(((uint32_t)(s * BK + 4 * kq + j) * (uint32_t)NW + (uint32_t)bwld) * 4u), 0, 0);
+    bsznext = load_sz<ZP>(p, min((s * BK + 4 * kq) / p.G, ngroups - 1), bwld);
   };
   // nibble I of the thread's word over its 4 k-rows -> 8 bytes of LDS row n = 8 bw + col(I);
   // the nibble's constants are derived right here so only the raw group words stay live
@@ -155,7 +191,6 @@ __global__ void __launch_bounds__(128 * NWN, 2) prefill_kn_kernel(const GemmArgs
     __builtin_amdgcn_sched_barrier(0);
     read_b(cb, 1, bf);
     af[0] = read_a(cb, 1, 0);
-    write_a(wb);
     uint32_t lo[2], hi[2];
     lo[0] = pair_lo(braw[0], braw[1]);
     hi[0] = pair_hi(braw[0], braw[1]);
@@ -179,10 +214,14 @@ __global__ void __launch_bounds__(128 * NWN, 2) prefill_kn_kernel(const GemmArgs
     }
   };
 
-  // prologue: stage 0 into buffer 0
-  load(0);
+  // prologue: stage 0 into buffer 0, stage 1's weights in registers
+  dma_a(0, 0);
+  load_b(0);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) braw[j] = bnext[j];
+  bsz = bsznext;
+  load_b(1);
   {
-    write_a(0);
     uint32_t lo[2], hi[2];
     lo[0] = pair_lo(braw[0], braw[1]);
     hi[0] = pair_hi(braw[0], braw[1]);
@@ -191,13 +230,24 @@ __global__ void __launch_bounds__(128 * NWN, 2) prefill_kn_kernel(const GemmArgs
 #pragma unroll
     for (int I = 0; I < 8; ++I) write_b_nib(0, I, lo, hi);
   }
+  AWQ_WAIT_VMCNT0();
+#pragma unroll
+  for (int j = 0; j < 4; ++j) braw[j] = bnext[j];
+  bsz = bsznext;
   __syncthreads();
-  // iteration s: request stage s + 1 (the last stage re-requests itself), compute stage s
-  // from buffer s & 1 and, in its second half, write stage s + 1 into the other buffer (after
-  // the last stage into a buffer nobody reads); one barrier per 64-k stage
+  // iteration s: request stage s + 1's activations (into the buffer stage s - 1 used) and
+  // stage s + 2's weights, compute stage s from buffer s & 1 and, in its second half, write
+  // stage s + 1's weights (held in registers since the last iteration) into the other buffer
+  // (after the last stage into a buffer nobody reads); one barrier per 64-k stage, after this
+  // wave's loads have landed
   for (int s = 0; s < nst; ++s) {
-    load(min(s + 1, nst - 1));
+    if (s + 1 < nst) dma_a(s + 1, (s & 1) ^ 1);
+    load_b(s + 2);
     step(s & 1, (s & 1) ^ 1);
+    AWQ_WAIT_VMCNT0();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) braw[j] = bnext[j];
+    bsz = bsznext;
     __syncthreads();
   }
 

@@ -130,6 +130,8 @@ SHAPES = [
     (5, 512, 264, 32), (8, 4096, 1024, 128), (16, 1024, 2048, 128), (17, 512, 520, 128),
     (32, 2048, 1536, 128), (33, 512, 512, 128), (64, 1024, 768, 64), (100, 512, 2056, 128),
     (256, 1024, 1024, 128), (300, 2048, 512, 128),
+    # group size 32 in the prefill kernel: two groups per 64-row stage, and K % 64 == 32
+    (40, 2080, 520, 32), (64, 1024, 1024, 32), (300, 96, 264, 32),
 ]
 
 
@@ -183,7 +185,8 @@ def test_gemm_bf16_activations(M, K, N):
     assert (np.abs(y - ye) <= ulp).all(), float((np.abs(y - ye) / ulp).max())
 
 
-@pytest.mark.parametrize("M,K,N,G", [(1, 1024, 512, 32), (4, 512, 256, 128), (64, 512, 512, 64)])
+@pytest.mark.parametrize("M,K,N,G", [(1, 1024, 512, 32), (4, 512, 256, 128), (64, 512, 512, 64),
+                                     (48, 1056, 256, 32)])
 def test_gemm_symmetric(M, K, N, G):
     ops = _lib()
     _note(f"gemm symmetric M={M} K={K} N={N} G={G}")
