@@ -189,32 +189,21 @@ int launch_moe_route(const void* logits, int64_t ld, int dtype, int64_t T, int E
   return launch_status();
 }
 
-template <int MODE, int MT, bool ZP, typename T, bool FAST>
-static void launch_gemm_t(const MoeArgs& a, int E, int sbf, hipStream_t st) {
-  const dim3 grid((unsigned)a.tiles, (unsigned)E);
-  const int spg = a.G / 32;
-  if (spg == 4)
-    hipLaunchKernelGGL((moe_gemm_kernel<MODE, MT, 2, 4, ZP, T, FAST>), grid, dim3(512), 0, st, a, sbf);
-  else if (spg == 2)
-    hipLaunchKernelGGL((moe_gemm_kernel<MODE, MT, 2, 2, ZP, T, FAST>), grid, dim3(512), 0, st, a, sbf);
-  else
-    hipLaunchKernelGGL((moe_gemm_kernel<MODE, MT, 2, 1, ZP, T, FAST>), grid, dim3(512), 0, st, a, sbf);
-}
-
 template <int MODE>
 static void launch_gemm_f16(const MoeArgs& a, int E, int mt, bool zp, hipStream_t st) {
-  if (mt == 4) zp ? launch_gemm_t<MODE, 4, true, f16, true>(a, E, 0, st) : launch_gemm_t<MODE, 4, false, f16, true>(a, E, 0, st);
-  else if (mt == 2) zp ? launch_gemm_t<MODE, 2, true, f16, true>(a, E, 0, st) : launch_gemm_t<MODE, 2, false, f16, true>(a, E, 0, st);
-  else zp ? launch_gemm_t<MODE, 1, true, f16, true>(a, E, 0, st) : launch_gemm_t<MODE, 1, false, f16, true>(a, E, 0, st);
+  if (mt == 2) zp ? launch_moe_gemm_t<MODE, 2, true, f16, false>(a, E, st) : launch_moe_gemm_t<MODE, 2, false, f16, false>(a, E, st);
+  else zp ? launch_moe_gemm_t<MODE, 1, true, f16, false>(a, E, st) : launch_moe_gemm_t<MODE, 1, false, f16, false>(a, E, st);
 }
 
 // expected routes per expert from which the grouped MFMA kernels take over
 constexpr int kMoeMfmaMinRoutes = 16;
 
 // 16-token tiles per wave group, from the expected routes per expert
+// (two tiles at most: the per-group and the scaled sums of four tiles would not fit the
+// registers of two waves per SIMD; larger route counts take more passes over the row loop)
 static int moe_mt(int64_t R, int E) {
   const int64_t avg = R / (E > 0 ? E : 1);
-  return avg <= 12 ? 1 : (avg <= 28 ? 2 : 4);
+  return avg <= 12 ? 1 : 2;
 }
 
 MoeWorkspace moe_workspace(int64_t T, int64_t H, int64_t I, int E, int topk, int act_bytes) {

@@ -68,12 +68,18 @@ __device__ __forceinline__ float moe_act(float g, int kind) {
   return g / (1.0f + expf(-g));
 }
 
-template <int MODE, int MT, int D, int SPG, bool ZP, typename T, bool FAST>
-__global__ void __launch_bounds__(512) moe_gemm_kernel(const MoeArgs p, int scale_bf16) {
+// MT: 16-route tiles per wave group.  SBF: scales are bf16 (fp16 otherwise).  Like the decode
+// kernel, the MFMAs multiply the activations by the exact integers q - z and each group's
+// fp32 sum is scaled once by the group's scale, so the weights enter unrounded -- the
+// reference's int4 kernels do the same, x * (q - 8) * s in fp32 (gemma4_moe_int4.py:736-742).
+template <int MODE, int MT, int D, int SPG, bool ZP, typename T, bool SBF>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(MT == 1 ? 4 : 2, MT == 1 ? 4 : 2)))
+moe_gemm_kernel(const MoeArgs p) {
   constexpr int NWV = 8;
   constexpr int NACC = 8 * MT;
   constexpr int CH = NACC < 16 ? NACC : 16;
   static_assert(NACC % CH == 0, "");
+  static_assert(D == 2 && (SPG == 1 || SPG % D == 0), "");
   __shared__ f32x4 red[(NWV / 2) * CH * 64];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -88,11 +94,12 @@ __global__ void __launch_bounds__(512) moe_gemm_kernel(const MoeArgs p, int scal
   const int ngroups = p.K / p.G;
   const int* list = p.lists + (int64_t)e * p.R;
   const uint32_t stream_bytes = (uint32_t)p.tiles * (uint32_t)KS * 2048u;
-  const __amdgpu_buffer_rsrc_t wrs = make_rsrc((const char*)p.qw + (int64_t)e * stream_bytes, stream_bytes);
-  const __amdgpu_buffer_rsrc_t srs = make_rsrc(p.sc + (int64_t)e * ngroups * p.N, (uint32_t)ngroups * (uint32_t)p.N * 2u);
-  const __amdgpu_buffer_rsrc_t zrs =
-      make_rsrc(ZP ? (const void*)(p.qz + (int64_t)e * ngroups * NW) : (const void*)p.sc, ZP ? (uint32_t)ngroups * (uint32_t)NW * 4u : 0u);
-  const __amdgpu_buffer_rsrc_t xrs = make_rsrc(p.a, (uint32_t)((uint64_t)p.rows_a * (uint64_t)p.lda * 2u));
+  const char* wbase = (const char*)p.qw + (int64_t)e * stream_bytes;
+  const uint16_t* sbase = p.sc + (int64_t)e * ngroups * p.N;
+  const void* zbase = ZP ? (const void*)(p.qz + (int64_t)e * ngroups * NW) : (const void*)p.sc;
+  const uint32_t s_bytes = (uint32_t)ngroups * (uint32_t)p.N * 2u;
+  const uint32_t z_bytes = ZP ? (uint32_t)ngroups * (uint32_t)NW * 4u : 0u;
+  const uint32_t x_bytes = (uint32_t)((uint64_t)p.rows_a * (uint64_t)p.lda * 2u);
   const int word = moe_word(t, r, p.half, NW);
   const uint32_t wc = word < 0 ? 0u : (uint32_t)word;  // padding lanes: word 0's constants, zero weights
   const MagicK mk = magic_consts();
@@ -109,33 +116,40 @@ __global__ void __launch_bounds__(512) moe_gemm_kernel(const MoeArgs p, int scal
     const int ks0 = KS * ki / wpg, ks1 = KS * (ki + 1) / wpg;
     const int nunits = ks1 - ks0;
 
-    f32x4 acc[8][MT];
+    f32x4 acc[8][MT];  // the current group's sums, integer weights
+    f32x4 tot[8][MT];  // the scaled sums of the groups done
 #pragma unroll
     for (int i = 0; i < 8; ++i)
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    int route[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int m = m0 + mt * 16 + r;
-      route[mt] = m < count ? list[m] : -1;
-    }
+      for (int mt = 0; mt < MT; ++mt) acc[i][mt] = tot[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     if (active && nunits > 0) {
+      // the activation operand: route row r of each 16-route tile, 8 k per lane
       uint32_t x_off[MT];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const int arow = MODE == 0 ? route[mt] / p.topk : route[mt];
-        x_off[mt] = route[mt] < 0 ? 0x80000000u : ((uint32_t)arow * (uint32_t)p.lda + 8u * (uint32_t)q) * 2u;
+        const int m = m0 + mt * 16 + r;
+        const int rt = m < count ? list[m] : -1;
+        const int arow = MODE == 0 ? rt / p.topk : rt;
+        x_off[mt] = rt < 0 ? 0x80000000u : ((uint32_t)arow * (uint32_t)p.lda + 8u * (uint32_t)q) * 2u;
       }
       uint32_t raw[D][8];
       u32x4 xr[D][MT];
       WordSZ sz[D];
-      ColConst cc[8];
-      int iks = ks0;
-      bool ipast = false;
+      uint32_t zm[8];  // biased zeros of the current group
+      u32x4 s4;        // scales of the current group (the word's 8 columns, raw 16-bit values)
+      // past the wave's last unit the ring's refills go through empty descriptors (zeros,
+      // no memory traffic), so every ring turn is a whole one
+      int iks = ks0, ileft = nunits;
       auto issue = [&](int slot) {
         const int ks = iks;
+        const bool past = ileft <= 0;
+        ++iks;
+        --ileft;
+        const __amdgpu_buffer_rsrc_t wrs = make_rsrc(wbase, past ? 0u : stream_bytes);
+        const __amdgpu_buffer_rsrc_t xrs = make_rsrc(p.a, past ? 0u : x_bytes);
+        const __amdgpu_buffer_rsrc_t srs = make_rsrc(sbase, past ? 0u : s_bytes);
+        const __amdgpu_buffer_rsrc_t zrs = make_rsrc(zbase, past ? 0u : z_bytes);
         const int kbase = (int)(((uint32_t)t * (uint32_t)KS + (uint32_t)ks) * 2048u);
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -146,52 +160,98 @@ __global__ void __launch_bounds__(512) moe_gemm_kernel(const MoeArgs p, int scal
         }
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
-          xr[slot][mt] = __builtin_bit_cast(
-              u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, ipast ? (int)0x80000000 : (int)x_off[mt], ks * 64, 0));
+          xr[slot][mt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)x_off[mt], ks * 64, 0));
         const int g = ks / SPG;
         sz[slot].s4 = __builtin_bit_cast(
             u32x4, __builtin_amdgcn_raw_buffer_load_b128(srs, (int)(16u * wc), (int)((uint32_t)g * (uint32_t)p.N * 2u), 0));
         sz[slot].zw = ZP ? __builtin_amdgcn_raw_buffer_load_b32(zrs, (int)(4u * wc), (int)((uint32_t)g * (uint32_t)NW * 4u), 0)
                          : 0x88888888u;
-        if (iks + 1 < ks1) ++iks; else ipast = true;
       };
-      int cks = ks0, g_cur = -1;
-      auto step = [&](int done, int slot) {
-        if (done < nunits) {
-          const int g = cks / SPG;
-          if (g != g_cur) {
-            g_cur = g;
-            prep_consts<false, FAST>(sz[slot], scale_bf16 != 0, cc);
-          }
-          ++cks;
-        }
+      // FRESH: the group's first unit (its MFMAs start from zero)
+      auto compute = [&](int slot, auto fresh) {
+        constexpr bool FRESH = decltype(fresh)::value;
         uint32_t mlo[4], mhi[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           mlo[v] = pair_lo(raw[slot][2 * v], raw[slot][2 * v + 1]);
           mhi[v] = pair_hi(raw[slot][2 * v], raw[slot][2 * v + 1]);
         }
-#define AWQ_MOE_NIB(I)                                                        \
-        {                                                                     \
-          const u32x4 op = rows_operand<I, FAST, T>(mlo, mhi, cc[I], mk);     \
-          _Pragma("unroll") for (int mt = 0; mt < MT; ++mt)                   \
-              acc[I][mt] = MfmaOp<T>::run(op, xr[slot][mt], acc[I][mt]);     \
+#define AWQ_MOE_NIB(I)                                                                          \
+        {                                                                                       \
+          const u32x4 op = int_operand<I, T>(mlo, mhi, zm[I], mk);                              \
+          _Pragma("unroll") for (int mt = 0; mt < MT; ++mt)                                     \
+              acc[I][mt] = MfmaOp<T>::run(xr[slot][mt], op, FRESH ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[I][mt]); \
         }
         AWQ_MOE_NIB(0) AWQ_MOE_NIB(1) AWQ_MOE_NIB(2) AWQ_MOE_NIB(3)
         AWQ_MOE_NIB(4) AWQ_MOE_NIB(5) AWQ_MOE_NIB(6) AWQ_MOE_NIB(7)
 #undef AWQ_MOE_NIB
       };
+      // tot += acc * scale of the group just finished (ZERO: acc restarts from zero)
+      auto flush = [&](auto zero) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int c = nib_col<false>(i);
+          const uint16_t sb = (uint16_t)(s4[c >> 1] >> (16 * (c & 1)));
+          const float sf = SBF ? bf_bits2f(sb) : h_bits2f(sb);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            tot[i][mt] += acc[i][mt] * sf;
+            if constexpr (decltype(zero)::value) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+          }
+        }
+      };
+      auto prep = [&](int slot) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) zm[i] = zero_magic(i & 1, (sz[slot].zw >> (4 * i)) & 0xF);
+        s4 = sz[slot].s4;
+      };
+
 #pragma unroll
       for (int u = 0; u < D; ++u) issue(u);
       __builtin_amdgcn_sched_barrier(0);
-      for (int done = 0; done < nunits; done += D) {
+      // (one token tile runs without it: the extra loop would cost the registers that let
+      // four waves share a SIMD)
+      constexpr bool kGroupLoop = SPG > 1 && MT > 1;
+      if (kGroupLoop && (ks0 % SPG) == 0 && (nunits % SPG) == 0) {
+        // whole groups: one group per iteration, its first unit in slot 0
+        for (int done = 0; done < nunits; done += SPG) {
+          prep(0);
 #pragma unroll
-        for (int u = 0; u < D; ++u) {
-          step(done + u, u);
-          __builtin_amdgcn_sched_barrier(0);
-          issue(u);
-          __builtin_amdgcn_sched_barrier(0);
+          for (int u = 0; u < SPG; ++u) {
+            if (u == 0) compute(0, std::true_type{});
+            else compute(u % D, std::false_type{});
+            __builtin_amdgcn_sched_barrier(0);
+            issue(u % D);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+          flush(std::false_type{});
         }
+      } else {
+        int cks = ks0, g_cur = -1;
+        for (int done = 0; done < nunits; done += D) {
+#pragma unroll
+          for (int u = 0; u < D; ++u) {
+            if (done + u < nunits) {  // wave-uniform: the last turn may hold fewer units
+              if constexpr (SPG == 1) {
+                prep(u);
+                compute(u, std::true_type{});
+                flush(std::false_type{});
+              } else {
+                const int g = cks++ / SPG;
+                if (g != g_cur) {
+                  if (g_cur >= 0) flush(std::true_type{});
+                  g_cur = g;
+                  prep(u);
+                }
+                compute(u, std::false_type{});
+              }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            issue(u);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+        if (SPG > 1 && g_cur >= 0) flush(std::false_type{});
       }
     }
 
@@ -203,36 +263,37 @@ __global__ void __launch_bounds__(512) moe_gemm_kernel(const MoeArgs p, int scal
         if (ki >= half && ki < 2 * half) {
 #pragma unroll
           for (int c = 0; c < CH; ++c)
-            red[((gi * hslots + ki - half) * CH + c) * 64 + lane] = acc[(c0 + c) / MT][(c0 + c) % MT];
+            red[((gi * hslots + ki - half) * CH + c) * 64 + lane] = tot[(c0 + c) / MT][(c0 + c) % MT];
         }
         __syncthreads();
         if (ki < half) {
 #pragma unroll
-          for (int c = 0; c < CH; ++c) acc[(c0 + c) / MT][(c0 + c) % MT] += red[((gi * hslots + ki) * CH + c) * 64 + lane];
+          for (int c = 0; c < CH; ++c) tot[(c0 + c) / MT][(c0 + c) % MT] += red[((gi * hslots + ki) * CH + c) * 64 + lane];
         }
         __syncthreads();
       }
     }
 
     // ---- epilogue: the group's first wave holds the sums ----
-    // lane (q, r), accumulator [i][mt] element v: row m0 + 16 mt + r, tile word 4q + v, column
-    // nib_col(i) of that word
+    // lane (q, r), accumulator [i][mt] element v: route row m0 + 16 mt + 4q + v, tile word r,
+    // column nib_col(i) of that word
     if (ki == 0 && active) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const int rt = route[mt];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
+          const int m = m0 + mt * 16 + 4 * q + v;
+          const int rt = m < count ? list[m] : -1;
           float o[8];
 #pragma unroll
-          for (int c = 0; c < 8; ++c) o[c] = acc[col_nib<false>(c)][mt][v];
+          for (int c = 0; c < 8; ++c) o[c] = tot[col_nib<false>(c)][mt][v];
           if constexpr (MODE == 0) {
-            // up values of the same columns sit 32 lanes higher (tile words 8 .. 15)
+            // the up values of the same columns sit 8 lanes higher (tile words 8 .. 15)
             float u[8];
 #pragma unroll
-            for (int c = 0; c < 8; ++c) u[c] = __shfl_xor(o[c], 32);
-            const int gw = 8 * t + 4 * q + v;  // gate word
-            if (q < 2 && rt >= 0 && gw < p.half) {
+            for (int c = 0; c < 8; ++c) u[c] = __shfl_xor(o[c], 8);
+            const int gw = 8 * t + r;  // gate word
+            if (r < 8 && rt >= 0 && gw < p.half) {
               const float wgt = load_route_weight(p.rw, p.rw_dtype, rt);
               float h[8];
 #pragma unroll
@@ -245,7 +306,7 @@ __global__ void __launch_bounds__(512) moe_gemm_kernel(const MoeArgs p, int scal
               *(u32x4*)((uint16_t*)p.out + (int64_t)rt * p.ldo + 8 * gw) = st;
             }
           } else {
-            const int w = 16 * t + 4 * q + v;
+            const int w = 16 * t + r;
             if (rt >= 0 && w < NW) {
               float* dst = (float*)p.out + (int64_t)rt * p.ldo + 8 * w;
               *(f32x4*)dst = f32x4{o[0], o[1], o[2], o[3]};
@@ -262,6 +323,21 @@ __global__ void __launch_bounds__(512) moe_gemm_kernel(const MoeArgs p, int scal
 }  // namespace awq
 
 namespace awq_host {
+using namespace awq;
+
+// grid (column tiles, experts); the group size picks the k-steps per group
+template <int MODE, int MT, bool ZP, typename T, bool SBF>
+inline void launch_moe_gemm_t(const MoeArgs& a, int E, hipStream_t st) {
+  const dim3 grid((unsigned)a.tiles, (unsigned)E);
+  const int spg = a.G / 32;
+  if (spg == 4)
+    hipLaunchKernelGGL((moe_gemm_kernel<MODE, MT, 2, 4, ZP, T, SBF>), grid, dim3(512), 0, st, a);
+  else if (spg == 2)
+    hipLaunchKernelGGL((moe_gemm_kernel<MODE, MT, 2, 2, ZP, T, SBF>), grid, dim3(512), 0, st, a);
+  else
+    hipLaunchKernelGGL((moe_gemm_kernel<MODE, MT, 2, 1, ZP, T, SBF>), grid, dim3(512), 0, st, a);
+}
+
 // grouped MFMA kernels for many routes per expert (awq_moe_mfma.hip); both K dims % 64 == 0
 void launch_moe_mfma(const awq::MoeArgs& gu, const awq::MoeArgs& dn, int E, bool zp, int act, int sbf,
                      hipStream_t st);

@@ -7,14 +7,8 @@ using namespace awq;
 
 template <int MODE, bool ZP, typename T>
 static void launch_misc_t(const MoeArgs& a, int E, int sbf, hipStream_t st) {
-  const dim3 grid((unsigned)a.tiles, (unsigned)E);
-  const int spg = a.G / 32;
-  if (spg == 4)
-    hipLaunchKernelGGL((moe_gemm_kernel<MODE, 2, 2, 4, ZP, T, false>), grid, dim3(512), 0, st, a, sbf);
-  else if (spg == 2)
-    hipLaunchKernelGGL((moe_gemm_kernel<MODE, 2, 2, 2, ZP, T, false>), grid, dim3(512), 0, st, a, sbf);
-  else
-    hipLaunchKernelGGL((moe_gemm_kernel<MODE, 2, 2, 1, ZP, T, false>), grid, dim3(512), 0, st, a, sbf);
+  if (sbf) launch_moe_gemm_t<MODE, 2, ZP, T, true>(a, E, st);
+  else launch_moe_gemm_t<MODE, 2, ZP, T, false>(a, E, st);
 }
 
 template <typename T>

@@ -1,7 +1,8 @@
 """GPU parity of the grouped AWQ MoE path (routing, gate_up + activation, down, combine)
 against the CPU oracle: ``oracle.awq_oracle.moe_grouped_exact`` (float64 sums, the
-intermediate rounded once, the reference grouped kernel's rounding points) and the
-``fused_moe`` restatement (``oracle.ref_cpu.fused_moe_cpu``).
+intermediate rounded once, the reference grouped kernel's rounding points, with the weights
+the serving kernel multiplies -- see ``_mfma_path``) and the ``fused_moe`` restatement
+(``oracle.ref_cpu.fused_moe_cpu``).
 
 Bar: the kernel's output within 4 fp16 ulps (ulps at max(|y|, RMS(y))) of the exact oracle
 and mean relative error <= 2e-4; bitwise reproducible across calls.  The intermediate is
@@ -46,6 +47,31 @@ def _dense_experts(d, G):
     w2 = torch.stack([ops.dequant(d["dq"][e], d["ds"][e], None if d["dz"] is None else d["dz"][e], G,
                                   layout="autoawq").t() for e in range(E)])
     return w1.cpu().numpy(), w2.cpu().numpy()
+
+
+def _mfma_path(T, E, H, I, topk):
+    """The grouped MFMA kernels serve at least 16 routes per expert when H and I are multiples
+    of 64; they multiply weights rounded to the activation dtype (dequantized into LDS).  The
+    decode-structured kernels serve the rest and multiply the exact integers q - z, scaling each
+    group's fp32 sum once: unrounded weights, as the reference's int4 kernels
+    (gemma4_moe_int4.py:736-742)."""
+    return T * topk >= 16 * E and H % 64 == 0 and I % 64 == 0
+
+
+def _unrounded_experts(p, G):
+    """w1 [E, 2I, H], w2 [E, H, I] as float32 (q - z) * s, never rounded."""
+    gq, gz, gs = p["gate_up"]
+    dq, dz, ds = p["down"]
+    E = gq.shape[0]
+    zp = gz is not None
+    f = lambda q, s, z: O.dequant_awq(q, s, z, G, out_dtype="float32", zero_point=zp).T
+    w1 = np.stack([f(gq[e], gs[e], gz[e] if zp else None) for e in range(E)])
+    w2 = np.stack([f(dq[e], ds[e], dz[e] if zp else None) for e in range(E)])
+    return w1, w2
+
+
+def _experts_used(p, d, G, mfma):
+    return _dense_experts(d, G) if mfma else _unrounded_experts(p, G)
 
 
 def _route_cpu(logits, topk):
@@ -114,7 +140,7 @@ def test_moe_vs_exact_oracle(T, E, H, I, topk, G, zp, act):
     y2 = ops.moe(x, tw.to(DEV), tid.to(DEV), d["gq"], d["gs"], d["gz"], d["dq"], d["ds"], d["dz"], G, act)
     torch.cuda.synchronize()
     assert torch.equal(y, y2), "not bitwise reproducible"
-    w1, w2 = _dense_experts(d, G)
+    w1, w2 = _experts_used(p, d, G, _mfma_path(T, E, H, I, topk))
     exact = O.moe_grouped_exact(p["x"], tw.numpy(), tid.numpy(), w1, w2, activation=act)
     _check(y.cpu().numpy(), exact, f"T={T} E={E} H={H} I={I} k={topk} G={G} zp={zp} {act}")
 
@@ -126,7 +152,7 @@ def test_moe_skewed_routing_multiple_passes():
     tid = torch.tensor([[3, 6]] * T, dtype=torch.int64)
     tw = torch.rand(T, topk, generator=torch.Generator().manual_seed(0))
     y = ops.moe(_dev(p["x"]), tw.to(DEV), tid.to(DEV), d["gq"], d["gs"], d["gz"], d["dq"], d["ds"], d["dz"], G)
-    w1, w2 = _dense_experts(d, G)
+    w1, w2 = _experts_used(p, d, G, _mfma_path(T, E, H, I, topk))
     exact = O.moe_grouped_exact(p["x"], tw.numpy(), tid.numpy(), w1, w2)
     _check(y.cpu().numpy(), exact, "skewed")
 
@@ -139,12 +165,9 @@ def test_moe_bf16_activations_and_out_of_range_ids():
     tid[::4, 1] = E + 3  # ignored routes
     xb = torch.from_numpy(p["x"]).float().bfloat16()
     y = ops.moe(xb.to(DEV), tw.to(DEV), tid.to(DEV), d["gq"], d["gs"], d["gz"], d["dq"], d["ds"], d["dz"], G)
-    # bf16 activations: weights dequantized to bf16 (one rounding of (q - z) * s)
-    gq, gz, gs = p["gate_up"]
-    dq, dz, ds = p["down"]
-    bf = lambda q, s, z: O.bf16_bits_to_f32(O.dequant_awq(q, s, z, G, out_dtype="bfloat16")).T
-    w1b = np.stack([bf(gq[e], gs[e], gz[e]) for e in range(E)])
-    w2b = np.stack([bf(dq[e], ds[e], dz[e]) for e in range(E)])
+    # bf16 activations, 7.5 routes per expert (the decode-structured kernels): unrounded weights
+    assert not _mfma_path(T, E, H, I, topk)
+    w1b, w2b = _unrounded_experts(p, G)
     xf = xb.float().numpy()
     exact = O.moe_grouped_exact(xf, tw.numpy(), tid.numpy(), w1b, w2b, inter_dtype="bfloat16")
     yf = y.float().cpu().numpy()
@@ -187,7 +210,8 @@ def test_fused_moe_surface_against_reference_port():
     tw, tid = _route_cpu(logits, topk)
     port = R.fused_moe_cpu(torch.from_numpy(p["x"]), torch.from_numpy(w1d), torch.from_numpy(w2d),
                            topk_weights=tw.half(), topk_ids=tid).double().numpy()
-    exact = O.moe_grouped_exact(p["x"], tw.numpy(), tid.numpy(), w1d, w2d)
+    w1u, w2u = _experts_used(p, d, G, _mfma_path(T, E, H, I, topk))
+    exact = O.moe_grouped_exact(p["x"], tw.numpy(), tid.numpy(), w1u, w2u)
     _check(y.numpy(), exact, "fused_moe")
     floor = float(np.sqrt(np.mean(exact ** 2)))
     # the port's fp16 intermediates and accumulation: a few ulps from both
@@ -201,7 +225,7 @@ def test_config4_full_size(T):
     p, d = _problem(T, E, H, I, topk, G, seed=40 + T)
     tw, tid = _route_cpu(torch.from_numpy(p["logits"]), topk)
     y = ops.moe(_dev(p["x"]), tw.to(DEV), tid.to(DEV), d["gq"], d["gs"], d["gz"], d["dq"], d["ds"], d["dz"], G)
-    w1, w2 = _dense_experts(d, G)
+    w1, w2 = _experts_used(p, d, G, _mfma_path(T, E, H, I, topk))
     exact = O.moe_grouped_exact(p["x"], tw.numpy(), tid.numpy(), w1, w2)
     _check(y.cpu().numpy(), exact, f"config4 T={T}")
 
