@@ -10,7 +10,7 @@ using namespace awq;
 // Each tile's K is cut into `splits` ranges by the reference's split-K rule
 // (awq_fused_gemm.py:1798-1800, BLOCK_K = 64): ceil(ceil(K / 64) / splits) blocks of 64 rows
 // per range, the last ones shorter or empty, one block of waves each (16 waves at four per
-// SIMD for M <= 16, 8 at two per SIMD above; a two-deep ring).  By default splits = CUs /
+// SIMD for M == 1, 8 at two per SIMD otherwise; a two-deep ring).  By default splits = CUs /
 // tiles (at least 1, at most one 64-row block each), so one round of blocks covers the chip;
 // split_k > 0 asks for that many ranges.
 DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t G, int split_k, DecodeMode mode) {

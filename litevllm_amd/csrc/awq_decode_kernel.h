@@ -183,8 +183,7 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
     for (int u = 0; u < D; ++u) issue(u);
     __builtin_amdgcn_sched_barrier(0);
     static_assert(D == 2 && (SPG == 1 || SPG % D == 0), "");
-    // (one tile of 16 tokens at four waves per SIMD has no registers to spare for it)
-    constexpr bool kGroupLoop = SPG > 1 && (ONE || MT > 1);
+    constexpr bool kGroupLoop = SPG > 1;
     if (kGroupLoop && (w0 % SPG) == 0 && (nunits % SPG) == 0) {
       // whole groups (the usual case): one group per iteration, its first unit in slot 0, so
       // the MFMAs of that unit start from zero and nothing but tot is carried between groups
@@ -314,12 +313,13 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
 namespace awq_host {
 using namespace awq;
 
-// One 16-token tile (M <= 16) needs few enough registers to run blocks of 16 waves at four
-// per SIMD, which hides more of the memory latency; two tiles run 8 waves at two per SIMD.
+// M == 1 needs few enough registers to run blocks of 16 waves at four per SIMD, which hides
+// more of the memory latency; more tokens run 8 waves at two per SIMD, whose registers leave
+// room for the whole-group loop (measured faster than 16 waves without it).
 template <int MT, bool SEQ, bool ZP, typename T, bool SBF, bool STREAM, bool ONE>
 inline void launch_t(const GemmArgs& a, const DecodePlan& s, hipStream_t st) {
   const DecodeWork wk{s.tiles, s.ksteps, s.splits, s.per};
-  constexpr int NWV = MT == 1 ? 16 : 8, OCC = MT == 1 ? 4 : 2;
+  constexpr int NWV = ONE ? 16 : 8, OCC = ONE ? 4 : 2;
   const dim3 grid((unsigned)s.blocks), block(NWV * 64);
   const int spg = a.G / 32;
   if (spg == 4)
