@@ -74,7 +74,8 @@ __global__ void __launch_bounds__(128 * NWN, 2) prefill_kn_kernel(const GemmArgs
   __shared__ u32x4 lds_a[2][BM * CPR];
   __shared__ u32x4 lds_b[2][BN * CPR];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform by construction
   const int q = lane >> 4, r = lane & 15;
   const int wave_m = wave / NWN, wave_n = wave % NWN;
 
@@ -120,23 +121,30 @@ __global__ void __launch_bounds__(128 * NWN, 2) prefill_kn_kernel(const GemmArgs
     a_k[i] = ch * 8;
     a_voff[i] = ((uint32_t)(m0 + row) * (uint32_t)p.lda + (uint32_t)(ch * 8)) * 2u;
   }
+  const uint32_t lds_a0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) u32x4*)&lds_a[0][wave * ACH * 64];
   auto dma_a = [&](int s, int buf) {
+    const bool tail = s * BK + BK > p.K;  // wave-uniform: only a last half stage checks columns
 #pragma unroll
-    for (int i = 0; i < ACH; ++i) {
-      const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) u32x4*)&lds_a[buf][(wave * ACH + i) * 64];
-      lds_dma16(ars, __builtin_amdgcn_readfirstlane(lds), s * BK + a_k[i] < p.K ? a_voff[i] : 0x80000000u,
-                (uint32_t)(s * BK * 2));
-    }
+    for (int i = 0; i < ACH; ++i)
+      lds_dma16(ars, lds_a0 + (uint32_t)buf * (uint32_t)sizeof(lds_a[0]) + (uint32_t)(i * 64 * 16),
+                tail && s * BK + a_k[i] >= p.K ? 0x80000000u : a_voff[i], (uint32_t)(s * BK * 2));
   };
-  // packed weights: rows past K (the tail and the prefetch past the last stage) read as zero
-  const __amdgpu_buffer_rsrc_t wrs = make_rsrc(p.qw, (uint32_t)((uint64_t)p.K * (uint64_t)NW * 4u));
+  // packed weights: the row offset of the stage rides in the SGPR offset; stages past the
+  // last one go through an empty descriptor, and a last half stage checks its rows
+  const uint32_t w_bytes = (uint32_t)((uint64_t)p.K * (uint64_t)NW * 4u);
+  const uint32_t b_voff = ((uint32_t)(4 * kq) * (uint32_t)NW + (uint32_t)bwld) * 4u;
   uint32_t braw[4], bnext[4];
   WordSZ bsz, bsznext;
   auto load_b = [&](int s) {
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(p.qw, s < nst ? w_bytes : 0u);
+    const bool tail = s * BK + BK > p.K;
+    const uint32_t soff = (uint32_t)(s * BK) * (uint32_t)NW * 4u;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t vo = b_voff + (uint32_t)j * (uint32_t)NW * 4u;
       bnext[j] = __builtin_amdgcn_raw_buffer_load_b32(
-          wrs, (int)(((uint32_t)(s * BK + 4 * kq + j) * (uint32_t)NW + (uint32_t)bwld) * 4u), 0, 0);
+          wrs, tail ? (int)(vo + soff) : (int)vo, tail ? 0 : (int)soff, 0);
+    }
     bsznext = load_sz<ZP>(p, min((s * BK + 4 * kq) / p.G, ngroups - 1), bwld);
   };
   // nibble I of the thread's word over its 4 k-rows -> 8 bytes of LDS row n = 8 bw + col(I);
