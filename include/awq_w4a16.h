@@ -198,6 +198,44 @@ int awq_w4a16_moe(const void* x, int64_t ldx, const void* topk_ids, int32_t ids_
                   int32_t E, int32_t top_k, int32_t group_size, int32_t activation, int32_t act_dtype,
                   int32_t scale_dtype, void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- dense gated MLP (gate and up projections with the activation fused) -------------
+ * Replaces the reference's M = 1 fused gate/up kernels (vllm/kernels/triton/awq_fused_gemm.py:
+ * 1406-1506 and 1509-1590, launched by packed_int4_symmetric_fused_gate_up_m1 and
+ * ..._group32_m1 at 3009-3120): out[m, n] = act(x[m] . Wg[n]) * (x[m] . Wu[n]), both sums in
+ * fp32 over unrounded weights (q - z) * s, one rounding at the end.
+ * The two projections travel as one interleaved matrix of 2 * ceil(I / 64) * 64 columns:
+ * block b of 128 columns holds gate columns [64 b, 64 b + 64) followed by the up columns of the
+ * same outputs (columns past I are zero).  awq_w4a16_gate_up_interleave builds it from the two
+ * AUTOAWQ matrices. */
+
+/* Interleave two row-major [rows, cols] matrices of elem_bytes-byte elements (2 or 4) into
+ * [rows, 2 * ceil(cols / half_tile) * half_tile]: each run of 2 * half_tile elements is
+ * half_tile elements of gate followed by the same half_tile elements of up, zero past cols.
+ * half_tile 8 for qweight / qzeros [K, I/8] words, 64 for scales [K/G, I].  No counterpart in
+ * the reference (its kernel reads the two matrices separately); it is the derived pack the
+ * reference would cache on the weight pair (tensor.py:1251-1256). */
+int awq_w4a16_gate_up_interleave(const void* gate, const void* up, void* out, int64_t rows, int64_t cols,
+                                 int32_t elem_bytes, int32_t half_tile, void* stream);
+
+/* Workspace of awq_w4a16_gate_up_act: that of awq_w4a16_gemm for the interleaved matrix,
+ * N = 2 * ceil(I / 64) * 64 (same zeroing rule). */
+size_t awq_w4a16_gate_up_workspace_bytes(int64_t M, int64_t I, int64_t K, int32_t group_size,
+                                         int32_t split_k, int32_t layout);
+
+/* out[M, I] = act(x . Wg^T) * (x . Wu^T), activation AWQ_MOE_ACT_SILU or AWQ_MOE_ACT_GELU_TANH
+ * (the tanh form, computed as g * sigmoid(2 * inner) like awq_fused_gemm.py:1493-1502).
+ *   x: [M, K] act_dtype (F16 or BF16), row stride ldx; out: [M, I] act_dtype, row stride ldo.
+ *   qweight / scales / qzeros: the interleaved matrix in layout AUTOAWQ or KN_SEQ
+ *   ([K, N/8] words, N = 2 * ceil(I / 64) * 64) or DECODE_STREAM (its awq_w4a16_pack_decode_stream
+ *   copy; F16 activations and scales); qzeros NULL = symmetric z = 8 (the reference's mode).
+ *   1 <= M <= 32 (the reference takes M == 1); group_size 32, 64 or 128 dividing K.
+ *   split_k as for awq_w4a16_gemm; results are bitwise reproducible for a given split. */
+int awq_w4a16_gate_up_act(const void* x, int64_t ldx, const int32_t* qweight, const void* scales,
+                          const int32_t* qzeros, void* out, int64_t ldo, int64_t M, int64_t I, int64_t K,
+                          int32_t group_size, int32_t split_k, int32_t layout, int32_t activation,
+                          int32_t act_dtype, int32_t scale_dtype, void* workspace, size_t workspace_bytes,
+                          void* stream);
+
 #ifdef __cplusplus
 }
 #endif

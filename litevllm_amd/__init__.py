@@ -3,8 +3,13 @@ reference's Python call surface for that path."""
 from . import _lib, ops  # noqa: F401
 from .awq import AWQConfig  # noqa: F401
 from .awq_fused_gemm import (  # noqa: F401
+    awq_fused_gate_up_enabled,
+    awq_fused_gate_up_group32_enabled,
     awq_fused_gemm,
     awq_fused_gemm_safe,
+    packed_int4_symmetric_fused_gate_up_group32_m1,
+    packed_int4_symmetric_fused_gate_up_m1,
+    packed_int4_symmetric_fused_gate_up_m1_safe,
     packed_int4_symmetric_fused_gemm,
     packed_int4_symmetric_fused_gemm_safe,
 )
@@ -14,7 +19,7 @@ from .awq_triton import (  # noqa: F401
     awq_gemm_triton,
     packed_int4_fused_capability_check,
 )
-from .fused_pair import try_fused_awq_pair_matmul  # noqa: F401
+from .fused_pair import try_fused_awq_gate_up_activation, try_fused_awq_pair_matmul  # noqa: F401
 from .moe import (  # noqa: F401
     AWQExperts,
     awq_moe,

@@ -1,7 +1,9 @@
 """Drop-in for the AWQ entry points of ``vllm/kernels/triton/awq_fused_gemm.py``:
 ``awq_fused_gemm``, ``awq_fused_gemm_safe``, ``packed_int4_symmetric_fused_gemm`` and
 ``packed_int4_symmetric_fused_gemm_safe`` keep the reference's arguments, validation,
-reason strings and split-K knob; the launch goes to the gfx950 HIP kernels.
+reason strings and split-K knob; the launch goes to the gfx950 HIP kernels.  The M = 1
+fused gate/up surfaces (``packed_int4_symmetric_fused_gate_up_m1``, its ``group32`` twin,
+``..._m1_safe`` and the two policy switches) do the same for the gated MLP.
 
 Differences, all deliberate:
   * split-K partials are reduced in fp32 in a fixed order (the reference rounds each
@@ -181,6 +183,120 @@ def packed_int4_symmetric_fused_gemm_safe(a, qweight, scales, group_size, out=No
             out=out, bias=bias.contiguous() if bias is not None else None, config=config,
             policy=policy, layout=layout)
         if c.shape != (m, n):
+            return c, False, "bad_output_shape"
+        return c, True, "ok"
+    except Exception:
+        return a, False, "kernel_exception"
+
+
+# ------------------------------------------------------------------ fused gate/up (M = 1)
+def _truthy(value) -> bool:
+    return str(value or "").strip().lower() in ("1", "true", "yes", "on")
+
+
+def _policy_flag(config, policy, name: str) -> bool:
+    raw = _kernel_policy(config, policy).get(name, False)
+    return raw if isinstance(raw, bool) else _truthy(raw)
+
+
+def awq_fused_gate_up_enabled(*, config: Any | None = None, policy: dict | None = None) -> bool:
+    """Policy key ``awq_fused_gate_up``, default off (``awq_fused_gemm.py:513-519``)."""
+    return _policy_flag(config, policy, "awq_fused_gate_up")
+
+
+def awq_fused_gate_up_group32_enabled(*, config: Any | None = None, policy: dict | None = None) -> bool:
+    """Policy key ``awq_fused_gate_up_group32``, default off (``awq_fused_gemm.py:522-528``)."""
+    return _policy_flag(config, policy, "awq_fused_gate_up_group32")
+
+
+def _gate_up_m1(name, a, gate_qweight, up_qweight, gate_scales, up_scales, group_size, activation, out):
+    m, k = a.shape
+    if m != 1:
+        raise ValueError(f"{name}: requires M == 1")
+    if int(group_size) != 32 or k % 32 != 0:
+        raise ValueError(f"{name}: requires group_size=32 and K%32==0")
+    if tuple(gate_qweight.shape) != tuple(up_qweight.shape):
+        raise ValueError(f"{name}: qweight shape mismatch")
+    if tuple(gate_scales.shape) != tuple(up_scales.shape):
+        raise ValueError(f"{name}: scale shape mismatch")
+    if int(gate_qweight.shape[1]) * 8 != k:
+        raise ValueError(f"{name}: K mismatch")
+    if out is not None and out.dtype != a.dtype:
+        raise ValueError(f"{name}: out must have the input's dtype")
+    as_i32 = lambda t: t if t.dtype == torch.int32 else t.to(torch.int32)
+    return ops.gate_up_act(a, as_i32(gate_qweight), as_i32(up_qweight), gate_scales, up_scales,
+                           int(group_size), activation=activation, layout="ref", out=out)
+
+
+def packed_int4_symmetric_fused_gate_up_m1(a, gate_qweight, up_qweight, gate_scales, up_scales,
+                                           group_size, *, activation: str = "silu", out=None,
+                                           config: Any | None = None, policy: dict | None = None):
+    """``out[0, n] = act(a . Wg[n]) * (a . Wu[n])`` for symmetric packed int4 (z = 8) weights
+    in the reference layout [N, K/8] with scales [N, K/32] (``awq_fused_gemm.py:3009-3071``,
+    kernel 1406-1506): one launch of the decode kernel with its gated epilogue over the cached
+    interleaved pair; sums in fp32 over unrounded (q - 8) * s, one rounding at the end."""
+    del config, policy
+    return _gate_up_m1("packed_int4_symmetric_fused_gate_up_m1", a, gate_qweight, up_qweight,
+                       gate_scales, up_scales, group_size, activation, out)
+
+
+def packed_int4_symmetric_fused_gate_up_group32_m1(a, gate_qweight, up_qweight, gate_scales,
+                                                   up_scales, group_size, *, activation: str = "silu",
+                                                   out=None, config: Any | None = None,
+                                                   policy: dict | None = None):
+    """The reference's group-oriented twin (``awq_fused_gemm.py:3074-3120``) computes the same
+    function; here both run the same kernel."""
+    del config, policy
+    m, k = a.shape
+    if m != 1 or int(group_size) != 32 or k % 32 != 0:
+        raise ValueError("group32 fused gate/up requires M=1 and aligned group32 K")
+    if tuple(gate_qweight.shape) != tuple(up_qweight.shape):
+        raise ValueError("group32 fused gate/up qweight shape mismatch")
+    if tuple(gate_scales.shape) != tuple(up_scales.shape):
+        raise ValueError("group32 fused gate/up scale shape mismatch")
+    if int(gate_qweight.shape[1]) * 8 != k:
+        raise ValueError("group32 fused gate/up K mismatch")
+    return _gate_up_m1("group32 fused gate/up", a, gate_qweight, up_qweight, gate_scales, up_scales,
+                       group_size, activation, out)
+
+
+def packed_int4_symmetric_fused_gate_up_m1_safe(a, gate_qweight, up_qweight, gate_scales, up_scales,
+                                                group_size, *, activation: str = "silu", out=None,
+                                                config: Any | None = None, policy: dict | None = None
+                                                ) -> tuple[torch.Tensor, bool, str]:
+    """Never raises; ``(out, True, "ok")`` or ``(a, False, reason)`` with the reference's
+    checks, order and reason strings (``awq_fused_gemm.py:3647-3710``)."""
+    if not awq_fused_gate_up_enabled(config=config, policy=policy):
+        return a, False, "disabled"
+    if a.dim() != 2 or int(a.shape[0]) != 1:
+        return a, False, "input_not_m1_2d"
+    if gate_qweight.dim() != 2 or up_qweight.dim() != 2:
+        return a, False, "qweight_not_2d"
+    if gate_scales.dim() != 2 or up_scales.dim() != 2:
+        return a, False, "scales_not_2d"
+    if tuple(gate_qweight.shape) != tuple(up_qweight.shape):
+        return a, False, "qweight_shape_mismatch"
+    if tuple(gate_scales.shape) != tuple(up_scales.shape):
+        return a, False, "scale_shape_mismatch"
+    if a.dtype not in (torch.float16, torch.bfloat16):
+        return a, False, f"unsupported_dtype_{str(a.dtype)}"
+    if int(group_size) != 32:
+        return a, False, "group_size_not_32"
+    if int(a.shape[1]) != int(gate_qweight.shape[1]) * 8:
+        return a, False, "k_mismatch"
+    if int(a.shape[1]) % 32 != 0:
+        return a, False, "k_not_group_aligned"
+    dev = a.device
+    if any(t.device != dev for t in (gate_qweight, up_qweight, gate_scales, up_scales)):
+        return a, False, "device_mismatch"
+    try:
+        runner = (packed_int4_symmetric_fused_gate_up_group32_m1
+                  if awq_fused_gate_up_group32_enabled(config=config, policy=policy)
+                  else packed_int4_symmetric_fused_gate_up_m1)
+        c = runner(a.contiguous(), gate_qweight.contiguous(), up_qweight.contiguous(),
+                   gate_scales.contiguous(), up_scales.contiguous(), int(group_size),
+                   activation=activation, out=out, config=config, policy=policy)
+        if c.shape != (1, int(gate_qweight.shape[0])):
             return c, False, "bad_output_shape"
         return c, True, "ok"
     except Exception:

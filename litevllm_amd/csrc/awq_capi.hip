@@ -253,4 +253,70 @@ int awq_w4a16_moe(const void* x, int64_t ldx, const void* topk_ids, int32_t ids_
   return launch_moe(c, (hipStream_t)stream);
 }
 
+int awq_w4a16_gate_up_interleave(const void* gate, const void* up, void* out, int64_t rows, int64_t cols,
+                                 int32_t elem_bytes, int32_t half_tile, void* stream) {
+  if (rows < 0 || cols < 0 || half_tile <= 0) return AWQ_ERR_SHAPE;
+  if (elem_bytes != 2 && elem_bytes != 4) return AWQ_ERR_UNSUPPORTED;
+  if (rows == 0 || cols == 0) return AWQ_OK;
+  if (!gate || !up || !out) return AWQ_ERR_NULL;
+  return launch_gate_up_interleave(gate, up, out, rows, cols, elem_bytes, half_tile, (hipStream_t)stream);
+}
+
+size_t awq_w4a16_gate_up_workspace_bytes(int64_t M, int64_t I, int64_t K, int32_t group_size,
+                                         int32_t split_k, int32_t layout) {
+  if (I <= 0) return 0;
+  return awq_w4a16_gemm_workspace_bytes(M, 2 * cdiv(I, 64) * 64, K, group_size, split_k, layout);
+}
+
+int awq_w4a16_gate_up_act(const void* x, int64_t ldx, const int32_t* qweight, const void* scales,
+                          const int32_t* qzeros, void* out, int64_t ldo, int64_t M, int64_t I, int64_t K,
+                          int32_t group_size, int32_t split_k, int32_t layout, int32_t activation,
+                          int32_t act_dtype, int32_t scale_dtype, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  if (M < 0 || I < 0 || K <= 0 || group_size <= 0 || split_k < 0) return AWQ_ERR_SHAPE;
+  if (M == 0 || I == 0) return AWQ_OK;
+  if (!x || !qweight || !scales || !out) return AWQ_ERR_NULL;
+  if (!dtype_16(act_dtype) || !dtype_16(scale_dtype)) return AWQ_ERR_UNSUPPORTED;
+  if (activation != AWQ_MOE_ACT_SILU && activation != AWQ_MOE_ACT_GELU_TANH) return AWQ_ERR_UNSUPPORTED;
+  if (layout != AWQ_LAYOUT_AUTOAWQ && layout != AWQ_LAYOUT_KN_SEQ && layout != AWQ_LAYOUT_DECODE_STREAM)
+    return AWQ_ERR_UNSUPPORTED;
+  if (!decode_covers(M, group_size)) return AWQ_ERR_UNSUPPORTED;
+  if ((K % group_size) != 0) return AWQ_ERR_SHAPE;
+  if (ldx < K || ldo < I || (ldx % 8) != 0) return AWQ_ERR_STRIDE;
+  if ((((uintptr_t)x) & 15) || (((uintptr_t)out) & 1) || (((uintptr_t)scales) & 15) ||
+      (((uintptr_t)qweight) & 15))
+    return AWQ_ERR_STRIDE;
+  const int64_t N = 2 * cdiv(I, 64) * 64;  // the interleaved matrix
+  if (decode_stream_bytes(K, N) > 0x7FFFFFFFLL || M * ldx * 2 > 0x7FFFFFFFLL) return AWQ_ERR_UNSUPPORTED;
+
+  GemmArgs ga{};
+  ga.a = (const uint16_t*)x;
+  ga.qw = (const uint32_t*)qweight;
+  ga.sc = (const uint16_t*)scales;
+  ga.qz = (const uint32_t*)qzeros;
+  ga.c = (uint16_t*)out;
+  ga.lda = ldx;
+  ga.ldc = ldo;
+  ga.M = (int)M;
+  ga.N = (int)N;
+  ga.K = (int)K;
+  ga.G = group_size;
+  ga.bias_dtype = AWQ_DTYPE_NONE;
+  ga.gate_act = 1 + activation;
+  ga.n_out = (int)I;
+  const DecodeMode mode = decode_mode(layout, act_dtype, scale_dtype);
+  const DecodePlan sp = plan_decode(M, N, K, group_size, split_k, mode);
+  if (sp.ws_bytes) {
+    if (!workspace || workspace_bytes < sp.ws_bytes) return AWQ_ERR_WORKSPACE;
+    if ((size_t)sp.tiles * sizeof(int) > kCounterBytes) return AWQ_ERR_UNSUPPORTED;
+    if (sp.ws_bytes - kCounterBytes > 0x7FFFFFFFu) return AWQ_ERR_UNSUPPORTED;  // 32-bit offsets
+    ga.counters = (int*)workspace;
+    ga.partial = (float*)((char*)workspace + kCounterBytes);
+  }
+  if (!launch_decode(ga, sp, mode, layout == AWQ_LAYOUT_KN_SEQ, qzeros != nullptr, act_dtype, scale_dtype,
+                     (hipStream_t)stream))
+    return AWQ_ERR_UNSUPPORTED;
+  return launch_status();
+}
+
 }  // extern "C"

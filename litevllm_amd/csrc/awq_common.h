@@ -138,6 +138,17 @@ __device__ __forceinline__ float load_bias(const void* bias, int dtype, int col)
   return 0.0f;
 }
 
+// act(g) of the reference's gated MLP kernels (awq_fused_gemm.py:1493-1502,
+// gemma4_moe_int4.py:748-756): kind 1 is GELU in its tanh form written as
+// g * sigmoid(2 * inner), 0.5 * (1 + tanh(y)) == sigmoid(2y); otherwise SiLU.
+__device__ __forceinline__ float gated_act(float g, int kind) {
+  if (kind == 1) {
+    const float inner = 0.7978845608028654f * (g + 0.044715f * g * g * g);
+    return g / (1.0f + expf(-2.0f * inner));
+  }
+  return g / (1.0f + expf(-g));
+}
+
 // Shared argument block of the GEMM kernels.
 struct GemmArgs {
   const uint16_t* a;
@@ -151,6 +162,10 @@ struct GemmArgs {
   int64_t lda, ldc;
   int M, N, K, G;
   int bias_dtype;
+  // decode only: 0 = plain GEMM; 1 + activation kind = gated epilogue.  Each 128-column tile
+  // then holds 64 gate columns and the 64 up columns of the same outputs, and output column
+  // 64 t + j (j < 64, below n_out) is act(gate) * up of tile t's columns j and 64 + j.
+  int gate_act, n_out;
 };
 
 // Work decomposition of the decode kernel: tiles x ksteps units; each tile's k-steps are cut

@@ -256,6 +256,21 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
     }
   __syncthreads();
   const int ncols = min(128, p.N - t * 128);
+  if (S == 1 && p.gate_act) {
+    // gated epilogue: column j < 64 of the tile is a gate sum, 64 + j the matching up sum
+    for (int o = tid; o < M * 64; o += NWV * 64) {
+      const int m = o >> 6, col = o & 63;
+      float g = red[m * 128 + col], u = red[m * 128 + 64 + col];
+#pragma unroll
+      for (int w = 1; w < NWV; ++w) {
+        g += red[(w * MROWS + m) * 128 + col];
+        u += red[(w * MROWS + m) * 128 + 64 + col];
+      }
+      const int oc = t * 64 + col;
+      if (oc < p.n_out) p.c[(int64_t)m * p.ldc + oc] = to_bits<T>(gated_act(g, p.gate_act - 1) * u);
+    }
+    return;
+  }
   for (int o = tid; o < M * 128; o += NWV * 64) {
     const int m = o >> 7, col = o & 127;
     float sum = red[m * 128 + col];
@@ -281,6 +296,35 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
   // the last of the S blocks of tile t sums the partials in split (k) order, adds the bias
   // and writes the output (all threads of the block)
   const uint32_t pstride = (uint32_t)tile_floats * 4u;  // bytes between splits
+  if (p.gate_act) {
+    // gated epilogue: gate columns 2ch, 2ch + 1 and their up columns 64 further on, each
+    // summed over the splits in split order like the plain output
+    for (int idx = tid; idx < M * 32; idx += NWV * 64) {
+      const int m = idx >> 5, ch = idx & 31;
+      const uint32_t off = tbase + ((uint32_t)m * 128u + 2u * (uint32_t)ch) * 4u;
+      f32x2 g = {0.f, 0.f}, u = {0.f, 0.f};
+      for (int c0 = 0; c0 < S; c0 += 4) {
+        f32x2 vg[4], vu[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t o = (c0 + e < S) ? off + (uint32_t)(c0 + e) * pstride : 0x80000000u;
+          vg[e] = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(prs, (int)o, 0, kDeviceCoherent));
+          vu[e] = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(prs, (int)(o + 256u), 0, kDeviceCoherent));
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          g += vg[e];
+          u += vu[e];
+        }
+      }
+      const int oc = t * 64 + 2 * ch;
+      uint16_t* dst = p.c + (int64_t)m * p.ldc + oc;
+      if (oc < p.n_out) dst[0] = to_bits<T>(gated_act(g[0], p.gate_act - 1) * u[0]);
+      if (oc + 1 < p.n_out) dst[1] = to_bits<T>(gated_act(g[1], p.gate_act - 1) * u[1]);
+    }
+    if (tid == 0) __hip_atomic_store(&p.counters[t], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
   const int nh = ncols >> 1;  // float2 chunks per row
   for (int idx = tid; idx < M * nh; idx += NWV * 64) {
     const int m = idx / nh, ch = idx - m * nh;

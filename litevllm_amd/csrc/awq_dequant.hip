@@ -152,6 +152,23 @@ __global__ void __launch_bounds__(256) pack_stream_kernel(const uint32_t* __rest
   }
 }
 
+// Gate/up interleave: out row r, column c = 2 half b + w takes element b half + (w mod half)
+// of gate (w < half) or up (w >= half), zero past the source's last column.
+template <typename E>
+__global__ void __launch_bounds__(256) gate_up_interleave_kernel(const E* __restrict__ gate,
+                                                                 const E* __restrict__ up,
+                                                                 E* __restrict__ out, int64_t rows,
+                                                                 int64_t cols, int64_t half,
+                                                                 int64_t ocols) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= rows * ocols) return;
+  const int64_t r = idx / ocols, c = idx - r * ocols;
+  const int64_t b = c / (2 * half), w = c - b * 2 * half;
+  const bool is_up = w >= half;
+  const int64_t sc = b * half + (is_up ? w - half : w);
+  out[idx] = sc < cols ? (is_up ? up : gate)[r * cols + sc] : (E)0;
+}
+
 }  // namespace awq
 
 namespace awq_host {
@@ -255,6 +272,21 @@ int launch_pack_decode_stream(const int32_t* qweight_kn, int32_t* out, int64_t K
   if (n > 0)
     hipLaunchKernelGGL(pack_stream_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st,
                        (const uint32_t*)qweight_kn, (uint32_t*)out, K, NW, tiles);
+  return launch_status();
+}
+
+int launch_gate_up_interleave(const void* gate, const void* up, void* out, int64_t rows, int64_t cols,
+                              int elem_bytes, int64_t half, hipStream_t st) {
+  const int64_t ocols = 2 * cdiv(cols, half) * half;
+  const int64_t n = rows * ocols;
+  if (n == 0) return AWQ_OK;
+  const dim3 grid((unsigned)cdiv(n, 256));
+  if (elem_bytes == 4)
+    hipLaunchKernelGGL(gate_up_interleave_kernel<uint32_t>, grid, dim3(256), 0, st, (const uint32_t*)gate,
+                       (const uint32_t*)up, (uint32_t*)out, rows, cols, half, ocols);
+  else
+    hipLaunchKernelGGL(gate_up_interleave_kernel<uint16_t>, grid, dim3(256), 0, st, (const uint16_t*)gate,
+                       (const uint16_t*)up, (uint16_t*)out, rows, cols, half, ocols);
   return launch_status();
 }
 

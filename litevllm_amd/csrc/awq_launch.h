@@ -58,6 +58,10 @@ int launch_repack_nk_to_autoawq(const int32_t* qweight_nk, const int32_t* qzeros
                                 void* scales_kn, int64_t N, int64_t K, int32_t group_size,
                                 hipStream_t st);
 
+// Gate/up interleave of the gated decode epilogue (elem_bytes 2 or 4).
+int launch_gate_up_interleave(const void* gate, const void* up, void* out, int64_t rows, int64_t cols,
+                              int elem_bytes, int64_t half, hipStream_t st);
+
 // ---- mixture of experts ----
 // Stream-packed expert stacks: gate_up (N = 2I) pairs 8 gate words with the 8 up words of the
 // same columns per tile (tiles = ceil(I / 64)); down (gate_up = 0) uses tiles of 16 words.

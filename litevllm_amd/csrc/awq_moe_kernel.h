@@ -59,15 +59,6 @@ __device__ __forceinline__ float load_route_weight(const void* rw, int dtype, in
   return ((const float*)rw)[r];
 }
 
-// act(g) of gemma4_moe_int4.py:748-756: silu, or GELU (tanh form) as g * sigmoid(2 * inner)
-__device__ __forceinline__ float moe_act(float g, int kind) {
-  if (kind == 1) {
-    const float inner = 0.7978845608028654f * (g + 0.044715f * g * g * g);
-    return g / (1.0f + expf(-2.0f * inner));
-  }
-  return g / (1.0f + expf(-g));
-}
-
 // MT: 16-route tiles per wave group.  SBF: scales are bf16 (fp16 otherwise).  Like the decode
 // kernel, the MFMAs multiply the activations by the exact integers q - z and each group's
 // fp32 sum is scaled once by the group's scale, so the weights enter unrounded -- the
@@ -297,7 +288,7 @@ moe_gemm_kernel(const MoeArgs p) {
               const float wgt = load_route_weight(p.rw, p.rw_dtype, rt);
               float h[8];
 #pragma unroll
-              for (int c = 0; c < 8; ++c) h[c] = moe_act(o[c], p.act_kind) * u[c] * wgt;
+              for (int c = 0; c < 8; ++c) h[c] = gated_act(o[c], p.act_kind) * u[c] * wgt;
               u32x4 st;
               st[0] = pack2<T>(h[0], h[1]);
               st[1] = pack2<T>(h[2], h[3]);

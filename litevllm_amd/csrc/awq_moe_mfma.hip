@@ -230,7 +230,7 @@ __global__ void __launch_bounds__(512, 1) moe_mfma_kernel(const MoeArgs p, int s
         for (int nt = 0; nt < 2; ++nt) {
           const int gc = 128 * tn + 32 * wave_n + nt * 16 + r;  // gate column
           if (gc >= 8 * p.half) continue;
-          const float h = moe_act(acc[mt][nt][v], p.act_kind) * acc[mt][nt + 2][v] * wgt;
+          const float h = gated_act(acc[mt][nt][v], p.act_kind) * acc[mt][nt + 2][v] * wgt;
           ((uint16_t*)p.out)[(int64_t)rt * p.ldo + gc] = to_bits<T>(h);
         }
       } else {

@@ -85,3 +85,44 @@ def try_fused_awq_pair_matmul(x: torch.Tensor, lin_a, lin_b, owner: nn.Module, c
     lead = x.shape[:-1]
     out = fused.matmul(x.reshape(-1, x.shape[-1]), fused_bias, config=inf_config)
     return out.reshape(*lead, 2 * int(lin_a.output_size))
+
+
+def try_fused_awq_gate_up_activation(x: torch.Tensor, gate_proj, up_proj, *, activation: str,
+                                     lora_mapping: Any = None, inf_config: Any = None):
+    """``act(gate_proj(x)) * up_proj(x)`` in one launch for decode (one token), or ``None``
+    where the reference declines (``_fused_awq_pair.py:169-240``): active LoRA, mismatched
+    sizes or group sizes, bias, high-fidelity layers, zero points, more than one token, or
+    the policy switch ``awq_fused_gate_up`` off."""
+    from .awq_fused_gemm import packed_int4_symmetric_fused_gate_up_m1_safe
+
+    if _lora_is_active(lora_mapping):
+        return None
+    if gate_proj.input_size != up_proj.input_size or gate_proj.output_size != up_proj.output_size:
+        return None
+    if getattr(gate_proj, "bias", None) is not None or getattr(up_proj, "bias", None) is not None:
+        return None
+    if getattr(gate_proj, "force_high_fidelity_awq", False) or getattr(up_proj, "force_high_fidelity_awq", False):
+        return None
+    if _present(getattr(gate_proj, "qzeros", None)) or _present(getattr(up_proj, "qzeros", None)):
+        return None
+    qwg, qwu = getattr(gate_proj, "qweight", None), getattr(up_proj, "qweight", None)
+    if not _present(qwg) or not _present(qwu) or tuple(qwg.shape) != tuple(qwu.shape):
+        return None
+    if tuple(gate_proj.scales.shape) != tuple(up_proj.scales.shape):
+        return None
+    gs = int(getattr(gate_proj, "group_size", 128))
+    if int(getattr(up_proj, "group_size", 128)) != gs:
+        return None
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, x.shape[-1])
+    if int(x2.shape[0]) != 1:
+        return None
+    try:
+        out, used, _ = packed_int4_symmetric_fused_gate_up_m1_safe(
+            x2.contiguous(), qwg, qwu, gate_proj.scales, up_proj.scales, gs, activation=activation,
+            config=inf_config)
+        if not used:
+            return None
+        return out.reshape(*lead, int(gate_proj.output_size))
+    except Exception:
+        return None

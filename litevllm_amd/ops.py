@@ -266,6 +266,108 @@ def gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, qzeros: t
     return out
 
 
+# ------------------------------------------------------------------ gated MLP (gate + up)
+def gate_up_interleave(gate: torch.Tensor, up: torch.Tensor, half_tile: int) -> torch.Tensor:
+    """Two [rows, cols] matrices (2- or 4-byte elements) -> [rows, 2 * ceil(cols / half_tile) *
+    half_tile], runs of ``half_tile`` gate elements each followed by the same run of up."""
+    lib = L.load()
+    _require_device(gate, up)
+    if gate.shape != up.shape or gate.dtype != up.dtype or gate.dim() != 2:
+        raise ValueError("gate and up must be 2-D tensors of one shape and dtype")
+    rows, cols = int(gate.shape[0]), int(gate.shape[1])
+    ocols = 2 * (-(-cols // int(half_tile))) * int(half_tile)
+    gate, up = gate.contiguous(), up.contiguous()
+    out = torch.empty((rows, ocols), dtype=gate.dtype, device=gate.device)
+    rc = lib.awq_w4a16_gate_up_interleave(_ptr(gate), _ptr(up), _ptr(out), rows, cols,
+                                          int(gate.element_size()), int(half_tile),
+                                          _stream_ptr(gate.device))
+    L.check("awq_w4a16_gate_up_interleave", rc)
+    return out
+
+
+def _pad_rows(t: torch.Tensor | None, rows: int) -> torch.Tensor | None:
+    if t is None or int(t.shape[0]) == rows:
+        return t
+    pad = torch.zeros((rows - int(t.shape[0]),) + tuple(t.shape[1:]), dtype=t.dtype, device=t.device)
+    return torch.cat([t, pad], 0)
+
+
+def pack_gate_up(gate_qweight, up_qweight, gate_scales, up_scales, gate_qzeros, up_qzeros,
+                 group_size: int, layout: str = "ref", stream: bool = False):
+    """The interleaved gate/up matrix of ``gate_up_act``: ``(qweight [K, N/8], scales [K/G, N],
+    qzeros [K/G, N/8] or None, decode stream copy or None)`` with N = 2 * ceil(I / 64) * 64.
+
+    ``layout="ref"`` takes the reference's [I, K/8] weights and [I, K/G] scales (I need not be
+    a multiple of 8: the missing rows are zero weights with zero scales); "autoawq" takes
+    [K, I/8] / [K/G, I]."""
+    if layout == "ref":
+        i = int(gate_qweight.shape[0])
+        i8 = -(-i // 8) * 8
+        packed = []
+        for qw, sc, qz in ((gate_qweight, gate_scales, gate_qzeros), (up_qweight, up_scales, up_qzeros)):
+            packed.append(repack_ref_to_autoawq(_pad_rows(qw.contiguous(), i8), _pad_rows(sc.contiguous(), i8),
+                                                _pad_rows(qz.contiguous(), i8) if qz is not None else None,
+                                                int(group_size)))
+        (gq, gs, gz), (uq, us, uz) = packed
+    else:
+        gq, gs, gz, uq, us, uz = gate_qweight, gate_scales, gate_qzeros, up_qweight, up_scales, up_qzeros
+    qw = gate_up_interleave(gq, uq, 8)
+    sc = gate_up_interleave(gs, us, 64)
+    qz = gate_up_interleave(gz, uz, 8) if gz is not None else None
+    return qw, sc, qz, (pack_decode_stream(qw) if stream else None)
+
+
+GATE_UP_CACHE = _DerivedCache(pack_gate_up)
+
+GATE_UP_ACTIVATIONS = {"silu": L.MOE_ACT_SILU, "gelu": L.MOE_ACT_GELU_TANH,
+                       "gelu_pytorch_tanh": L.MOE_ACT_GELU_TANH}
+
+
+def gate_up_act(x: torch.Tensor, gate_qweight: torch.Tensor, up_qweight: torch.Tensor,
+                gate_scales: torch.Tensor, up_scales: torch.Tensor, group_size: int,
+                gate_qzeros: torch.Tensor | None = None, up_qzeros: torch.Tensor | None = None,
+                activation: str = "silu", layout: str = "ref", out: torch.Tensor | None = None,
+                split_k: int = 0) -> torch.Tensor:
+    """``out[M, I] = act(x @ Wg^T) * (x @ Wu^T)`` in one launch of the decode kernel with its
+    gated epilogue (M <= 32).  ``activation``: "gelu" / "gelu_pytorch_tanh" select GELU (tanh
+    form), anything else SiLU, as the reference decides (awq_fused_gemm.py:3040-3041).  The
+    interleaved weight pair is built once and cached."""
+    lib = L.load()
+    if x.dim() != 2:
+        raise ValueError("x must be 2-D")
+    dev = _require_device(x, gate_qweight, up_qweight, gate_scales, up_scales, gate_qzeros, up_qzeros, out)
+    if (gate_qzeros is None) != (up_qzeros is None):
+        raise ValueError("gate and up zeros must both be given or both be None")
+    M, K = int(x.shape[0]), int(x.shape[1])
+    if layout == "ref":
+        I, kw = int(gate_qweight.shape[0]), int(gate_qweight.shape[1]) * 8
+    else:
+        kw, I = int(gate_qweight.shape[0]), int(gate_qweight.shape[1]) * 8
+    if kw != K:
+        raise ValueError(f"K mismatch: x has {K}, weights have {kw}")
+    act = GATE_UP_ACTIVATIONS.get(str(activation).lower(), L.MOE_ACT_SILU)
+    use_stream = (x.dtype == torch.float16 and gate_scales.dtype == torch.float16 and K % 32 == 0
+                  and M <= DECODE_MAX_M)
+    qw, sc, qz, st = GATE_UP_CACHE.get(gate_qweight, up_qweight, gate_scales, up_scales, gate_qzeros,
+                                       up_qzeros, args=(int(group_size), layout, use_stream))
+    lc = L.LAYOUT_DECODE_STREAM if st is not None else L.LAYOUT_AUTOAWQ
+    if st is not None:
+        qw = st
+    x = x if x.stride(1) == 1 and x.stride(0) % 8 == 0 else x.contiguous()
+    if out is None:
+        out = torch.empty((M, I), dtype=x.dtype, device=dev)
+    if out.stride(1) != 1:
+        raise ValueError("out must have unit column stride")
+    ws_bytes = int(lib.awq_w4a16_gate_up_workspace_bytes(M, I, K, int(group_size), int(split_k), lc))
+    ws = WORKSPACE.get(dev, ws_bytes) if ws_bytes else None
+    rc = lib.awq_w4a16_gate_up_act(
+        _ptr(x), int(x.stride(0)), _ptr(qw), _ptr(sc), _ptr(qz), _ptr(out), int(out.stride(0)), M, I, K,
+        int(group_size), int(split_k), lc, act, dtype_code(x.dtype), dtype_code(sc.dtype), _ptr(ws),
+        ws_bytes if ws is not None else 0, _stream_ptr(dev))
+    L.check("awq_w4a16_gate_up_act", rc)
+    return out
+
+
 # ------------------------------------------------------------------ mixture of experts
 MOE_ACTIVATIONS = {"silu": L.MOE_ACT_SILU, "swish": L.MOE_ACT_SILU,
                    "gelu": L.MOE_ACT_GELU_TANH, "gelu_pytorch_tanh": L.MOE_ACT_GELU_TANH}

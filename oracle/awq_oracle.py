@@ -233,10 +233,29 @@ def moe_act(g: np.ndarray, activation: str = "silu") -> np.ndarray:
     (``vllm/kernels/triton/gemma4_moe_int4.py:748-756``): silu ``g / (1 + e^-g)``, or the
     tanh-form GELU ``g / (1 + e^(-2 * 0.79788456 (g + 0.044715 g^3)))``."""
     g = np.asarray(g, dtype=np.float64)
-    if str(activation).lower() in ("gelu", "gelu_pytorch_tanh"):
-        inner = 0.7978845608028654 * (g + 0.044715 * g * g * g)
-        return g / (1.0 + np.exp(-2.0 * inner))
-    return g / (1.0 + np.exp(-g))
+    with np.errstate(over="ignore"):  # e^large = inf gives the limit g / inf = -0
+        if str(activation).lower() in ("gelu", "gelu_pytorch_tanh"):
+            inner = 0.7978845608028654 * (g + 0.044715 * g * g * g)
+            return g / (1.0 + np.exp(-2.0 * inner))
+        return g / (1.0 + np.exp(-g))
+
+
+def gate_up_exact(x, w_gate, w_up, activation="silu"):
+    """Dense gated MLP input ``act(x @ Wg^T) * (x @ Wu^T)`` in float64, returned unrounded:
+    the M = 1 fused gate/up kernels of ``vllm/kernels/triton/awq_fused_gemm.py:1406-1506``
+    sum ``x * (q - 8) * s`` in fp32 for both projections, apply the activation
+    (:func:`moe_act`'s mapping, ``3040-3041``) and cast once.  ``w_gate`` / ``w_up`` are the
+    dequantized [N, K] weights (pass float32 products for the unrounded ``(q - z) * s``).
+
+    Pinned by: ``torch.nn.functional.silu`` / ``gelu(approximate="tanh")`` of float64
+    ``F.linear`` products, the reference tests' own construction
+    (``tests/test_gemma4_mlp_pair_fusion.py:260-356``), and the identity-weight case that
+    reduces to the activation of ``x`` times ``x``.
+    """
+    x = np.asarray(x, dtype=np.float64)
+    g = x @ np.asarray(w_gate, dtype=np.float64).T
+    u = x @ np.asarray(w_up, dtype=np.float64).T
+    return moe_act(g, activation) * u
 
 
 def moe_grouped_exact(x_f16, topk_weights, topk_ids, w1, w2, activation="silu", inter_dtype="float16"):
