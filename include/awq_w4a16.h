@@ -54,7 +54,7 @@ extern "C" {
  * AWQ_LAYOUT_DECODE_STREAM : an AUTOAWQ qweight re-ordered by awq_w4a16_pack_decode_stream so
  *                      that the decode kernel reads it as contiguous 2 KiB runs; qzeros and
  *                      scales stay in the AUTOAWQ layout.  Accepted by awq_w4a16_gemm for
- *                      M <= 32, group sizes 32/64/128, f16 activations and scales.
+ *                      M <= 32 and group sizes 32/64/128.
  */
 #define AWQ_LAYOUT_AUTOAWQ 0
 #define AWQ_LAYOUT_KN_SEQ 1
@@ -227,7 +227,7 @@ size_t awq_w4a16_gate_up_workspace_bytes(int64_t M, int64_t I, int64_t K, int32_
  *   x: [M, K] act_dtype (F16 or BF16), row stride ldx; out: [M, I] act_dtype, row stride ldo.
  *   qweight / scales / qzeros: the interleaved matrix in layout AUTOAWQ or KN_SEQ
  *   ([K, N/8] words, N = 2 * ceil(I / 64) * 64) or DECODE_STREAM (its awq_w4a16_pack_decode_stream
- *   copy; F16 activations and scales); qzeros NULL = symmetric z = 8 (the reference's mode).
+ *   copy); qzeros NULL = symmetric z = 8 (the reference's mode).
  *   1 <= M <= 32 (the reference takes M == 1); group_size 32, 64 or 128 dividing K.
  *   split_k as for awq_w4a16_gemm; results are bitwise reproducible for a given split. */
 int awq_w4a16_gate_up_act(const void* x, int64_t ldx, const int32_t* qweight, const void* scales,

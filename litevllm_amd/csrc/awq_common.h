@@ -264,6 +264,131 @@ __device__ __forceinline__ u32x4 int_operand(const uint32_t (&mlo)[4], const uin
   return r;
 }
 
+// Biased-integer MFMA operands of the decode kernels: eight rows (k .. k+7) of nibble I as
+// exact values in T whose activation-weighted sums a kernel turns back into sum x (q - z)
+// when it scales the group (biased_terms), using the group's activation sum, i.e. the same
+// MFMA against ones:
+//  * fp16 (exponent 6, 64 + mantissa / 16): nibbles P = 0, 1 of each 16-bit half are
+//    masked into mantissa bits 4-7 (P = 0 after a 4-bit shift) and read 64 + q_P; nibbles
+//    P = 2, 3 are moved there whole with their neighbour by one byte permute and read
+//    64 + q_P + q_{P-1} / 16 -- one shift per word, one AND-OR or permute per pair of rows;
+//  * bf16 (exponent 7, 128 + mantissa): nibble P shifted to bits 0-3 and masked, 128 + q_P.
+// Small biases keep the fp32 sums' cancellation small (a bias of 1024, fp16 with the nibble
+// at bits 0-3, costs up to 2 fp16 ulps on all-positive activations; 64 stays within the
+// final rounding's half ulp).
+struct BiasK {
+  uint32_t mask, magic;
+};
+template <typename T>
+__device__ __forceinline__ BiasK bias_consts() {
+  BiasK k = std::is_same<T, f16>::value ? BiasK{0x00F000F0u, 0x54005400u} : BiasK{0x000F000Fu, 0x43004300u};
+  asm volatile("" : "+v"(k.mask), "+v"(k.magic));  // VGPR operands (one constant-bus slot per VOP3)
+  return k;
+}
+// 1.0 in both halves: the operand whose MFMA yields the activation sums
+template <typename T>
+__host__ __device__ constexpr uint32_t ones2() {
+  return std::is_same<T, f16>::value ? 0x3C003C00u : 0x3F803F80u;
+}
+template <int I, typename T>
+__device__ __forceinline__ u32x4 biased_operand(const uint32_t (&mlo)[4], const uint32_t (&mhi)[4], const BiasK& k) {
+  constexpr int P = I & 3;
+  u32x4 r;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const uint32_t m = I < 4 ? mlo[u] : mhi[u];
+    if constexpr (std::is_same<T, f16>::value) {
+      const uint32_t w = (P == 0 || P == 2) ? (m << 4) : m;
+      // P 2, 3: bytes 1 and 3 (the nibble and its lower neighbour) under the magic's high bytes
+      r[u] = (P < 2) ? ((w & k.mask) | k.magic) : __builtin_amdgcn_perm(k.magic, w, 0x07030501u);
+    } else {
+      r[u] = ((m >> (4 * P)) & k.mask) | k.magic;
+    }
+  }
+  return r;
+}
+// (bias + z) of nibble i of a zero word as fp32, built from its bits: 64 + z = 2^6 (1 + z/64),
+// 128 + z = 2^7 (1 + z/128) (a bit-field extract and a shift-or, no conversion)
+template <typename T>
+__device__ __forceinline__ float biased_zero(uint32_t zw, int i) {
+  const uint32_t z = (zw >> (4 * i)) & 0xFu;
+  return std::is_same<T, f16>::value ? __builtin_bit_cast(float, 0x42800000u | (z << 17))
+                                     : __builtin_bit_cast(float, 0x43000000u | (z << 16));
+}
+static_assert(__builtin_bit_cast(float, 0x42800000u | (15u << 17)) == 79.0f, "64 + 15");
+static_assert(__builtin_bit_cast(float, 0x43000000u | (15u << 16)) == 143.0f, "128 + 15");
+// Per-group coefficients that turn the biased sums of one 16-bit half (nibbles P = 0..3 at
+// columns i0 + P) into the scaled sums s_P * sum x (q_P - z_P):
+//   fp16: P 0, 1:  s acc_P - s (64 + z) ax
+//         P 2:     s (acc_2 - acc_1 / 16) - s (60 + z) ax
+//         P 3:     s (acc_3 - (acc_2 - acc_1 / 16) / 16) - s (60.25 + z) ax
+//   bf16: every P: s acc_P - s (128 + z) ax
+struct HalfCoef {
+  float s[4], cz[4];
+};
+template <typename T>
+__device__ __forceinline__ HalfCoef half_coef(const float (&s)[4], uint32_t zw, int i0) {
+  HalfCoef h;
+#pragma unroll
+  for (int P = 0; P < 4; ++P) {
+    float b = biased_zero<T>(zw, i0 + P);
+    if constexpr (std::is_same<T, f16>::value) b -= (P == 2) ? 4.0f : (P == 3) ? 3.75f : 0.0f;
+    h.s[P] = s[P];
+    h.cz[P] = b * s[P];
+  }
+  return h;
+}
+// tot_P += the scaled sum of nibble P, all fused multiply-adds (the chain terms are taken off
+// the raw sums first: t2 = acc_2 - acc_1 / 16, t3 = acc_3 - t2 / 16, which leaves biases
+// 60 and 60.25 on them)
+template <typename T>
+__device__ __forceinline__ void biased_terms(float (&tot)[4], const float (&acc)[4], float ax, const HalfCoef& h) {
+  float a[4] = {acc[0], acc[1], acc[2], acc[3]};
+  if constexpr (std::is_same<T, f16>::value) {
+    a[2] = __builtin_fmaf(-0.0625f, a[1], a[2]);
+    a[3] = __builtin_fmaf(-0.0625f, a[2], a[3]);
+  }
+#pragma unroll
+  for (int P = 0; P < 4; ++P) tot[P] = __builtin_fmaf(-h.cz[P], ax, __builtin_fmaf(a[P], h.s[P], tot[P]));
+}
+template <typename T>
+__device__ __forceinline__ void biased_terms(f32x4 (&tot)[4], const f32x4 (&acc)[4], const f32x4& ax, const HalfCoef& h) {
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    float t[4] = {tot[0][v], tot[1][v], tot[2][v], tot[3][v]};
+    const float a[4] = {acc[0][v], acc[1][v], acc[2][v], acc[3][v]};
+    biased_terms<T>(t, a, ax[v], h);
+#pragma unroll
+    for (int P = 0; P < 4; ++P) tot[P][v] = t[P];
+  }
+}
+
+// tot[i][mt] += the scaled sums of a group (AutoAWQ nibble order) from its biased sums acc,
+// activation sums ax, raw scales s4 and zero word zw
+template <typename T, bool SBF, int MT>
+__device__ __forceinline__ void flush_biased(f32x4 (&tot)[8][MT], const f32x4 (&acc)[8][MT], const f32x4 (&ax)[MT],
+                                             const u32x4& s4, uint32_t zw) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    float sc[4];
+#pragma unroll
+    for (int P = 0; P < 4; ++P) {
+      const int c = nib_col<false>(4 * h + P);
+      const uint16_t sb = (uint16_t)(s4[c >> 1] >> (16 * (c & 1)));
+      sc[P] = SBF ? bf_bits2f(sb) : h_bits2f(sb);
+    }
+    const HalfCoef hc = half_coef<T>(sc, zw, 4 * h);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      f32x4 tv[4] = {tot[4 * h][mt], tot[4 * h + 1][mt], tot[4 * h + 2][mt], tot[4 * h + 3][mt]};
+      const f32x4 av[4] = {acc[4 * h][mt], acc[4 * h + 1][mt], acc[4 * h + 2][mt], acc[4 * h + 3][mt]};
+      biased_terms<T>(tv, av, ax[mt], hc);
+#pragma unroll
+      for (int P = 0; P < 4; ++P) tot[4 * h + P][mt] = tv[P];
+    }
+  }
+}
+
 // Buffer resource over a whole tensor (raw addressing, bounds = nbytes).  Range checks
 // cover the VGPR offset only (the SGPR offset is excluded), so anything that must read as
 // zero past the end has to carry its position in the VGPR offset.

@@ -12,11 +12,13 @@
 //    8q .. 8q+7.  For each nibble i the lane builds one 32 k x 16 column operand of
 //    v_mfma_f32_16x16x32_{f16,bf16} and multiplies the activations (16 tokens x 32 k) by it,
 //    so lane (q, r) accumulates tokens 4q .. 4q+3 of column 8 * word + nib_col(i).
-//  * The weights enter the MFMA as the exact integers q - z, so each group's products and
-//    sums are fp32-exact up to the accumulation's own rounding; when the group ends its sum
-//    is multiplied once by the group's fp32 scale.  This is the reference's M = 1
-//    formulation, b = (q - z) * s kept in fp32 and never rounded (awq_fused_gemm.py:1966-1971);
-//    its tl.dot path for M > 1 rounds b to fp16 first (1973-1976), which this kernel does not.
+//  * The weights enter the MFMA as the exact biased integers B + q (biased_operand: one
+//    AND-OR per pair of rows, no subtraction), and one more MFMA per k-step against ones sums
+//    the activations; when a group ends, (B + z) times that sum is taken off each column's sum
+//    and the result is multiplied once by the group's fp32 scale.  So the weights are
+//    (q - z) * s, never rounded -- the reference's M = 1 formulation, b = (q - z) * s kept in
+//    fp32 (awq_fused_gemm.py:1966-1971); its tl.dot path for M > 1 rounds b to fp16 first
+//    (1973-1976), which this kernel does not.
 //  * Each wave keeps a D-deep ring of k-steps in registers.  Scheduling barriers pin every
 //    slot's refill right after the slot is consumed, so D-1 k-steps of loads stay in flight
 //    while one is dequantized and multiplied.
@@ -46,6 +48,11 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
   static_assert((SPG & (SPG - 1)) == 0, "");
   static_assert(NWV >= 2 && (NWV & (NWV - 1)) == 0, "power-of-two waves per block");
   static_assert(!ONE || MT == 1, "");
+  // Biased operands (one AND-OR or permute per pair of rows, the zero taken off per group) pay
+  // when a group spans several k-steps of one token tile, and always for bf16 (whose exact
+  // integer operands need conversions); otherwise the exact integers q - z (one more packed
+  // subtraction per pair of rows, a single multiply-add per group) are cheaper.
+  constexpr bool BIASED = (SPG >= 2 && MT == 1) || (!std::is_same<T, f16>::value && !(MT == 2 && SPG == 1));
   constexpr int MROWS = ONE ? 1 : 16 * MT;  // token rows a wave can hold
   __shared__ float red[NWV * MROWS * 128];  // every wave's sums: [wave][token][tile column]
   __shared__ int s_last;
@@ -63,7 +70,8 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
   const int nunits = k0 + len * (wave + 1) / NWV - w0;
   const int word = t * 16 + r;  // the lane's packed word
 
-  f32x4 acc[8][MT];  // the current group's sums, integer weights
+  f32x4 acc[8][MT];  // the current group's sums, biased integer weights B + q
+  f32x4 ax[MT];      // the current group's activation sums (the bias correction)
   f32x4 tot[8][MT];  // the scaled sums of the groups done (general case)
   float tot1[8];     // the same when ONE (element 0 only)
 #pragma unroll
@@ -72,6 +80,8 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[i][mt] = tot[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) ax[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int ngroups = p.K / p.G;
   const uint32_t row_bytes = (uint32_t)NW * 4u;
@@ -85,7 +95,9 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
       x_lane_off[mt] = ((uint32_t)(mt * 16 + r) * (uint32_t)p.lda + 8u * (uint32_t)q) * 2u;
+    const BiasK bk = bias_consts<T>();
     const MagicK mk = magic_consts();
+    const u32x4 ones = {ones2<T>(), ones2<T>(), ones2<T>(), ones2<T>()};
     // per-column clamp (columns past N are computed, never stored)
     const uint32_t wc = (uint32_t)min(word, NW - 1);
     const uint32_t w_lane_off = STREAM ? (uint32_t)lane * 16u : (uint32_t)(8 * q) * row_bytes + wc * 4u;
@@ -93,7 +105,8 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
     uint32_t raw[D][8];
     u32x4 xr[D][MT];
     WordSZ sz[D];    // raw constants of each slot's group (used when the group changes)
-    uint32_t zm[8];  // biased zeros of the current group
+    uint32_t zwc;    // zero word of the current group (biased operands)
+    uint32_t zm[8];  // biased zeros of the current group (exact integer operands)
     u32x4 s4;        // scales of the current group (the word's 8 columns, raw 16-bit values)
 
     // Issue cursor over the wave's units, advanced one unit per issue.  Past the last unit the
@@ -151,31 +164,76 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
       }
 #define AWQ_DECODE_NIB(I)                                                                      \
       {                                                                                        \
-        const u32x4 op = int_operand<I, T>(mlo, mhi, zm[I], mk);                               \
+        const u32x4 op = BIASED ? biased_operand<I, T>(mlo, mhi, bk) : int_operand<I, T>(mlo, mhi, zm[I], mk); \
         _Pragma("unroll") for (int mt = 0; mt < MT; ++mt)                                      \
             acc[I][mt] = MfmaOp<T>::run(xr[slot][mt], op, FRESH ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[I][mt]); \
       }
       AWQ_DECODE_NIB(0) AWQ_DECODE_NIB(1) AWQ_DECODE_NIB(2) AWQ_DECODE_NIB(3)
       AWQ_DECODE_NIB(4) AWQ_DECODE_NIB(5) AWQ_DECODE_NIB(6) AWQ_DECODE_NIB(7)
 #undef AWQ_DECODE_NIB
-    };
-    // tot += acc * scale of the group just finished (ZERO: acc restarts from zero)
-    auto flush = [&](auto zero) {
+      if constexpr (BIASED)
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+        for (int mt = 0; mt < MT; ++mt)
+          ax[mt] = MfmaOp<T>::run(xr[slot][mt], ones, FRESH ? f32x4{0.f, 0.f, 0.f, 0.f} : ax[mt]);
+    };
+    // tot += the scaled sums s * sum x (q - z) of the group just finished, from the biased
+    // sums and the activation sums (ZERO: the sums restart from zero)
+    auto flush = [&](auto zero) {
+      if constexpr (!BIASED) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const int c = nib_col<SEQ>(i);
+            const uint16_t sb = (uint16_t)(s4[c >> 1] >> (16 * (c & 1)));
+            const float sf = SBF ? bf_bits2f(sb) : h_bits2f(sb);
+            if constexpr (ONE) tot1[i] += acc[i][mt][0] * sf;
+            else tot[i][mt] += acc[i][mt] * sf;
+            if constexpr (decltype(zero)::value) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+          }
+        return;
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        float sc[4];
+#pragma unroll
+        for (int P = 0; P < 4; ++P) {
+          const int c = nib_col<SEQ>(4 * h + P);
+          const uint16_t sb = (uint16_t)(s4[c >> 1] >> (16 * (c & 1)));
+          sc[P] = SBF ? bf_bits2f(sb) : h_bits2f(sb);
+        }
+        const HalfCoef hc = half_coef<T>(sc, zwc, 4 * h);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          const int c = nib_col<SEQ>(i);
-          const uint16_t sb = (uint16_t)(s4[c >> 1] >> (16 * (c & 1)));
-          const float sf = SBF ? bf_bits2f(sb) : h_bits2f(sb);
-          if constexpr (ONE) tot1[i] += acc[i][mt][0] * sf;
-          else tot[i][mt] += acc[i][mt] * sf;
-          if constexpr (decltype(zero)::value) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+          if constexpr (ONE) {
+            float tv[4] = {tot1[4 * h], tot1[4 * h + 1], tot1[4 * h + 2], tot1[4 * h + 3]};
+            const float av[4] = {acc[4 * h][mt][0], acc[4 * h + 1][mt][0], acc[4 * h + 2][mt][0], acc[4 * h + 3][mt][0]};
+            biased_terms<T>(tv, av, ax[mt][0], hc);
+#pragma unroll
+            for (int P = 0; P < 4; ++P) tot1[4 * h + P] = tv[P];
+          } else {
+            f32x4 tv[4] = {tot[4 * h][mt], tot[4 * h + 1][mt], tot[4 * h + 2][mt], tot[4 * h + 3][mt]};
+            const f32x4 av[4] = {acc[4 * h][mt], acc[4 * h + 1][mt], acc[4 * h + 2][mt], acc[4 * h + 3][mt]};
+            biased_terms<T>(tv, av, ax[mt], hc);
+#pragma unroll
+            for (int P = 0; P < 4; ++P) tot[4 * h + P][mt] = tv[P];
+          }
         }
+      }
+      if constexpr (decltype(zero)::value) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          ax[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
     };
     auto prep = [&](int slot) {
+      if constexpr (BIASED) zwc = sz[slot].zw;
+      else
 #pragma unroll
-      for (int i = 0; i < 8; ++i) zm[i] = zero_magic(i & 1, (sz[slot].zw >> (4 * i)) & 0xF);
+        for (int i = 0; i < 8; ++i) zm[i] = zero_magic(i & 1, (sz[slot].zw >> (4 * i)) & 0xF);
       s4 = sz[slot].s4;
     };
 

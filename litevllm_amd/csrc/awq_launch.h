@@ -21,7 +21,7 @@ struct DecodePlan {
 };
 
 // Which instantiations of the decode kernel serve a call:
-//   kDecodeStream : weights in the decode stream layout (AutoAWQ nibble order, f16 act/scales)
+//   kDecodeStream : weights in the decode stream layout (AutoAWQ nibble order)
 //   kDecodeWide   : AutoAWQ [K, N/8], f16 activations and scales (every tile width)
 //   kDecodeNarrow : the other dtype / layout combinations (one word per lane)
 enum DecodeMode { kDecodeStream = 0, kDecodeWide = 1, kDecodeNarrow = 2 };
@@ -33,9 +33,11 @@ inline DecodeMode decode_mode(int layout, int act, int sdt) {
 DecodePlan plan_decode(int64_t M, int64_t N, int64_t K, int64_t G, int split_k, DecodeMode mode);
 bool launch_decode(const awq::GemmArgs& a, const DecodePlan& s, DecodeMode mode, bool seq, bool zp,
                    int act, int sdt, hipStream_t st);
-// bf16 scales or bf16 activations (sbf: scales are bf16)
+// bf16 scales or bf16 activations (sbf: scales are bf16); AUTOAWQ / KN_SEQ and stream layouts
 bool launch_decode_misc(const awq::GemmArgs& a, const DecodePlan& s, bool seq, bool zp, int act, int sbf,
                         hipStream_t st);
+bool launch_decode_misc_stream(const awq::GemmArgs& a, const DecodePlan& s, bool zp, int act, int sbf,
+                               hipStream_t st);
 
 // Decode stream layout (tile = 16 packed words = 128 columns): the (tile t, k-step s) run of
 // 2048 bytes starts at byte (t * K/32 + s) * 2048.  Lane l = 16 q + r owns word 16 t + r

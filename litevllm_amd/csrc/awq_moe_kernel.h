@@ -94,6 +94,11 @@ moe_gemm_kernel(const MoeArgs p) {
   const int word = moe_word(t, r, p.half, NW);
   const uint32_t wc = word < 0 ? 0u : (uint32_t)word;  // padding lanes: word 0's constants, zero weights
   const MagicK mk = magic_consts();
+  const BiasK bk = bias_consts<T>();
+  const u32x4 ones = {ones2<T>(), ones2<T>(), ones2<T>(), ones2<T>()};
+  // biased operands (see biased_operand) where they need fewer instructions than the exact
+  // integers q - z: several k-steps per group of one route tile, and bf16
+  constexpr bool BIASED = (SPG >= 2 && MT == 1) || (!std::is_same<T, f16>::value && !(MT == 2 && SPG == 1));
 
   for (int base = 0; base < count; ) {
     // wave groups of 16 * MT rows; the waves of a group split K
@@ -107,12 +112,15 @@ moe_gemm_kernel(const MoeArgs p) {
     const int ks0 = KS * ki / wpg, ks1 = KS * (ki + 1) / wpg;
     const int nunits = ks1 - ks0;
 
-    f32x4 acc[8][MT];  // the current group's sums, integer weights
+    f32x4 acc[8][MT];  // the current group's sums, integer (or biased) weights
+    f32x4 ax[MT];      // the current group's activation sums (biased operands)
     f32x4 tot[8][MT];  // the scaled sums of the groups done
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int mt = 0; mt < MT; ++mt) {
+      ax[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) acc[i][mt] = tot[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int i = 0; i < 8; ++i) acc[i][mt] = tot[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
 
     if (active && nunits > 0) {
       // the activation operand: route row r of each 16-route tile, 8 k per lane
@@ -127,7 +135,8 @@ moe_gemm_kernel(const MoeArgs p) {
       uint32_t raw[D][8];
       u32x4 xr[D][MT];
       WordSZ sz[D];
-      uint32_t zm[8];  // biased zeros of the current group
+      uint32_t zm[8];  // biased zeros of the current group (exact integer operands)
+      uint32_t zwc;    // zero word of the current group (biased operands)
       u32x4 s4;        // scales of the current group (the word's 8 columns, raw 16-bit values)
       // past the wave's last unit the ring's refills go through empty descriptors (zeros,
       // no memory traffic), so every ring turn is a whole one
@@ -169,31 +178,45 @@ moe_gemm_kernel(const MoeArgs p) {
         }
 #define AWQ_MOE_NIB(I)                                                                          \
         {                                                                                       \
-          const u32x4 op = int_operand<I, T>(mlo, mhi, zm[I], mk);                              \
+          const u32x4 op = BIASED ? biased_operand<I, T>(mlo, mhi, bk) : int_operand<I, T>(mlo, mhi, zm[I], mk); \
           _Pragma("unroll") for (int mt = 0; mt < MT; ++mt)                                     \
               acc[I][mt] = MfmaOp<T>::run(xr[slot][mt], op, FRESH ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[I][mt]); \
         }
         AWQ_MOE_NIB(0) AWQ_MOE_NIB(1) AWQ_MOE_NIB(2) AWQ_MOE_NIB(3)
         AWQ_MOE_NIB(4) AWQ_MOE_NIB(5) AWQ_MOE_NIB(6) AWQ_MOE_NIB(7)
 #undef AWQ_MOE_NIB
+        if constexpr (BIASED)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            ax[mt] = MfmaOp<T>::run(xr[slot][mt], ones, FRESH ? f32x4{0.f, 0.f, 0.f, 0.f} : ax[mt]);
       };
       // tot += acc * scale of the group just finished (ZERO: acc restarts from zero)
       auto flush = [&](auto zero) {
+        if constexpr (BIASED) {
+          flush_biased<T, SBF>(tot, acc, ax, s4, zwc);
+        } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int c = nib_col<false>(i);
-          const uint16_t sb = (uint16_t)(s4[c >> 1] >> (16 * (c & 1)));
-          const float sf = SBF ? bf_bits2f(sb) : h_bits2f(sb);
+          for (int i = 0; i < 8; ++i) {
+            const int c = nib_col<false>(i);
+            const uint16_t sb = (uint16_t)(s4[c >> 1] >> (16 * (c & 1)));
+            const float sf = SBF ? bf_bits2f(sb) : h_bits2f(sb);
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt) {
-            tot[i][mt] += acc[i][mt] * sf;
-            if constexpr (decltype(zero)::value) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int mt = 0; mt < MT; ++mt) tot[i][mt] += acc[i][mt] * sf;
           }
         }
+        if constexpr (decltype(zero)::value)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            ax[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+          }
       };
       auto prep = [&](int slot) {
+        if constexpr (BIASED) zwc = sz[slot].zw;
+        else
 #pragma unroll
-        for (int i = 0; i < 8; ++i) zm[i] = zero_magic(i & 1, (sz[slot].zw >> (4 * i)) & 0xF);
+          for (int i = 0; i < 8; ++i) zm[i] = zero_magic(i & 1, (sz[slot].zw >> (4 * i)) & 0xF);
         s4 = sz[slot].s4;
       };
 

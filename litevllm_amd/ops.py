@@ -213,11 +213,9 @@ DECODE_GROUPS = (32, 64, 128)
 def _use_decode_stream(M, K, group_size, a, scales, layout, decode_stream):
     if decode_stream is False or layout != "autoawq":
         return False
-    eligible = (M <= DECODE_MAX_M and int(group_size) in DECODE_GROUPS and K % 32 == 0
-                and a.dtype == torch.float16 and scales.dtype == torch.float16)
+    eligible = M <= DECODE_MAX_M and int(group_size) in DECODE_GROUPS and K % 32 == 0
     if decode_stream is True and not eligible:
-        raise ValueError("the decode stream layout needs M <= 32, group 32/64/128 and fp16 "
-                         "activations and scales")
+        raise ValueError("the decode stream layout needs M <= 32 and group 32/64/128")
     return eligible
 
 
@@ -346,8 +344,7 @@ def gate_up_act(x: torch.Tensor, gate_qweight: torch.Tensor, up_qweight: torch.T
     if kw != K:
         raise ValueError(f"K mismatch: x has {K}, weights have {kw}")
     act = GATE_UP_ACTIVATIONS.get(str(activation).lower(), L.MOE_ACT_SILU)
-    use_stream = (x.dtype == torch.float16 and gate_scales.dtype == torch.float16 and K % 32 == 0
-                  and M <= DECODE_MAX_M)
+    use_stream = K % 32 == 0 and M <= DECODE_MAX_M
     qw, sc, qz, st = GATE_UP_CACHE.get(gate_qweight, up_qweight, gate_scales, up_scales, gate_qzeros,
                                        up_qzeros, args=(int(group_size), layout, use_stream))
     lc = L.LAYOUT_DECODE_STREAM if st is not None else L.LAYOUT_AUTOAWQ

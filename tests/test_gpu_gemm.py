@@ -185,6 +185,32 @@ def test_gemm_bf16_activations(M, K, N):
     assert (np.abs(y - ye) <= ulp).all(), float((np.abs(y - ye) / ulp).max())
 
 
+@pytest.mark.parametrize("act,sdt", [(torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float16),
+                                     (torch.float16, torch.bfloat16), (torch.float16, torch.float16)])
+@pytest.mark.parametrize("M,G", [(1, 128), (1, 64), (1, 32), (4, 128), (17, 32), (32, 64)])
+@pytest.mark.parametrize("stream", [True, False])
+@pytest.mark.parametrize("zp", [True, False])
+def test_decode_dtype_combinations(act, sdt, M, G, stream, zp):
+    """Every activation / scale dtype pair through the decode kernel, stream copy or AutoAWQ
+    layout, with and without zero points: within one ulp of the output dtype (at max(|y|, 1))
+    of the exact sum over unrounded weights (q - z) * s, s taken in its own dtype."""
+    ops = _lib()
+    K, N = 2048, 1040
+    _note(f"decode dtypes act={act} scales={sdt} M={M} G={G} stream={stream} zp={zp}")
+    p = make_awq_problem(M=M, K=K, N=N, group_size=G, seed=M * 31 + G)
+    sc = torch.from_numpy(p["scales"]).to(sdt)
+    xa = torch.from_numpy(p["x"]).to(act)
+    qz = torch.from_numpy(p["qzeros"]).to(DEV) if zp else None
+    y = ops.gemm(xa.to(DEV), torch.from_numpy(p["qweight"]).to(DEV), sc.to(DEV), qz, G, layout="autoawq",
+                 decode_stream=stream).float().cpu().numpy()
+    w = O.dequant_awq(p["qweight"], sc.float().numpy(), p["qzeros"] if zp else None, G, out_dtype="float32",
+                      zero_point=zp)
+    ye = xa.double().numpy() @ w.astype(np.float64)
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(ye), 1.0))) - (10 if act == torch.float16 else 7))
+    err = np.abs(y - ye) / ulp
+    assert err.max() <= 1.0, float(err.max())
+
+
 @pytest.mark.parametrize("M,K,N,G", [(1, 1024, 512, 32), (4, 512, 256, 128), (64, 512, 512, 64),
                                      (48, 1056, 256, 32)])
 def test_gemm_symmetric(M, K, N, G):
