@@ -282,7 +282,7 @@ def main():
             for c in range(copies):
                 qw, qz, sc = W[(m, n)][c]
                 ops.gemm(X[m], qw, sc, qz, G, layout="autoawq", out=Y[(m, n)])
-        ms, g = _time_graph(torch, one, 5)
+        ms, g = _time_graph(torch, one, 20)
         del g
         us = ms * 1e3 / copies
         b = alg_bytes(m, K_DEC, n)

@@ -55,11 +55,17 @@ extern "C" {
  *                      that the decode kernel reads it as contiguous 2 KiB runs; qzeros and
  *                      scales stay in the AUTOAWQ layout.  Accepted by awq_w4a16_gemm for
  *                      M <= 32 and group sizes 32/64/128.
+ * AWQ_LAYOUT_DECODE_NARROW : an AUTOAWQ qweight re-ordered by awq_w4a16_pack_decode_narrow
+ *                      into 16-column tiles (one 32-bit word per column and 8 rows), read by
+ *                      the narrow decode kernel: one block per 16 columns over the whole K,
+ *                      no split-K.  For decode shapes whose N is small against the chip
+ *                      (N <= 16 x 2 x CUs); same conditions as DECODE_STREAM.
  */
 #define AWQ_LAYOUT_AUTOAWQ 0
 #define AWQ_LAYOUT_KN_SEQ 1
 #define AWQ_LAYOUT_NK_SEQ 2
 #define AWQ_LAYOUT_DECODE_STREAM 3
+#define AWQ_LAYOUT_DECODE_NARROW 4
 
 /* ---- element types ---- */
 #define AWQ_DTYPE_NONE 0 /* e.g. no bias */
@@ -109,7 +115,8 @@ size_t awq_w4a16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t g
  * awq_fused_gemm.py:1966-1971.  Otherwise (the prefill kernel): W rounded once to act_dtype,
  * as awq_w4a16_dequant computes it (the reference's tl.dot branch, 1973-1976).
  *   a: [M, K] act_dtype (F16 or BF16), row stride lda (elements).
- *   layout: AUTOAWQ or KN_SEQ (qweight [K, N/8]), or DECODE_STREAM (M <= 32).  An NK_SEQ
+ *   layout: AUTOAWQ or KN_SEQ (qweight [K, N/8]), or DECODE_STREAM / DECODE_NARROW
+ *           (M <= 32).  An NK_SEQ
  *           weight is converted once with awq_w4a16_repack_nk_to_autoawq; passing NK_SEQ
  *           here returns AWQ_ERR_UNSUPPORTED.
  *   qzeros == NULL: symmetric z = 8.  scales: scale_dtype (F16 or BF16).
@@ -119,7 +126,8 @@ size_t awq_w4a16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t g
  *            are added in a fixed order (0 = choose automatically; the prefill kernel does
  *            not split K).  For a given (M, N, K, split_k) the result is bitwise
  *            reproducible.  Partition s covers rows [64 s I, min(64 (s+1) I, K)) with
- *            I = ceil(ceil(K / 64) / split_k), as in awq_fused_gemm.py:1798-1800.
+ *            I = ceil(ceil(K / 64) / split_k), as in awq_fused_gemm.py:1798-1800.  The
+ *            DECODE_NARROW layout never splits K (split_k is ignored there).
  *   Requirements: N % 8 == 0, group_size % 32 == 0, K % group_size == 0.
  */
 int awq_w4a16_gemm(const void* a, int64_t lda, const int32_t* qweight, const void* scales,
@@ -145,6 +153,15 @@ int64_t awq_w4a16_decode_stream_bytes(int64_t K, int64_t N);
  * objects (vllm/model_executor/layers/quantization/tensor.py:1251-1256), built once per
  * weight so that decode-shaped calls stream the weight contiguously.  K % 32 == 0. */
 int awq_w4a16_pack_decode_stream(const int32_t* qweight_kn, int32_t* out, int64_t K, int64_t N,
+                                 void* stream);
+
+/* Bytes of the narrow decode copy of a [K, N/8] qweight (N rounded up to 16 columns). */
+int64_t awq_w4a16_decode_narrow_bytes(int64_t K, int64_t N);
+
+/* Lossless re-ordering of an AUTOAWQ qweight [K, N/8] into the narrow decode layout (out holds
+ * awq_w4a16_decode_narrow_bytes(K, N) bytes).  No counterpart in the reference: a derived pack
+ * like awq_w4a16_pack_decode_stream (tensor.py:1251-1256).  K % 32 == 0. */
+int awq_w4a16_pack_decode_narrow(const int32_t* qweight_kn, int32_t* out, int64_t K, int64_t N,
                                  void* stream);
 
 /* ---- mixture of experts ------------------------------------------------------------

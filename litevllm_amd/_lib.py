@@ -17,6 +17,7 @@ LAYOUT_AUTOAWQ = 0
 LAYOUT_KN_SEQ = 1
 LAYOUT_NK_SEQ = 2
 LAYOUT_DECODE_STREAM = 3
+LAYOUT_DECODE_NARROW = 4
 
 DTYPE_NONE = 0
 DTYPE_F16 = 1
@@ -45,6 +46,8 @@ SIGNATURES = {
     "awq_w4a16_repack_nk_to_autoawq": (ctypes.c_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64,
                                                       _c_i64, _c_i32, _c_p]),
     "awq_w4a16_decode_stream_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "awq_w4a16_decode_narrow_bytes": (_c_i64, [_c_i64, _c_i64]),
+    "awq_w4a16_pack_decode_narrow": (ctypes.c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_p]),
     "awq_w4a16_pack_decode_stream": (ctypes.c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_p]),
     "awq_w4a16_moe_stream_bytes": (_c_i64, [_c_i64, _c_i64, _c_i64, _c_i32]),
     "awq_w4a16_moe_pack_stream": (ctypes.c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p]),
@@ -95,6 +98,21 @@ def load(path: str | None = None) -> ctypes.CDLL:
         if path is None:
             _lib = lib
         return lib
+
+
+_num_cus = None
+
+
+def num_cus() -> int:
+    """Compute units of the current device (256 on MI355X; 256 when no GPU is visible)."""
+    global _num_cus
+    if _num_cus is None:
+        try:
+            import torch
+            _num_cus = int(torch.cuda.get_device_properties(torch.cuda.current_device()).multi_processor_count)
+        except Exception:
+            _num_cus = 256
+    return _num_cus
 
 
 def strerror(code: int) -> str:

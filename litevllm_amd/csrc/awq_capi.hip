@@ -68,6 +68,7 @@ size_t awq_w4a16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t g
                                       int32_t split_k, int32_t layout) {
   if (M <= 0 || N <= 0 || K <= 0 || (N % 8) != 0 || split_k < 0) return 0;
   if (group_size <= 0 || (K % group_size) != 0 || !decode_covers(M, group_size)) return 0;
+  if (layout == AWQ_LAYOUT_DECODE_NARROW) return 0;  // the narrow kernel does not split K
   // the plan also depends on the dtype path: size for the largest
   size_t ws = 0;
   for (DecodeMode m : {kDecodeStream, kDecodeWide, kDecodeNarrow}) {
@@ -97,10 +98,11 @@ int awq_w4a16_gemm(const void* a, int64_t lda, const int32_t* qweight, const voi
   if ((((uintptr_t)a) & 15) || (((uintptr_t)c) & 15) || (((uintptr_t)scales) & 15) ||
       (((uintptr_t)qweight) & 15))
     return AWQ_ERR_STRIDE;
-  if (layout != AWQ_LAYOUT_AUTOAWQ && layout != AWQ_LAYOUT_KN_SEQ && layout != AWQ_LAYOUT_DECODE_STREAM)
+  if (layout != AWQ_LAYOUT_AUTOAWQ && layout != AWQ_LAYOUT_KN_SEQ && layout != AWQ_LAYOUT_DECODE_STREAM &&
+      layout != AWQ_LAYOUT_DECODE_NARROW)
     return AWQ_ERR_UNSUPPORTED;
-  const bool stream_layout = layout == AWQ_LAYOUT_DECODE_STREAM;
-  if (stream_layout && !decode_covers(M, group_size)) return AWQ_ERR_UNSUPPORTED;
+  const bool stream_layout = layout == AWQ_LAYOUT_DECODE_STREAM || layout == AWQ_LAYOUT_DECODE_NARROW;
+  if (stream_layout && (!decode_covers(M, group_size) || (K % 32) != 0)) return AWQ_ERR_UNSUPPORTED;
   // 32-bit buffer offsets: weights, activations and the output must stay below 2 GiB
   if (decode_stream_bytes(K, N) > 0x7FFFFFFFLL || M * lda * 2 > 0x7FFFFFFFLL) return AWQ_ERR_UNSUPPORTED;
   hipStream_t st = (hipStream_t)stream;
@@ -122,6 +124,10 @@ int awq_w4a16_gemm(const void* a, int64_t lda, const int32_t* qweight, const voi
   const bool seq = layout == AWQ_LAYOUT_KN_SEQ;
   const bool zp = qzeros != nullptr;
 
+  if (layout == AWQ_LAYOUT_DECODE_NARROW) {  // whole K per block: no workspace
+    if (!launch_decode_narrow(ga, zp, act_dtype, scale_dtype, st)) return AWQ_ERR_UNSUPPORTED;
+    return launch_status();
+  }
   if (decode_covers(M, group_size)) {
     const DecodeMode mode = decode_mode(layout, act_dtype, scale_dtype);
     const DecodePlan sp = plan_decode(M, N, K, group_size, split_k, mode);
@@ -146,6 +152,18 @@ int awq_w4a16_repack_nk_to_autoawq(const int32_t* qweight_nk, const int32_t* qze
                                    void* stream) {
   return launch_repack_nk_to_autoawq(qweight_nk, qzeros_nk, scales_nk, qweight_kn, qzeros_kn,
                                      scales_kn, N, K, group_size, (hipStream_t)stream);
+}
+
+int64_t awq_w4a16_decode_narrow_bytes(int64_t K, int64_t N) {
+  if (K <= 0 || N <= 0 || (N % 8) != 0 || (K % 32) != 0) return 0;
+  return decode_narrow_bytes(K, N);
+}
+
+int awq_w4a16_pack_decode_narrow(const int32_t* qweight_kn, int32_t* out, int64_t K, int64_t N, void* stream) {
+  if (!qweight_kn || !out) return AWQ_ERR_NULL;
+  if (K <= 0 || N <= 0 || (N % 8) != 0 || (K % 32) != 0) return AWQ_ERR_SHAPE;
+  if (decode_narrow_bytes(K, N) > 0x7FFFFFFFLL) return AWQ_ERR_UNSUPPORTED;
+  return launch_pack_decode_narrow(qweight_kn, out, K, N, (hipStream_t)stream);
 }
 
 int64_t awq_w4a16_decode_stream_bytes(int64_t K, int64_t N) {

@@ -389,6 +389,41 @@ __device__ __forceinline__ void flush_biased(f32x4 (&tot)[8][MT], const f32x4 (&
   }
 }
 
+// waits until no vector-memory operation of this wave is outstanding (gfx9 s_waitcnt
+// encoding, expcnt and lgkmcnt unconstrained); as an intrinsic the compiler's own wait
+// bookkeeping sees it
+#define AWQ_WAIT_VMCNT0() __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8))
+// the same, leaving at most N (< 64) vector-memory operations of this wave outstanding
+#define AWQ_WAIT_VMCNT(N) \
+  __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8) | ((N) & 0xF) | ((((N) >> 4) & 0x3) << 14))
+
+// Raw, range-checked buffer descriptor as four SGPR words (for the LDS DMA below).
+__device__ __forceinline__ u32x4 rsrc_words(const void* base, uint32_t nbytes) {
+  const uint64_t b = (uint64_t)(uintptr_t)base;
+  return u32x4{(uint32_t)b, (uint32_t)(b >> 32) & 0xFFFFu, nbytes, 0x00020000u};
+}
+
+// Buffer loads straight into LDS: lane l's 16 (lds_dma16) or 4 (lds_dma4) bytes land at
+// lds + 16 l (+ 4 l).  Written as assembly so the compiler does not pair them with unrelated
+// LDS reads (it cannot tell LDS buffers apart and would wait for every load in flight before
+// each of them); a kernel waits for these loads itself before its barrier.  M0 carries the
+// LDS address and nothing else in these kernels uses M0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16(const u32x4& rsrc, uint32_t lds, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma4(const u32x4& rsrc, uint32_t lds, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+               :
+               : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
 // Buffer resource over a whole tensor (raw addressing, bounds = nbytes).  Range checks
 // cover the VGPR offset only (the SGPR offset is excluded), so anything that must read as
 // zero past the end has to carry its position in the VGPR offset.

@@ -41,11 +41,15 @@ namespace awq {
 // MT: 16-token MFMA tiles (M <= 16 MT).  ONE: M == 1, so only element 0 of lane q = 0's
 // accumulators holds a real token and only that element is scaled and reduced.
 // SBF: scales are bf16 (fp16 otherwise).  STREAM: weights in the decode stream layout.
+// XL (ONE, stream layout): the block's slice of the activation row is staged in LDS once by
+// DMA and every lane reads its k-slice from there (the MFMA's other 15 rows repeat row 0 and
+// are never read back), instead of a 16-byte load per lane and k-step.
 template <int MT, int NWV, int D, int SPG, bool SEQ, bool ZP, typename T, bool SBF, bool STREAM, bool ONE,
-          int OCC>
+          int OCC, bool XL>
 __global__ void __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
 decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
   static_assert((SPG & (SPG - 1)) == 0, "");
+  static_assert(!XL || (ONE && STREAM), "");
   static_assert(NWV >= 2 && (NWV & (NWV - 1)) == 0, "power-of-two waves per block");
   static_assert(!ONE || MT == 1, "");
   // Biased operands (one AND-OR or permute per pair of rows, the zero taken off per group) pay
@@ -56,6 +60,7 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
   constexpr int MROWS = ONE ? 1 : 16 * MT;  // token rows a wave can hold
   __shared__ float red[NWV * MROWS * 128];  // every wave's sums: [wave][token][tile column]
   __shared__ int s_last;
+  extern __shared__ __align__(16) unsigned char xsm[];  // XL: activations k0 * 32 .. k1 * 32 of row 0
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform by construction
@@ -85,6 +90,17 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
 
   const int ngroups = p.K / p.G;
   const uint32_t row_bytes = (uint32_t)NW * 4u;
+  if constexpr (XL) {
+    // 16-byte pieces i of the block's activation slice; wave w issues DMA instructions
+    // w, w + NWV, ... of 64 pieces
+    const u32x4 xrs4 = rsrc_words(p.a, (uint32_t)((uint64_t)p.lda * 2u));
+    const uint32_t xsm_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)xsm;
+    const int npieces = len * 4;
+    for (int j = wave; j * 64 < npieces; j += NWV) {
+      const int i = j * 64 + lane;
+      lds_dma16(xrs4, xsm_base + (uint32_t)j * 1024u, i < npieces ? (uint32_t)(k0 * 64 + i * 16) : 0x80000000u, 0u);
+    }
+  }
   if (nunits > 0) {
     const uint32_t w_bytes = STREAM ? (uint32_t)wk.tiles * (uint32_t)KS * 2048u : (uint32_t)p.K * row_bytes;
     const uint32_t x_bytes = (uint32_t)((uint64_t)p.M * (uint64_t)p.lda * 2u);
@@ -112,8 +128,10 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
     // Issue cursor over the wave's units, advanced one unit per issue.  Past the last unit the
     // ring's refills go through empty buffer descriptors (zeros, no memory traffic), so every
     // ring turn is a whole one; all per-unit index math is 32-bit scalar arithmetic.
+    // A unit's scales and zeros are loaded only where a group starts (or in the first turn,
+    // which includes the wave's first unit): prep reads no other slot's.
     int iks = w0, ileft = nunits;
-    auto issue = [&](int slot) {
+    auto issue = [&](int slot, bool first_turn) {
       const int ks = iks;  // wave-uniform
       const bool past = ileft <= 0;
       ++iks;
@@ -139,14 +157,24 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
         for (int j = 0; j < 8; ++j)
           raw[slot][j] = __builtin_amdgcn_raw_buffer_load_b32(wrs, (int)w_lane_off, (int)(kbase + (uint32_t)j * row_bytes), 0);
       }
+      if constexpr (!XL)
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-        xr[slot][mt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)x_lane_off[mt], ks * 64, 0));
-      const int g = ks / SPG;
-      sz[slot].s4 = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(srs, (int)(16u * wc), (int)((uint32_t)g * (uint32_t)p.N * 2u), 0));
-      sz[slot].zw = ZP ? __builtin_amdgcn_raw_buffer_load_b32(zrs, (int)(4u * wc), (int)((uint32_t)g * (uint32_t)NW * 4u), 0)
-                       : 0x88888888u;
+        for (int mt = 0; mt < MT; ++mt)
+          xr[slot][mt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)x_lane_off[mt], ks * 64, 0));
+      // (the 16-wave M == 1 kernel without LDS activations keeps the per-unit loads: holding
+      // a slot's constants across turns would not fit its 128 registers)
+      if (first_turn || (ks & (SPG - 1)) == 0 || (ONE && !XL)) {  // wave-uniform
+        const int g = ks / SPG;
+        sz[slot].s4 = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(srs, (int)(16u * wc), (int)((uint32_t)g * (uint32_t)p.N * 2u), 0));
+        sz[slot].zw = ZP ? __builtin_amdgcn_raw_buffer_load_b32(zrs, (int)(4u * wc), (int)((uint32_t)g * (uint32_t)NW * 4u), 0)
+                         : 0x88888888u;
+      }
+    };
+    int cks_x = w0;  // the next unit to compute (XL reads its activations from LDS)
+    auto xop = [&](int slot, int mt) -> u32x4 {
+      if constexpr (XL) return *(const u32x4*)(xsm + ((cks_x - k0) * 32 + 8 * q) * 2);
+      else return xr[slot][mt];
     };
     // FRESH: the group's first unit (its MFMAs start from zero)
     auto compute = [&](int slot, auto fresh) {
@@ -162,11 +190,15 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
           mhi[v] = pair_hi(raw[slot][2 * v], raw[slot][2 * v + 1]);
         }
       }
+      u32x4 xv[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) xv[mt] = xop(slot, mt);
+      ++cks_x;
 #define AWQ_DECODE_NIB(I)                                                                      \
       {                                                                                        \
         const u32x4 op = BIASED ? biased_operand<I, T>(mlo, mhi, bk) : int_operand<I, T>(mlo, mhi, zm[I], mk); \
         _Pragma("unroll") for (int mt = 0; mt < MT; ++mt)                                      \
-            acc[I][mt] = MfmaOp<T>::run(xr[slot][mt], op, FRESH ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[I][mt]); \
+            acc[I][mt] = MfmaOp<T>::run(xv[mt], op, FRESH ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[I][mt]); \
       }
       AWQ_DECODE_NIB(0) AWQ_DECODE_NIB(1) AWQ_DECODE_NIB(2) AWQ_DECODE_NIB(3)
       AWQ_DECODE_NIB(4) AWQ_DECODE_NIB(5) AWQ_DECODE_NIB(6) AWQ_DECODE_NIB(7)
@@ -174,7 +206,7 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
       if constexpr (BIASED)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
-          ax[mt] = MfmaOp<T>::run(xr[slot][mt], ones, FRESH ? f32x4{0.f, 0.f, 0.f, 0.f} : ax[mt]);
+          ax[mt] = MfmaOp<T>::run(xv[mt], ones, FRESH ? f32x4{0.f, 0.f, 0.f, 0.f} : ax[mt]);
     };
     // tot += the scaled sums s * sum x (q - z) of the group just finished, from the biased
     // sums and the activation sums (ZERO: the sums restart from zero)
@@ -238,8 +270,15 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
     };
 
 #pragma unroll
-    for (int u = 0; u < D; ++u) issue(u);
+    for (int u = 0; u < D; ++u) issue(u, true);
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (XL) {
+      // this wave's DMA (issued before the ring) has landed once no more than the ring's loads
+      // (two weight pieces, the scales and the zeros per unit) are in flight; the barrier then
+      // covers every wave's
+      AWQ_WAIT_VMCNT(D * (ZP ? 4 : 3));
+      __syncthreads();
+    }
     static_assert(D == 2 && (SPG == 1 || SPG % D == 0), "");
     constexpr bool kGroupLoop = SPG > 1;
     if (kGroupLoop && (w0 % SPG) == 0 && (nunits % SPG) == 0) {
@@ -252,7 +291,7 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
           if (u == 0) compute(0, std::true_type{});
           else compute(u % D, std::false_type{});
           __builtin_amdgcn_sched_barrier(0);
-          issue(u % D);
+          issue(u % D, false);
           __builtin_amdgcn_sched_barrier(0);
         }
         flush(std::false_type{});
@@ -281,12 +320,15 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
             }
           }
           __builtin_amdgcn_sched_barrier(0);
-          issue(u);
+          issue(u, false);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
       if (SPG > 1 && g_cur >= 0) flush(std::false_type{});  // the last group
     }
+  } else if constexpr (XL) {
+    AWQ_WAIT_VMCNT0();  // no ring: wait for this wave's DMA alone
+    __syncthreads();
   }
 
   const int M = p.M;
@@ -418,18 +460,33 @@ using namespace awq;
 // M == 1 needs few enough registers to run blocks of 16 waves at four per SIMD, which hides
 // more of the memory latency; more tokens run 8 waves at two per SIMD, whose registers leave
 // room for the whole-group loop (measured faster than 16 waves without it).
-template <int MT, bool SEQ, bool ZP, typename T, bool SBF, bool STREAM, bool ONE>
-inline void launch_t(const GemmArgs& a, const DecodePlan& s, hipStream_t st) {
+// Activation slices up to this many bytes per block are staged in LDS (M == 1, stream layout).
+constexpr uint32_t kDecodeXlMax = 49152;
+
+template <int MT, bool SEQ, bool ZP, typename T, bool SBF, bool STREAM, bool ONE, bool XL>
+inline void launch_x(const GemmArgs& a, const DecodePlan& s, uint32_t shmem, hipStream_t st) {
   const DecodeWork wk{s.tiles, s.ksteps, s.splits, s.per};
   constexpr int NWV = ONE ? 16 : 8, OCC = ONE ? 4 : 2;
   const dim3 grid((unsigned)s.blocks), block(NWV * 64);
   const int spg = a.G / 32;
   if (spg == 4)
-    hipLaunchKernelGGL((decode_kn_kernel<MT, NWV, 2, 4, SEQ, ZP, T, SBF, STREAM, ONE, OCC>), grid, block, 0, st, a, wk);
+    hipLaunchKernelGGL((decode_kn_kernel<MT, NWV, 2, 4, SEQ, ZP, T, SBF, STREAM, ONE, OCC, XL>), grid, block, shmem, st, a, wk);
   else if (spg == 2)
-    hipLaunchKernelGGL((decode_kn_kernel<MT, NWV, 2, 2, SEQ, ZP, T, SBF, STREAM, ONE, OCC>), grid, block, 0, st, a, wk);
+    hipLaunchKernelGGL((decode_kn_kernel<MT, NWV, 2, 2, SEQ, ZP, T, SBF, STREAM, ONE, OCC, XL>), grid, block, shmem, st, a, wk);
   else
-    hipLaunchKernelGGL((decode_kn_kernel<MT, NWV, 2, 1, SEQ, ZP, T, SBF, STREAM, ONE, OCC>), grid, block, 0, st, a, wk);
+    hipLaunchKernelGGL((decode_kn_kernel<MT, NWV, 2, 1, SEQ, ZP, T, SBF, STREAM, ONE, OCC, XL>), grid, block, shmem, st, a, wk);
+}
+
+template <int MT, bool SEQ, bool ZP, typename T, bool SBF, bool STREAM, bool ONE>
+inline void launch_t(const GemmArgs& a, const DecodePlan& s, hipStream_t st) {
+  if constexpr (ONE && STREAM) {
+    const uint32_t xbytes = (uint32_t)((s.per + 15) / 16) * 1024u;  // whole DMA instructions
+    if (xbytes <= kDecodeXlMax) {
+      launch_x<MT, SEQ, ZP, T, SBF, STREAM, ONE, true>(a, s, xbytes, st);
+      return;
+    }
+  }
+  launch_x<MT, SEQ, ZP, T, SBF, STREAM, ONE, false>(a, s, 0, st);
 }
 
 // ONE selects the M == 1 instantiation (the f16 paths only; the others use the general one)

@@ -1,0 +1,309 @@
+// Narrow decode kernel (M <= 32, N small against the chip): one block per 16 output columns
+// over the whole K, so no split-K hand-off -- the role of the reference's decode kernels at
+// BLOCK_M = 1 .. 32 (vllm/kernels/triton/awq_fused_gemm.py:1883-1990) for shapes whose 128-
+// column tiles are too few to fill 256 CUs.
+//
+//  * Narrow stream layout (awq_w4a16_pack_decode_narrow): tile t = columns 16 t .. 16 t + 15;
+//    the (tile t, k-step s) run of 256 bytes starts at byte (t * K/32 + s) * 256 and lane
+//    l = 16 q + r owns its u32 at byte 4 l: the eight nibbles of column 16 t + r at rows
+//    32 s + 8 q + j, rows 2u and 2u + 1 at nibble u of the low and the high 16-bit half.  One
+//    u32 is then the lane's whole MFMA operand: pair u (rows 2u, 2u + 1) is magic_bits<u>.
+//  * Lane (q, r) multiplies the activations (16 tokens x 32 k) by column 16 t + r's 32 rows
+//    with one v_mfma_f32_16x16x32 per k-step; the operand holds the exact integers q - z
+//    (magic-exponent unpack, one packed subtraction per pair of rows), each group's sum is
+//    scaled once by the column's fp32 scale -- unrounded weights, as in the wide decode
+//    kernel and the reference's M = 1 formulation (awq_fused_gemm.py:1966-1971).
+//  * The block's waves take contiguous shares of K with an 8-deep register ring (one u32 of
+//    weights per k-step and lane), meet in LDS, and sum in wave order (bitwise reproducible).
+#include "awq_decode_kernel.h"
+
+namespace awq {
+
+// LDS of one block (bytes): the waves' sums [NWV][MROWS][16] fp32, then the tile's scales
+// [groups][16] (2 B each), zero words [groups][2], and with XL the activation row [K] (2 B).
+// Each region spans whole DMA instructions (a 64-lane DMA writes all 64 lanes' slots, those
+// past the data as zeros), so no instruction reaches into the next region.
+struct NarrowLds {
+  uint32_t sc, zw, x, total;
+};
+__host__ __device__ inline NarrowLds narrow_lds(int nwv, int mrows, int ngroups, int K, bool zp, bool xl) {
+  const uint32_t n_pieces = ((uint32_t)ngroups * 2u + 63u) / 64u;  // instructions for scales, and for zeros
+  NarrowLds l;
+  l.sc = (uint32_t)(nwv * mrows * 16 * 4);
+  l.zw = l.sc + n_pieces * 1024u;
+  l.x = l.zw + (zp ? n_pieces * 256u : 0u);
+  l.total = l.x + (xl ? ((uint32_t)K / 8u + 63u) / 64u * 1024u : 0u);
+  return l;
+}
+
+// XL (M == 1): the activation row is staged in LDS once and every lane reads its k-slice from
+// there (the MFMA's other 15 rows repeat row 0 and are never read back); otherwise each
+// k-step loads the token rows per lane.
+template <int MT, int NWV, int SPG, bool ZP, typename T, bool SBF, bool ONE, bool XL>
+__global__ void __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(4, 4)))
+decode_narrow_kernel(const GemmArgs p, int tiles) {
+  static_assert(!ONE || MT == 1, "");
+  static_assert(!XL || ONE, "");
+  constexpr int D = 8;
+  constexpr int MROWS = ONE ? 1 : 16 * MT;
+  extern __shared__ __align__(16) unsigned char smem[];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q = lane >> 4, r = lane & 15;
+  const int t = blockIdx.x;
+  const int KS = p.K >> 5;
+  const int ks0 = KS * wave / NWV, nunits = KS * (wave + 1) / NWV - ks0;
+  const int col = t * 16 + r;
+  const int NW = p.N >> 3;
+  const int ngroups = p.K / p.G;
+  const NarrowLds L = narrow_lds(NWV, MROWS, ngroups, p.K, ZP, XL);
+  float* red = (float*)smem;
+  const uint16_t* s_lds = (const uint16_t*)(smem + L.sc);
+  const uint32_t* z_lds = (const uint32_t*)(smem + L.zw);
+  const uint16_t* x_lds = (const uint16_t*)(smem + L.x);
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)smem;
+
+  // ---- the tile's scales and zero words (and with XL the activation row) go to LDS by DMA;
+  // wave w issues instructions w, w + NWV, ... of 64 lanes each ----
+  {
+    const u32x4 srs = rsrc_words(p.sc, (uint32_t)((uint64_t)ngroups * p.N * 2u));
+    const u32x4 zrs = rsrc_words(p.qz, ZP ? (uint32_t)((uint64_t)ngroups * NW * 4u) : 0u);
+    const u32x4 xrs = rsrc_words(p.a, (uint32_t)((uint64_t)p.lda * 2u));
+    const int n_s = (ngroups * 2 + 63) / 64;      // 16-byte pieces: group i / 2, half i % 2
+    const int n_z = ZP ? (ngroups * 2 + 63) / 64 : 0;  // words: group i / 2, word 2t + i % 2
+    const int n_x = XL ? (p.K / 8 + 63) / 64 : 0;     // 16-byte pieces of the row
+    for (int j = wave; j < n_s + n_z + n_x; j += NWV) {
+      if (j < n_s) {
+        const int i = j * 64 + lane;
+        const uint32_t voff = i < ngroups * 2 ? (((uint32_t)(i >> 1) * (uint32_t)p.N + 16u * (uint32_t)t + 8u * (uint32_t)(i & 1)) * 2u)
+                                              : 0x80000000u;
+        lds_dma16(srs, lds_base + L.sc + (uint32_t)j * 1024u, voff, 0u);
+      } else if (j < n_s + n_z) {
+        const int i = (j - n_s) * 64 + lane;
+        const uint32_t voff = i < ngroups * 2 ? (((uint32_t)(i >> 1) * (uint32_t)NW + 2u * (uint32_t)t + (uint32_t)(i & 1)) * 4u)
+                                              : 0x80000000u;
+        lds_dma4(zrs, lds_base + L.zw + (uint32_t)(j - n_s) * 256u, voff, 0u);
+      } else {
+        const int i = (j - n_s - n_z) * 64 + lane;
+        lds_dma16(xrs, lds_base + L.x + (uint32_t)(j - n_s - n_z) * 1024u, i < p.K / 8 ? (uint32_t)i * 16u : 0x80000000u,
+                  0u);
+      }
+    }
+  }
+
+  f32x4 acc[MT], tot[MT];
+  float tot1 = 0.f;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = tot[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const uint32_t w_bytes = (uint32_t)tiles * (uint32_t)KS * 256u;
+  const uint32_t x_bytes = (uint32_t)((uint64_t)p.M * (uint64_t)p.lda * 2u);
+  uint32_t x_lane_off[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) x_lane_off[mt] = ((uint32_t)(mt * 16 + r) * (uint32_t)p.lda + 8u * (uint32_t)q) * 2u;
+  const uint32_t w_lane_off = (uint32_t)lane * 4u;
+  const int zsh = 4 * col_nib<false>(r & 7);
+  const MagicK mk = magic_consts();
+
+  uint32_t wr[D];
+  u32x4 xr[XL ? 1 : D][MT];
+  int iks = ks0, ileft = nunits;
+  auto issue = [&](int slot) {
+    const int ks = iks;  // wave-uniform
+    const bool past = ileft <= 0;
+    ++iks;
+    --ileft;
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(p.qw, past ? 0u : w_bytes);
+    wr[slot] = __builtin_amdgcn_raw_buffer_load_b32(wrs, (int)w_lane_off,
+                                                    (int)(((uint32_t)t * (uint32_t)KS + (uint32_t)ks) * 256u), 0);
+    if constexpr (!XL) {
+      const __amdgpu_buffer_rsrc_t xrs = make_rsrc(p.a, past ? 0u : x_bytes);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        xr[slot][mt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)x_lane_off[mt], ks * 64, 0));
+    }
+  };
+#pragma unroll
+  for (int u = 0; u < D; ++u) issue(u);
+  // this wave's DMA (issued before the ring) has landed once at most the ring is in flight;
+  // the barrier then covers every wave's
+  AWQ_WAIT_VMCNT(XL ? D : D * (1 + MT));
+  __syncthreads();
+
+  uint32_t zm0 = 0, zm1 = 0;  // biased zero of the current group (even / odd nibble forms)
+  float sf = 0.f;             // scale of the current group
+  auto flush = [&]() {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      if constexpr (ONE) tot1 += acc[mt][0] * sf;
+      else tot[mt] += acc[mt] * sf;
+      acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  auto prep = [&](int g) {
+    const uint32_t z = ZP ? (z_lds[2 * g + (r >> 3)] >> zsh) & 0xFu : 8u;
+    zm0 = zero_magic(0, z);
+    zm1 = zero_magic(1, z);
+    const uint16_t sb = s_lds[16 * g + r];
+    sf = SBF ? bf_bits2f(sb) : h_bits2f(sb);
+  };
+  auto compute = [&](int slot, int ks) {
+    const uint32_t w = wr[slot];
+    u32x4 op;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      uint32_t mb;
+      switch (u) {
+        case 0: mb = magic_bits<0>(w, mk); break;
+        case 1: mb = magic_bits<1>(w, mk); break;
+        case 2: mb = magic_bits<2>(w, mk); break;
+        default: mb = magic_bits<3>(w, mk); break;
+      }
+      const f16x2 d = as_h2(mb) - as_h2((u & 1) ? zm1 : zm0);
+      if constexpr (std::is_same<T, f16>::value) op[u] = as_u(d);
+      else op[u] = pack2<bf16>((float)d.x, (float)d.y);
+    }
+    if constexpr (XL) {
+      const u32x4 xv = *(const u32x4*)(x_lds + ks * 32 + 8 * q);
+      acc[0] = MfmaOp<T>::run(xv, op, acc[0]);
+    } else {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[mt] = MfmaOp<T>::run(xr[slot][mt], op, acc[mt]);
+    }
+  };
+
+  if (nunits > 0) {
+    int g_cur = -1, cks = ks0;
+    for (int done = 0; done < nunits; done += D) {
+#pragma unroll
+      for (int u = 0; u < D; ++u) {
+        if (done + u < nunits) {  // wave-uniform
+          const int ks = cks++;
+          const int g = ks / SPG;
+          if (g != g_cur) {
+            if (g_cur >= 0) flush();
+            g_cur = g;
+            prep(g);
+          }
+          compute(u, ks);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        issue(u);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    flush();
+  }
+
+  // ---- the waves' sums meet in LDS: lane (q, r), element v = token mt*16 + 4q + v, column r
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int v = 0; v < (ONE ? 1 : 4); ++v) {
+      const int m = mt * 16 + 4 * q + v;
+      if (m < p.M) red[(wave * MROWS + m) * 16 + r] = ONE ? tot1 : tot[mt][v];
+    }
+  __syncthreads();
+  for (int o = tid; o < p.M * 16; o += NWV * 64) {
+    const int m = o >> 4, c = o & 15;
+    float sum = red[m * 16 + c];
+#pragma unroll
+    for (int w = 1; w < NWV; ++w) sum += red[(w * MROWS + m) * 16 + c];
+    const int oc = t * 16 + c;
+    if (oc < p.N) {
+      if (p.bias) sum += load_bias(p.bias, p.bias_dtype, oc);
+      p.c[(int64_t)m * p.ldc + oc] = to_bits<T>(sum);
+    }
+  }
+}
+
+// Narrow stream pack: thread = one lane's u32 of one (tile, k-step) run.
+__global__ void __launch_bounds__(256) pack_narrow_kernel(const uint32_t* __restrict__ in, uint32_t* __restrict__ out,
+                                                          int64_t K, int64_t N, int64_t tiles) {
+  const int64_t KS = K / 32;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= tiles * KS * 64) return;
+  const int l = (int)(idx & 63);
+  const int64_t ts = idx >> 6;
+  const int64_t t = ts / KS, s = ts - t * KS;
+  const int q = l >> 4, r = l & 15;
+  const int64_t col = t * 16 + r;
+  uint32_t v = 0;
+  if (col < N) {
+    const int64_t NW = N / 8;
+    const int sh = 4 * col_nib<false>((int)(col & 7));
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t nib = (in[(s * 32 + 8 * q + j) * NW + (col >> 3)] >> sh) & 0xFu;
+      v |= nib << ((j & 1) * 16 + (j >> 1) * 4);
+    }
+  }
+  out[idx] = v;
+}
+
+}  // namespace awq
+
+namespace awq_host {
+using namespace awq;
+
+static int narrow_status() {
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? AWQ_OK : AWQ_ERR_LAUNCH;
+}
+
+int64_t decode_narrow_bytes(int64_t K, int64_t N) { return cdiv(N, 16) * 16 * K / 2; }
+
+int launch_pack_decode_narrow(const int32_t* qweight_kn, int32_t* out, int64_t K, int64_t N, hipStream_t st) {
+  const int64_t tiles = cdiv(N, 16);
+  const int64_t n = tiles * (K / 32) * 64;
+  if (n > 0)
+    hipLaunchKernelGGL(pack_narrow_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st, (const uint32_t*)qweight_kn,
+                       (uint32_t*)out, K, N, tiles);
+  return narrow_status();
+}
+
+// 16 waves per block (one block per CU) when the tiles fit the CUs once, else 8 (two per CU);
+// M == 1 stages the activation row in LDS when it fits
+constexpr uint32_t kNarrowLdsMax = 65536;
+
+template <int MT, bool ZP, typename T, bool SBF, bool ONE, bool XL>
+static bool launch_narrow_t(const GemmArgs& a, hipStream_t st) {
+  const int tiles = (int)cdiv(a.N, 16);
+  const int spg = a.G / 32;
+  const dim3 grid((unsigned)tiles);
+  const int nwv = tiles <= num_cus() ? 16 : 8;
+  const NarrowLds L = narrow_lds(nwv, ONE ? 1 : 16 * MT, a.K / a.G, a.K, ZP, XL);
+  if (L.total > kNarrowLdsMax) return false;
+#define AWQ_NARROW_L(NWV, SPG_) \
+  hipLaunchKernelGGL((decode_narrow_kernel<MT, NWV, SPG_, ZP, T, SBF, ONE, XL>), grid, dim3((NWV) * 64), L.total, st, a, tiles)
+  if (nwv == 16) {
+    if (spg == 4) AWQ_NARROW_L(16, 4);
+    else if (spg == 2) AWQ_NARROW_L(16, 2);
+    else AWQ_NARROW_L(16, 1);
+  } else {
+    if (spg == 4) AWQ_NARROW_L(8, 4);
+    else if (spg == 2) AWQ_NARROW_L(8, 2);
+    else AWQ_NARROW_L(8, 1);
+  }
+#undef AWQ_NARROW_L
+  return true;
+}
+
+template <bool ZP, typename T, bool SBF>
+static bool launch_narrow_m(const GemmArgs& a, hipStream_t st) {
+  if (a.M > 16) return launch_narrow_t<2, ZP, T, SBF, false, false>(a, st);
+  if (a.M > 1) return launch_narrow_t<1, ZP, T, SBF, false, false>(a, st);
+  return launch_narrow_t<1, ZP, T, SBF, true, true>(a, st) || launch_narrow_t<1, ZP, T, SBF, true, false>(a, st);
+}
+
+bool launch_decode_narrow(const GemmArgs& a, bool zp, int act, int sdt, hipStream_t st) {
+  const bool sbf = sdt == AWQ_DTYPE_BF16;
+  if (act == AWQ_DTYPE_F16) {
+    if (sbf) return zp ? launch_narrow_m<true, f16, true>(a, st) : launch_narrow_m<false, f16, true>(a, st);
+    return zp ? launch_narrow_m<true, f16, false>(a, st) : launch_narrow_m<false, f16, false>(a, st);
+  }
+  if (sbf) return zp ? launch_narrow_m<true, bf16, true>(a, st) : launch_narrow_m<false, bf16, true>(a, st);
+  return zp ? launch_narrow_m<true, bf16, false>(a, st) : launch_narrow_m<false, bf16, false>(a, st);
+}
+
+}  // namespace awq_host

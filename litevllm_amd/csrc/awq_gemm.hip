@@ -30,25 +30,6 @@ __device__ __forceinline__ WordSZ load_sz(const GemmArgs& p, int g, int word) {
   return r;
 }
 
-// waits until no vector-memory operation of this wave is outstanding (gfx9 s_waitcnt
-// encoding, expcnt and lgkmcnt unconstrained); as an intrinsic the compiler's own wait
-// bookkeeping sees it
-#define AWQ_WAIT_VMCNT0() __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0xF << 8))
-
-// 16 bytes per lane from a buffer straight into LDS: lane l's bytes land at lds + 16 l.
-// Written as assembly so the compiler does not pair it with the LDS reads of the other
-// buffer (it cannot tell the two buffers apart and would wait for every load in flight
-// before each of them); the kernel waits for these loads itself before its barrier.  M0
-// carries the LDS address and nothing else in these kernels uses M0.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void lds_dma16(const u32x4& rsrc, uint32_t lds, uint32_t voff, uint32_t soff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-               :
-               : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
-               : "memory", "m0");
-}
-#pragma clang diagnostic pop
 
 // 16-byte chunk swizzles of 128-byte LDS rows (eight chunks).  Operand reads take 16
 // consecutive rows; activation rows are stored whole, weight rows n = 8 w + c by lanes of

@@ -152,3 +152,14 @@ def test_moe_route_rejects_bad_args(lib):
     assert r(ld=4) == L.ERR_STRIDE
     assert r(dt=9) == L.ERR_UNSUPPORTED
     assert r(T=0) == L.OK
+
+
+def test_decode_layout_choice():
+    """The decode layout rule: narrow 16-column tiles only where measured faster."""
+    from litevllm_amd import ops
+    cus = L.num_cus()
+    assert ops._narrow_fits(1, 4096, 4096, 0) and ops._narrow_fits(1, 32 * cus, 14336, 0)
+    assert not ops._narrow_fits(1, 32 * cus + 16, 4096, 0)
+    assert not ops._narrow_fits(1, 4096, 4096, 2)          # an explicit split asks for the stream kernel
+    assert ops._narrow_fits(4, 16 * cus, 4096, 0) and not ops._narrow_fits(4, 16 * cus, 8192, 0)
+    assert not ops._narrow_fits(16, 16 * cus + 16, 4096, 0) and not ops._narrow_fits(17, 4096, 4096, 0)

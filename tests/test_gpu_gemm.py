@@ -188,7 +188,7 @@ def test_gemm_bf16_activations(M, K, N):
 @pytest.mark.parametrize("act,sdt", [(torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float16),
                                      (torch.float16, torch.bfloat16), (torch.float16, torch.float16)])
 @pytest.mark.parametrize("M,G", [(1, 128), (1, 64), (1, 32), (4, 128), (17, 32), (32, 64)])
-@pytest.mark.parametrize("stream", [True, False])
+@pytest.mark.parametrize("stream", ["stream", "narrow", False])
 @pytest.mark.parametrize("zp", [True, False])
 def test_decode_dtype_combinations(act, sdt, M, G, stream, zp):
     """Every activation / scale dtype pair through the decode kernel, stream copy or AutoAWQ
@@ -202,7 +202,7 @@ def test_decode_dtype_combinations(act, sdt, M, G, stream, zp):
     xa = torch.from_numpy(p["x"]).to(act)
     qz = torch.from_numpy(p["qzeros"]).to(DEV) if zp else None
     y = ops.gemm(xa.to(DEV), torch.from_numpy(p["qweight"]).to(DEV), sc.to(DEV), qz, G, layout="autoawq",
-                 decode_stream=stream).float().cpu().numpy()
+                 decode_stream=stream is not False, decode_layout=stream or None).float().cpu().numpy()
     w = O.dequant_awq(p["qweight"], sc.float().numpy(), p["qzeros"] if zp else None, G, out_dtype="float32",
                       zero_point=zp)
     ye = xa.double().numpy() @ w.astype(np.float64)
@@ -330,6 +330,52 @@ def _stream_layout_numpy(qw_kn):
     n = np.stack([plo, phi], axis=2)                         # [s, q, e, v, t, r]
     lane = n.transpose(4, 0, 2, 1, 5, 3)                     # [t, s, e, q, r, v]
     return np.ascontiguousarray(lane).reshape(-1).view(np.int32)
+
+
+def _narrow_layout_numpy(qw):
+    """Narrow decode layout: (tile t, k-step s, lane 16 q + r) -> u32 holding column 16 t + r at
+    rows 32 s + 8 q + j, row j at bit 16 (j % 2) + 4 (j // 2)."""
+    K, NW = qw.shape
+    N = NW * 8
+    tiles, KS = -(-N // 16), K // 32
+    pad = np.zeros((K, tiles * 16), dtype=np.uint32)
+    pad[:, :N] = O.unpack_awq(qw)
+    v = pad.reshape(KS, 4, 8, tiles, 16)                     # [s, q, j, t, r]
+    out = np.zeros((tiles, KS, 4, 16), dtype=np.uint32)
+    for j in range(8):
+        out |= v[:, :, j].transpose(2, 0, 1, 3) << np.uint32((j & 1) * 16 + (j >> 1) * 4)
+    return out.reshape(-1).view(np.int32)
+
+
+@pytest.mark.parametrize("K,N", [(256, 4096), (128, 1000), (64, 520), (32, 8)])
+def test_pack_decode_narrow_layout(K, N):
+    ops = _lib()
+    rng = np.random.default_rng(K * 3 + N)
+    qw = rng.integers(-2**31, 2**31 - 1, size=(K, N // 8), dtype=np.int64).astype(np.int32)
+    got = ops.pack_decode_narrow(torch.from_numpy(qw).to(DEV)).cpu().numpy()
+    assert np.array_equal(got, _narrow_layout_numpy(qw))
+
+
+@pytest.mark.parametrize("M,K,N,G", [(1, 4096, 4096, 128), (1, 2048, 1000, 32), (4, 4096, 6144, 128),
+                                     (16, 1024, 520, 64), (17, 2048, 1536, 128), (32, 512, 264, 32),
+                                     (1, 14336, 4096, 128), (9, 96, 2056, 32)])
+@pytest.mark.parametrize("zp", [True, False])
+def test_gemm_decode_narrow_vs_oracle(M, K, N, G, zp):
+    """The narrow layout (whole K per 16-column block): within 1 ulp of the exact oracle with
+    unrounded weights, bias included, and bitwise stable across calls."""
+    ops = _lib()
+    _note(f"decode narrow M={M} K={K} N={N} G={G} zp={zp}")
+    p = make_awq_problem(M=M, K=K, N=N, group_size=G, seed=M + 3 * N + K)
+    t = _to_dev(p)
+    qz = t["qzeros"] if zp else None
+    b = torch.from_numpy(np.random.default_rng(M).standard_normal(N).astype(np.float32)).half()
+    y = ops.gemm(t["x"], t["qweight"], t["scales"], qz, G, bias=b.to(DEV), layout="autoawq",
+                 decode_stream=True, decode_layout="narrow")
+    y2 = ops.gemm(t["x"], t["qweight"], t["scales"], qz, G, bias=b.to(DEV), layout="autoawq",
+                  decode_stream=True, decode_layout="narrow")
+    assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
+    w = _w_used(p, M, G, zp=zp)
+    _check_vs_exact(y.cpu().numpy(), O.linear_exact(p["x"], w.T, b.double().numpy()), f"narrow M={M} N={N}")
 
 
 @pytest.mark.parametrize("K,N", [(256, 4096), (128, 1000), (64, 520)])
