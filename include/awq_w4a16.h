@@ -235,7 +235,7 @@ int awq_w4a16_gate_up_interleave(const void* gate, const void* up, void* out, in
                                  int32_t elem_bytes, int32_t half_tile, void* stream);
 
 /* Workspace of awq_w4a16_gate_up_act: that of awq_w4a16_gemm for the interleaved matrix,
- * N = 2 * ceil(I / 64) * 64 (same zeroing rule). */
+ * N = 2 * ceil(I / 64) * 64 (same zeroing rule); 0 for DECODE_NARROW. */
 size_t awq_w4a16_gate_up_workspace_bytes(int64_t M, int64_t I, int64_t K, int32_t group_size,
                                          int32_t split_k, int32_t layout);
 
@@ -244,7 +244,9 @@ size_t awq_w4a16_gate_up_workspace_bytes(int64_t M, int64_t I, int64_t K, int32_
  *   x: [M, K] act_dtype (F16 or BF16), row stride ldx; out: [M, I] act_dtype, row stride ldo.
  *   qweight / scales / qzeros: the interleaved matrix in layout AUTOAWQ or KN_SEQ
  *   ([K, N/8] words, N = 2 * ceil(I / 64) * 64) or DECODE_STREAM (its awq_w4a16_pack_decode_stream
- *   copy); qzeros NULL = symmetric z = 8 (the reference's mode).
+ *   copy); or DECODE_NARROW: the pair interleaved per 8 columns instead (half_tile 1 for
+ *   words, 8 for scales; N = 2 * ceil(I / 8) * 8), qweight as its awq_w4a16_pack_decode_narrow
+ *   copy, no workspace.  qzeros NULL = symmetric z = 8 (the reference's mode).
  *   1 <= M <= 32 (the reference takes M == 1); group_size 32, 64 or 128 dividing K.
  *   split_k as for awq_w4a16_gemm; results are bitwise reproducible for a given split. */
 int awq_w4a16_gate_up_act(const void* x, int64_t ldx, const int32_t* qweight, const void* scales,

@@ -282,7 +282,7 @@ int awq_w4a16_gate_up_interleave(const void* gate, const void* up, void* out, in
 
 size_t awq_w4a16_gate_up_workspace_bytes(int64_t M, int64_t I, int64_t K, int32_t group_size,
                                          int32_t split_k, int32_t layout) {
-  if (I <= 0) return 0;
+  if (I <= 0 || layout == AWQ_LAYOUT_DECODE_NARROW) return 0;
   return awq_w4a16_gemm_workspace_bytes(M, 2 * cdiv(I, 64) * 64, K, group_size, split_k, layout);
 }
 
@@ -296,15 +296,19 @@ int awq_w4a16_gate_up_act(const void* x, int64_t ldx, const int32_t* qweight, co
   if (!x || !qweight || !scales || !out) return AWQ_ERR_NULL;
   if (!dtype_16(act_dtype) || !dtype_16(scale_dtype)) return AWQ_ERR_UNSUPPORTED;
   if (activation != AWQ_MOE_ACT_SILU && activation != AWQ_MOE_ACT_GELU_TANH) return AWQ_ERR_UNSUPPORTED;
-  if (layout != AWQ_LAYOUT_AUTOAWQ && layout != AWQ_LAYOUT_KN_SEQ && layout != AWQ_LAYOUT_DECODE_STREAM)
+  if (layout != AWQ_LAYOUT_AUTOAWQ && layout != AWQ_LAYOUT_KN_SEQ && layout != AWQ_LAYOUT_DECODE_STREAM &&
+      layout != AWQ_LAYOUT_DECODE_NARROW)
     return AWQ_ERR_UNSUPPORTED;
   if (!decode_covers(M, group_size)) return AWQ_ERR_UNSUPPORTED;
   if ((K % group_size) != 0) return AWQ_ERR_SHAPE;
+  const bool narrow = layout == AWQ_LAYOUT_DECODE_NARROW;
+  if (narrow && (K % 32) != 0) return AWQ_ERR_SHAPE;
   if (ldx < K || ldo < I || (ldx % 8) != 0) return AWQ_ERR_STRIDE;
   if ((((uintptr_t)x) & 15) || (((uintptr_t)out) & 1) || (((uintptr_t)scales) & 15) ||
       (((uintptr_t)qweight) & 15))
     return AWQ_ERR_STRIDE;
-  const int64_t N = 2 * cdiv(I, 64) * 64;  // the interleaved matrix
+  // the interleaved matrix: 64-column halves (8 for the narrow layout)
+  const int64_t N = narrow ? 2 * cdiv(I, 8) * 8 : 2 * cdiv(I, 64) * 64;
   if (decode_stream_bytes(K, N) > 0x7FFFFFFFLL || M * ldx * 2 > 0x7FFFFFFFLL) return AWQ_ERR_UNSUPPORTED;
 
   GemmArgs ga{};
@@ -322,6 +326,12 @@ int awq_w4a16_gate_up_act(const void* x, int64_t ldx, const int32_t* qweight, co
   ga.bias_dtype = AWQ_DTYPE_NONE;
   ga.gate_act = 1 + activation;
   ga.n_out = (int)I;
+  if (narrow) {
+    if (decode_narrow_bytes(K, N) > 0x7FFFFFFFLL) return AWQ_ERR_UNSUPPORTED;
+    if (!launch_decode_narrow(ga, qzeros != nullptr, act_dtype, scale_dtype, (hipStream_t)stream))
+      return AWQ_ERR_UNSUPPORTED;
+    return launch_status();
+  }
   const DecodeMode mode = decode_mode(layout, act_dtype, scale_dtype);
   const DecodePlan sp = plan_decode(M, N, K, group_size, split_k, mode);
   if (sp.ws_bytes) {

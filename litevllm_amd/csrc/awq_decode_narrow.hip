@@ -15,6 +15,8 @@
 //    kernel and the reference's M = 1 formulation (awq_fused_gemm.py:1966-1971).
 //  * The block's waves take contiguous shares of K with an 8-deep register ring (one u32 of
 //    weights per k-step and lane), meet in LDS, and sum in wave order (bitwise reproducible).
+//  * Gated epilogue (GemmArgs::gate_act): the gate/up pair interleaved per 8 columns, so a
+//    tile's columns c < 8 and 8 + c are the gate and up sums of output 8 t + c.
 #include "awq_decode_kernel.h"
 
 namespace awq {
@@ -205,6 +207,21 @@ decode_narrow_kernel(const GemmArgs p, int tiles) {
       if (m < p.M) red[(wave * MROWS + m) * 16 + r] = ONE ? tot1 : tot[mt][v];
     }
   __syncthreads();
+  if (p.gate_act) {
+    // gated epilogue: columns c < 8 of the tile are gate sums, 8 + c the matching up sums
+    for (int o = tid; o < p.M * 8; o += NWV * 64) {
+      const int m = o >> 3, c = o & 7;
+      float g = red[m * 16 + c], u = red[m * 16 + 8 + c];
+#pragma unroll
+      for (int w = 1; w < NWV; ++w) {
+        g += red[(w * MROWS + m) * 16 + c];
+        u += red[(w * MROWS + m) * 16 + 8 + c];
+      }
+      const int oc = t * 8 + c;
+      if (oc < p.n_out) p.c[(int64_t)m * p.ldc + oc] = to_bits<T>(gated_act(g, p.gate_act - 1) * u);
+    }
+    return;
+  }
   for (int o = tid; o < p.M * 16; o += NWV * 64) {
     const int m = o >> 4, c = o & 15;
     float sum = red[m * 16 + c];

@@ -326,9 +326,11 @@ def _pad_rows(t: torch.Tensor | None, rows: int) -> torch.Tensor | None:
 
 
 def pack_gate_up(gate_qweight, up_qweight, gate_scales, up_scales, gate_qzeros, up_qzeros,
-                 group_size: int, layout: str = "ref", stream: bool = False):
+                 group_size: int, layout: str = "ref", kind: str = "autoawq"):
     """The interleaved gate/up matrix of ``gate_up_act``: ``(qweight [K, N/8], scales [K/G, N],
-    qzeros [K/G, N/8] or None, decode stream copy or None)`` with N = 2 * ceil(I / 64) * 64.
+    qzeros [K/G, N/8] or None, derived decode copy or None)``.  ``kind`` "autoawq" or
+    "stream" (the decode stream copy) interleave per 64 columns, N = 2 * ceil(I / 64) * 64;
+    "narrow" (the narrow decode copy) per 8 columns, N = 2 * ceil(I / 8) * 8.
 
     ``layout="ref"`` takes the reference's [I, K/8] weights and [I, K/G] scales (I need not be
     a multiple of 8: the missing rows are zero weights with zero scales); "autoawq" takes
@@ -344,10 +346,12 @@ def pack_gate_up(gate_qweight, up_qweight, gate_scales, up_scales, gate_qzeros, 
         (gq, gs, gz), (uq, us, uz) = packed
     else:
         gq, gs, gz, uq, us, uz = gate_qweight, gate_scales, gate_qzeros, up_qweight, up_scales, up_qzeros
-    qw = gate_up_interleave(gq, uq, 8)
-    sc = gate_up_interleave(gs, us, 64)
-    qz = gate_up_interleave(gz, uz, 8) if gz is not None else None
-    return qw, sc, qz, (pack_decode_stream(qw) if stream else None)
+    wh, sh = (1, 8) if kind == "narrow" else (8, 64)
+    qw = gate_up_interleave(gq, uq, wh)
+    sc = gate_up_interleave(gs, us, sh)
+    qz = gate_up_interleave(gz, uz, wh) if gz is not None else None
+    derived = {"stream": pack_decode_stream, "narrow": pack_decode_narrow}.get(kind)
+    return qw, sc, qz, (derived(qw) if derived else None)
 
 
 GATE_UP_CACHE = _DerivedCache(pack_gate_up)
@@ -360,11 +364,12 @@ def gate_up_act(x: torch.Tensor, gate_qweight: torch.Tensor, up_qweight: torch.T
                 gate_scales: torch.Tensor, up_scales: torch.Tensor, group_size: int,
                 gate_qzeros: torch.Tensor | None = None, up_qzeros: torch.Tensor | None = None,
                 activation: str = "silu", layout: str = "ref", out: torch.Tensor | None = None,
-                split_k: int = 0) -> torch.Tensor:
-    """``out[M, I] = act(x @ Wg^T) * (x @ Wu^T)`` in one launch of the decode kernel with its
+                split_k: int = 0, decode_layout: str | None = None) -> torch.Tensor:
+    """``out[M, I] = act(x @ Wg^T) * (x @ Wu^T)`` in one launch of a decode kernel with its
     gated epilogue (M <= 32).  ``activation``: "gelu" / "gelu_pytorch_tanh" select GELU (tanh
     form), anything else SiLU, as the reference decides (awq_fused_gemm.py:3040-3041).  The
-    interleaved weight pair is built once and cached."""
+    interleaved weight pair is built once and cached.  ``decode_layout``: "narrow", "stream"
+    or None (chosen by shape, as for ``gemm``)."""
     lib = L.load()
     if x.dim() != 2:
         raise ValueError("x must be 2-D")
@@ -379,10 +384,16 @@ def gate_up_act(x: torch.Tensor, gate_qweight: torch.Tensor, up_qweight: torch.T
     if kw != K:
         raise ValueError(f"K mismatch: x has {K}, weights have {kw}")
     act = GATE_UP_ACTIVATIONS.get(str(activation).lower(), L.MOE_ACT_SILU)
-    use_stream = K % 32 == 0 and M <= DECODE_MAX_M
+    if decode_layout not in (None, "narrow", "stream"):
+        raise ValueError(f"unknown decode_layout {decode_layout!r}")
+    kind = "autoawq"
+    if K % 32 == 0 and M <= DECODE_MAX_M:
+        n_narrow = 2 * (-(-I // 8)) * 8
+        narrow = decode_layout == "narrow" or (decode_layout is None and _narrow_fits(M, n_narrow, K, int(split_k)))
+        kind = "narrow" if narrow else "stream"
     qw, sc, qz, st = GATE_UP_CACHE.get(gate_qweight, up_qweight, gate_scales, up_scales, gate_qzeros,
-                                       up_qzeros, args=(int(group_size), layout, use_stream))
-    lc = L.LAYOUT_DECODE_STREAM if st is not None else L.LAYOUT_AUTOAWQ
+                                       up_qzeros, args=(int(group_size), layout, kind))
+    lc = {"narrow": L.LAYOUT_DECODE_NARROW, "stream": L.LAYOUT_DECODE_STREAM}.get(kind, L.LAYOUT_AUTOAWQ)
     if st is not None:
         qw = st
     x = x if x.stride(1) == 1 and x.stride(0) % 8 == 0 else x.contiguous()

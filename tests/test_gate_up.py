@@ -206,6 +206,25 @@ def test_fused_gate_up_m1_matches_oracle(n, k, act, dt, group32):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("n,k", [(704, 2816), (257, 288), (1000, 1536), (8, 32)])
+@pytest.mark.parametrize("M", [1, 4, 17])
+@pytest.mark.parametrize("layout", ["narrow", "stream"])
+def test_gate_up_act_both_decode_layouts(n, k, M, layout):
+    """The gated epilogue of both decode kernels: 16-column narrow tiles (pair interleaved per
+    8 columns) and 128-column stream tiles (per 64)."""
+    from litevllm_amd import ops
+    print(f"gate_up_act layout={layout} n={n} k={k} M={M}", flush=True)
+    for dt in (torch.bfloat16, torch.float16):
+        pair = _pair(n, k, seed=n + M, sdt=dt)
+        (qg, sg), (qu, su) = pair
+        x = torch.randn(M, k, dtype=dt)
+        y = ops.gate_up_act(x.to(DEV), qg.to(DEV), qu.to(DEV), sg.to(DEV), su.to(DEV), 32,
+                            activation="gelu_pytorch_tanh", decode_layout=layout)
+        torch.cuda.synchronize()
+        _check(y, _exact(x, pair, 32, "gelu_pytorch_tanh"), dt, (layout, n, k, M, dt))
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("M", [1, 3, 16, 17, 32])
 @pytest.mark.parametrize("split_k", [0, 1, 3, 7])
 def test_gate_up_act_rows_and_splits(M, split_k):
