@@ -28,24 +28,24 @@ namespace awq {
 struct NarrowLds {
   uint32_t sc, zw, x, total;
 };
-__host__ __device__ inline NarrowLds narrow_lds(int nwv, int mrows, int ngroups, int K, bool zp, bool xl) {
+__host__ __device__ inline NarrowLds narrow_lds(int nwv, int mrows, int ngroups, int K, bool zp, int xrows) {
   const uint32_t n_pieces = ((uint32_t)ngroups * 2u + 63u) / 64u;  // instructions for scales, and for zeros
   NarrowLds l;
   l.sc = (uint32_t)(nwv * mrows * 16 * 4);
   l.zw = l.sc + n_pieces * 1024u;
   l.x = l.zw + (zp ? n_pieces * 256u : 0u);
-  l.total = l.x + (xl ? ((uint32_t)K / 8u + 63u) / 64u * 1024u : 0u);
+  l.total = l.x + ((uint32_t)xrows * (uint32_t)K / 8u + 63u) / 64u * 1024u;
   return l;
 }
 
-// XL (M == 1): the activation row is staged in LDS once and every lane reads its k-slice from
-// there (the MFMA's other 15 rows repeat row 0 and are never read back); otherwise each
-// k-step loads the token rows per lane.
+// XL (one token tile): the M activation rows are staged in LDS once ([M][K]) and every lane
+// reads its k-slice of row min(r, M - 1) from there (the MFMA's rows past M repeat a real row
+// and are never read back); otherwise each k-step loads the token rows per lane.
 template <int MT, int NWV, int SPG, bool ZP, typename T, bool SBF, bool ONE, bool XL>
 __global__ void __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(4, 4)))
 decode_narrow_kernel(const GemmArgs p, int tiles) {
   static_assert(!ONE || MT == 1, "");
-  static_assert(!XL || ONE, "");
+  static_assert(!XL || MT == 1, "");
   constexpr int D = 8;
   constexpr int MROWS = ONE ? 1 : 16 * MT;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -59,7 +59,7 @@ decode_narrow_kernel(const GemmArgs p, int tiles) {
   const int col = t * 16 + r;
   const int NW = p.N >> 3;
   const int ngroups = p.K / p.G;
-  const NarrowLds L = narrow_lds(NWV, MROWS, ngroups, p.K, ZP, XL);
+  const NarrowLds L = narrow_lds(NWV, MROWS, ngroups, p.K, ZP, XL ? p.M : 0);
   float* red = (float*)smem;
   const uint16_t* s_lds = (const uint16_t*)(smem + L.sc);
   const uint32_t* z_lds = (const uint32_t*)(smem + L.zw);
@@ -71,10 +71,11 @@ decode_narrow_kernel(const GemmArgs p, int tiles) {
   {
     const u32x4 srs = rsrc_words(p.sc, (uint32_t)((uint64_t)ngroups * p.N * 2u));
     const u32x4 zrs = rsrc_words(p.qz, ZP ? (uint32_t)((uint64_t)ngroups * NW * 4u) : 0u);
-    const u32x4 xrs = rsrc_words(p.a, (uint32_t)((uint64_t)p.lda * 2u));
+    const u32x4 xrs = rsrc_words(p.a, (uint32_t)((uint64_t)p.M * (uint64_t)p.lda * 2u));
     const int n_s = (ngroups * 2 + 63) / 64;      // 16-byte pieces: group i / 2, half i % 2
     const int n_z = ZP ? (ngroups * 2 + 63) / 64 : 0;  // words: group i / 2, word 2t + i % 2
-    const int n_x = XL ? (p.K / 8 + 63) / 64 : 0;     // 16-byte pieces of the row
+    const int kp = p.K / 8;                            // 16-byte pieces per activation row
+    const int n_x = XL ? (p.M * kp + 63) / 64 : 0;
     for (int j = wave; j < n_s + n_z + n_x; j += NWV) {
       if (j < n_s) {
         const int i = j * 64 + lane;
@@ -88,8 +89,9 @@ decode_narrow_kernel(const GemmArgs p, int tiles) {
         lds_dma4(zrs, lds_base + L.zw + (uint32_t)(j - n_s) * 256u, voff, 0u);
       } else {
         const int i = (j - n_s - n_z) * 64 + lane;
-        lds_dma16(xrs, lds_base + L.x + (uint32_t)(j - n_s - n_z) * 1024u, i < p.K / 8 ? (uint32_t)i * 16u : 0x80000000u,
-                  0u);
+        const int row = i / kp, pc = i - row * kp;
+        lds_dma16(xrs, lds_base + L.x + (uint32_t)(j - n_s - n_z) * 1024u,
+                  row < p.M ? ((uint32_t)row * (uint32_t)p.lda + 8u * (uint32_t)pc) * 2u : 0x80000000u, 0u);
       }
     }
   }
@@ -106,6 +108,7 @@ decode_narrow_kernel(const GemmArgs p, int tiles) {
   for (int mt = 0; mt < MT; ++mt) x_lane_off[mt] = ((uint32_t)(mt * 16 + r) * (uint32_t)p.lda + 8u * (uint32_t)q) * 2u;
   const uint32_t w_lane_off = (uint32_t)lane * 4u;
   const int zsh = 4 * col_nib<false>(r & 7);
+  const int x_row_off = ONE ? 0 : min(r, p.M - 1) * p.K;  // XL: the lane's activation row in LDS
   const MagicK mk = magic_consts();
 
   uint32_t wr[D];
@@ -167,7 +170,7 @@ decode_narrow_kernel(const GemmArgs p, int tiles) {
       else op[u] = pack2<bf16>((float)d.x, (float)d.y);
     }
     if constexpr (XL) {
-      const u32x4 xv = *(const u32x4*)(x_lds + ks * 32 + 8 * q);
+      const u32x4 xv = *(const u32x4*)(x_lds + x_row_off + ks * 32 + 8 * q);
       acc[0] = MfmaOp<T>::run(xv, op, acc[0]);
     } else {
 #pragma unroll
@@ -289,7 +292,7 @@ static bool launch_narrow_t(const GemmArgs& a, hipStream_t st) {
   const int spg = a.G / 32;
   const dim3 grid((unsigned)tiles);
   const int nwv = tiles <= num_cus() ? 16 : 8;
-  const NarrowLds L = narrow_lds(nwv, ONE ? 1 : 16 * MT, a.K / a.G, a.K, ZP, XL);
+  const NarrowLds L = narrow_lds(nwv, ONE ? 1 : 16 * MT, a.K / a.G, a.K, ZP, XL ? a.M : 0);
   if (L.total > kNarrowLdsMax) return false;
 #define AWQ_NARROW_L(NWV, SPG_) \
   hipLaunchKernelGGL((decode_narrow_kernel<MT, NWV, SPG_, ZP, T, SBF, ONE, XL>), grid, dim3((NWV) * 64), L.total, st, a, tiles)
@@ -309,7 +312,8 @@ static bool launch_narrow_t(const GemmArgs& a, hipStream_t st) {
 template <bool ZP, typename T, bool SBF>
 static bool launch_narrow_m(const GemmArgs& a, hipStream_t st) {
   if (a.M > 16) return launch_narrow_t<2, ZP, T, SBF, false, false>(a, st);
-  if (a.M > 1) return launch_narrow_t<1, ZP, T, SBF, false, false>(a, st);
+  if (a.M > 1)
+    return launch_narrow_t<1, ZP, T, SBF, false, true>(a, st) || launch_narrow_t<1, ZP, T, SBF, false, false>(a, st);
   return launch_narrow_t<1, ZP, T, SBF, true, true>(a, st) || launch_narrow_t<1, ZP, T, SBF, true, false>(a, st);
 }
 

@@ -141,7 +141,10 @@ moe_gemm_kernel(const MoeArgs p) {
       // past the wave's last unit the ring's refills go through empty descriptors (zeros,
       // no memory traffic), so every ring turn is a whole one
       int iks = ks0, ileft = nunits;
-      auto issue = [&](int slot) {
+      // scales and zeros only where a group starts or in the first turn (prep reads no other
+      // slot's); the single-tile kernel keeps per-unit loads (its 128 registers have no room
+      // to hold a slot's constants across turns)
+      auto issue = [&](int slot, bool first_turn) {
         const int ks = iks;
         const bool past = ileft <= 0;
         ++iks;
@@ -161,11 +164,13 @@ moe_gemm_kernel(const MoeArgs p) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
           xr[slot][mt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)x_off[mt], ks * 64, 0));
-        const int g = ks / SPG;
-        sz[slot].s4 = __builtin_bit_cast(
-            u32x4, __builtin_amdgcn_raw_buffer_load_b128(srs, (int)(16u * wc), (int)((uint32_t)g * (uint32_t)p.N * 2u), 0));
-        sz[slot].zw = ZP ? __builtin_amdgcn_raw_buffer_load_b32(zrs, (int)(4u * wc), (int)((uint32_t)g * (uint32_t)NW * 4u), 0)
-                         : 0x88888888u;
+        if (first_turn || (ks & (SPG - 1)) == 0 || MT == 1) {  // wave-uniform
+          const int g = ks / SPG;
+          sz[slot].s4 = __builtin_bit_cast(
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(srs, (int)(16u * wc), (int)((uint32_t)g * (uint32_t)p.N * 2u), 0));
+          sz[slot].zw = ZP ? __builtin_amdgcn_raw_buffer_load_b32(zrs, (int)(4u * wc), (int)((uint32_t)g * (uint32_t)NW * 4u), 0)
+                           : 0x88888888u;
+        }
       };
       // FRESH: the group's first unit (its MFMAs start from zero)
       auto compute = [&](int slot, auto fresh) {
@@ -221,7 +226,7 @@ moe_gemm_kernel(const MoeArgs p) {
       };
 
 #pragma unroll
-      for (int u = 0; u < D; ++u) issue(u);
+      for (int u = 0; u < D; ++u) issue(u, true);
       __builtin_amdgcn_sched_barrier(0);
       // (one token tile runs without it: the extra loop would cost the registers that let
       // four waves share a SIMD)
@@ -235,7 +240,7 @@ moe_gemm_kernel(const MoeArgs p) {
             if (u == 0) compute(0, std::true_type{});
             else compute(u % D, std::false_type{});
             __builtin_amdgcn_sched_barrier(0);
-            issue(u % D);
+            issue(u % D, false);
             __builtin_amdgcn_sched_barrier(0);
           }
           flush(std::false_type{});
@@ -261,7 +266,7 @@ moe_gemm_kernel(const MoeArgs p) {
               }
             }
             __builtin_amdgcn_sched_barrier(0);
-            issue(u);
+            issue(u, false);
             __builtin_amdgcn_sched_barrier(0);
           }
         }

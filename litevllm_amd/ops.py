@@ -240,11 +240,12 @@ def _use_decode_stream(M, K, group_size, a, scales, layout, decode_stream):
 def _narrow_fits(M: int, N: int, K: int, split_k: int) -> bool:
     """Whether the narrow layout (one block per 16 columns over the whole K, no split-K hand-
     off) serves a decode-shaped call faster than the 128-column stream (measured on MI355X:
-    M = 1 up to two 16-column tiles per CU; 2 <= M <= 16 up to one tile per CU and K <= 4096)."""
+    up to two 16-column tiles per CU while the activation rows fit the kernel's LDS staging,
+    M = 1 .. 4; otherwise, up to M = 16, one tile per CU and K <= 4096)."""
     if split_k != 0:
         return False
     tiles = -(-N // 16)
-    if M == 1:
+    if M <= 4 and M * K * 2 <= 49152:
         return tiles <= 2 * L.num_cus()
     return M <= 16 and tiles <= L.num_cus() and K <= 4096
 
