@@ -3,6 +3,7 @@ reference's Python call surface for that path."""
 from . import _lib, ops  # noqa: F401
 from .awq import AWQConfig  # noqa: F401
 from .awq_fused_gemm import (  # noqa: F401
+    awq_decode_gemv_enabled,
     awq_fused_gate_up_enabled,
     awq_fused_gate_up_group32_enabled,
     awq_fused_gemm,
@@ -10,6 +11,10 @@ from .awq_fused_gemm import (  # noqa: F401
     packed_int4_symmetric_fused_gate_up_group32_m1,
     packed_int4_symmetric_fused_gate_up_m1,
     packed_int4_symmetric_fused_gate_up_m1_safe,
+    packed_int4_symmetric_fused_qkv_m1,
+    packed_int4_symmetric_fused_qkv_m1_safe,
+    packed_int4_symmetric_fused_qkv_m2,
+    packed_int4_symmetric_fused_qkv_m2_safe,
     packed_int4_symmetric_fused_gemm,
     packed_int4_symmetric_fused_gemm_safe,
 )

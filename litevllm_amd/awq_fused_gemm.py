@@ -3,7 +3,9 @@
 ``packed_int4_symmetric_fused_gemm_safe`` keep the reference's arguments, validation,
 reason strings and split-K knob; the launch goes to the gfx950 HIP kernels.  The M = 1
 fused gate/up surfaces (``packed_int4_symmetric_fused_gate_up_m1``, its ``group32`` twin,
-``..._m1_safe`` and the two policy switches) do the same for the gated MLP.
+``..._m1_safe`` and the two policy switches) do the same for the gated MLP, and the fused QKV
+surfaces (``packed_int4_symmetric_fused_qkv_m1/_m2(_safe)``, ``awq_decode_gemv_enabled``) for
+the attention projections.
 
 Differences, all deliberate:
   * split-K partials are reduced in fp32 in a fixed order (the reference rounds each
@@ -297,6 +299,148 @@ def packed_int4_symmetric_fused_gate_up_m1_safe(a, gate_qweight, up_qweight, gat
                    gate_scales.contiguous(), up_scales.contiguous(), int(group_size),
                    activation=activation, out=out, config=config, policy=policy)
         if c.shape != (1, int(gate_qweight.shape[0])):
+            return c, False, "bad_output_shape"
+        return c, True, "ok"
+    except Exception:
+        return a, False, "kernel_exception"
+
+
+# ------------------------------------------------------------------ fused QKV (M = 1, 2)
+def awq_decode_gemv_enabled(*, config: Any | None = None, policy: dict | None = None) -> bool:
+    """Policy key ``awq_decode_gemv``, default off (``awq_fused_gemm.py:503-509``)."""
+    return _policy_flag(config, policy, "awq_decode_gemv")
+
+
+def _concat_qkv(q_qweight, k_qweight, v_qweight, q_scales, k_scales, v_scales):
+    """q | k | v along N in the reference layout, rows padded to a multiple of 8 with zero
+    weights and zero scales (built once per weight triple and cached)."""
+    qw = [q_qweight, k_qweight] + ([v_qweight] if v_qweight is not None else [])
+    sc = [q_scales, k_scales] + ([v_scales] if v_scales is not None else [])
+    qw = torch.cat([t.to(torch.int32) for t in qw], 0)
+    sc = torch.cat(list(sc), 0)
+    pad = (-int(qw.shape[0])) % 8
+    if pad:
+        qw = torch.cat([qw, qw.new_zeros((pad, qw.shape[1]))], 0)
+        sc = torch.cat([sc, sc.new_zeros((pad, sc.shape[1]))], 0)
+    return qw.contiguous(), sc.contiguous()
+
+
+_QKV_CACHE = ops._DerivedCache(_concat_qkv)
+
+
+def _qkv(a, q_qweight, k_qweight, v_qweight, q_scales, k_scales, v_scales, group_size, out):
+    has_v = v_qweight is not None and v_scales is not None
+    if not has_v:
+        v_qweight = v_scales = None
+    total_n = int(q_qweight.shape[0]) + int(k_qweight.shape[0]) + (int(v_qweight.shape[0]) if has_v else 0)
+    qw, sc = _QKV_CACHE.get(q_qweight, k_qweight, v_qweight, q_scales, k_scales, v_scales)
+    m = int(a.shape[0])
+    if out is None:
+        out = torch.empty((m, total_n), device=a.device, dtype=a.dtype)
+    if int(qw.shape[0]) == total_n and out.is_contiguous():
+        return ops.gemm(a, qw, sc, None, int(group_size), layout="ref", out=out)
+    y = ops.gemm(a, qw, sc, None, int(group_size), layout="ref")
+    out.copy_(y[:, :total_n])
+    return out
+
+
+def packed_int4_symmetric_fused_qkv_m1(a, q_qweight, k_qweight, v_qweight, q_scales, k_scales, v_scales,
+                                       group_size, *, out=None, config: Any | None = None,
+                                       policy: dict | None = None):
+    """``[q | k | v] = a @ W^T`` for symmetric packed int4 (z = 8) reference-layout projections
+    in one launch (``awq_fused_gemm.py:3345-3423``; kernel ``1286-1402``): the three weights
+    concatenated along N once (cached) and served by the decode kernels, unrounded
+    ``(q - 8) * s`` weights summed in fp32, one rounding."""
+    m, k = a.shape
+    if m != 1:
+        raise ValueError("packed_int4_symmetric_fused_qkv_m1: requires M == 1")
+    if int(group_size) != 32 or k % 32 != 0:
+        raise ValueError("packed_int4_symmetric_fused_qkv_m1: requires group_size=32 and K%32==0")
+    del config, policy
+    return _qkv(a, q_qweight, k_qweight, v_qweight, q_scales, k_scales, v_scales, group_size, out)
+
+
+def packed_int4_symmetric_fused_qkv_m2(a, q_qweight, k_qweight, v_qweight, q_scales, k_scales, v_scales,
+                                       group_size, *, config: Any | None = None, policy: dict | None = None):
+    """The M = 2 form (``awq_fused_gemm.py:3426-3523``)."""
+    if int(a.shape[0]) != 2:
+        raise ValueError("packed_int4_symmetric_fused_qkv_m2: requires M == 2")
+    del config, policy
+    return _qkv(a, q_qweight, k_qweight, v_qweight, q_scales, k_scales, v_scales, group_size, None)
+
+
+def packed_int4_symmetric_fused_qkv_m1_safe(a, q_qweight, k_qweight, v_qweight, q_scales, k_scales, v_scales,
+                                            group_size, *, config: Any | None = None,
+                                            policy: dict | None = None) -> tuple[torch.Tensor, bool, str]:
+    """Never raises; the reference's checks, order and reasons (``awq_fused_gemm.py:3526-3589``)."""
+    if not awq_decode_gemv_enabled(config=config, policy=policy):
+        return a, False, "decode_gemv_disabled"
+    if a.dim() != 2 or int(a.shape[0]) != 1:
+        return a, False, "input_not_m1_2d"
+    if q_qweight.dim() != 2 or k_qweight.dim() != 2:
+        return a, False, "qk_weight_not_2d"
+    if q_scales.dim() != 2 or k_scales.dim() != 2:
+        return a, False, "qk_scales_not_2d"
+    has_v = v_qweight is not None and v_scales is not None
+    if has_v and (v_qweight.dim() != 2 or v_scales.dim() != 2):
+        return a, False, "v_bad_shape"
+    if int(group_size) != 32:
+        return a, False, "group_size_not_32"
+    k = int(a.shape[1])
+    if k % 32 != 0:
+        return a, False, "k_not_group_aligned"
+    if k != int(q_qweight.shape[1]) * 8 or k != int(k_qweight.shape[1]) * 8:
+        return a, False, "qk_k_mismatch"
+    if has_v and k != int(v_qweight.shape[1]) * 8:
+        return a, False, "v_k_mismatch"
+    tensors = [q_qweight, k_qweight, q_scales, k_scales] + ([v_qweight, v_scales] if has_v else [])
+    if any(t.device != a.device for t in tensors):
+        return a, False, "device_mismatch"
+    if a.dtype not in (torch.float16, torch.bfloat16):
+        return a, False, f"unsupported_dtype_{str(a.dtype)}"
+    try:
+        c = packed_int4_symmetric_fused_qkv_m1(
+            a.contiguous(), q_qweight.contiguous(), k_qweight.contiguous(),
+            v_qweight.contiguous() if has_v else None, q_scales.contiguous(), k_scales.contiguous(),
+            v_scales.contiguous() if has_v else None, int(group_size), config=config, policy=policy)
+        expected_n = int(q_qweight.shape[0]) + int(k_qweight.shape[0]) + (int(v_qweight.shape[0]) if has_v else 0)
+        if c.shape != (1, expected_n):
+            return c, False, "bad_output_shape"
+        return c, True, "ok"
+    except Exception:
+        return a, False, "kernel_exception"
+
+
+def packed_int4_symmetric_fused_qkv_m2_safe(a, q_qweight, k_qweight, v_qweight, q_scales, k_scales, v_scales,
+                                            group_size, *, config: Any | None = None,
+                                            policy: dict | None = None) -> tuple[torch.Tensor, bool, str]:
+    """Never raises; the reference's checks, order and reasons (``awq_fused_gemm.py:3592-3644``)."""
+    if not awq_decode_gemv_enabled(config=config, policy=policy):
+        return a, False, "decode_gemv_disabled"
+    if a.dim() != 2 or int(a.shape[0]) != 2:
+        return a, False, "input_not_m2_2d"
+    if int(group_size) != 32 or int(a.shape[1]) % 32 != 0:
+        return a, False, "unsupported_group_layout"
+    tensors = [q_qweight, k_qweight, q_scales, k_scales]
+    if v_qweight is not None or v_scales is not None:
+        if v_qweight is None or v_scales is None:
+            return a, False, "v_bad_shape"
+        tensors.extend([v_qweight, v_scales])
+    if any(t.dim() != 2 or t.device != a.device for t in tensors):
+        return a, False, "tensor_layout_or_device"
+    if any(int(a.shape[1]) != int(w.shape[1]) * 8 for w in tensors[:2]):
+        return a, False, "qk_k_mismatch"
+    if v_qweight is not None and int(a.shape[1]) != int(v_qweight.shape[1]) * 8:
+        return a, False, "v_k_mismatch"
+    try:
+        c = packed_int4_symmetric_fused_qkv_m2(
+            a.contiguous(), q_qweight.contiguous(), k_qweight.contiguous(),
+            v_qweight.contiguous() if v_qweight is not None else None, q_scales.contiguous(),
+            k_scales.contiguous(), v_scales.contiguous() if v_scales is not None else None, int(group_size),
+            config=config, policy=policy)
+        expected_n = (int(q_qweight.shape[0]) + int(k_qweight.shape[0])
+                      + (int(v_qweight.shape[0]) if v_qweight is not None else 0))
+        if c.shape != (2, expected_n):
             return c, False, "bad_output_shape"
         return c, True, "ok"
     except Exception:
