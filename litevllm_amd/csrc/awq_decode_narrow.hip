@@ -282,8 +282,9 @@ int launch_pack_decode_narrow(const int32_t* qweight_kn, int32_t* out, int64_t K
   return narrow_status();
 }
 
-// 16 waves per block (one block per CU) when the tiles fit the CUs once, else 8 (two per CU);
-// M == 1 stages the activation row in LDS when it fits
+// 16 waves per block (one block per CU) when the tiles fit the CUs once and the activations
+// come from LDS, else 8 (two per CU; with per-k-step activation loads 8 waves also measured
+// faster at one tile per CU); one token tile stages its activation rows in LDS when they fit
 constexpr uint32_t kNarrowLdsMax = 65536;
 
 template <int MT, bool ZP, typename T, bool SBF, bool ONE, bool XL>
@@ -291,7 +292,7 @@ static bool launch_narrow_t(const GemmArgs& a, hipStream_t st) {
   const int tiles = (int)cdiv(a.N, 16);
   const int spg = a.G / 32;
   const dim3 grid((unsigned)tiles);
-  const int nwv = tiles <= num_cus() ? 16 : 8;
+  const int nwv = (tiles <= num_cus() && XL) ? 16 : 8;
   const NarrowLds L = narrow_lds(nwv, ONE ? 1 : 16 * MT, a.K / a.G, a.K, ZP, XL ? a.M : 0);
   if (L.total > kNarrowLdsMax) return false;
 #define AWQ_NARROW_L(NWV, SPG_) \
