@@ -146,7 +146,7 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           const u32x4 v = __builtin_bit_cast(
-              u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, (int)w_lane_off, kbase + 1024 * e, 0));
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, (int)w_lane_off, kbase + 1024 * e, kStreamNT));
 #pragma unroll
           for (int c = 0; c < 4; ++c) raw[slot][4 * e + c] = v[c];
         }

@@ -157,7 +157,7 @@ moe_gemm_kernel(const MoeArgs p) {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
           const u32x4 v = __builtin_bit_cast(
-              u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, (int)((uint32_t)lane * 16u), kbase + 1024 * i, 0));
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, (int)((uint32_t)lane * 16u), kbase + 1024 * i, kStreamNT));
 #pragma unroll
           for (int c = 0; c < 4; ++c) raw[slot][4 * i + c] = v[c];
         }
