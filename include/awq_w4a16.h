@@ -30,6 +30,9 @@
  *   awq_w4a16_moe_route <- the routing of fused_moe.py:12-15 / gemma4/moe.py:106-116
  *   awq_w4a16_moe_pack_stream <- no kernel in the reference: the expert-major weight prepack the
  *                         grouped kernels read (the reference reads its [E, N, K/8] stacks directly)
+ *   awq_w4a16_rmsnorm_gemm <- rmsnorm_awq_fused_linear / rmsnorm_awq_fused_kernel
+ *                         (vllm/kernels/triton/rmsnorm_awq_fused.py:43-189)
+ *   awq_w4a16_rmsnorm  <- the RMSNorm phase of that kernel (rmsnorm_awq_fused.py:108-131)
  */
 #ifndef AWQ_W4A16_H
 #define AWQ_W4A16_H
@@ -254,6 +257,35 @@ int awq_w4a16_gate_up_act(const void* x, int64_t ldx, const int32_t* qweight, co
                           int32_t group_size, int32_t split_k, int32_t layout, int32_t activation,
                           int32_t act_dtype, int32_t scale_dtype, void* workspace, size_t workspace_bytes,
                           void* stream);
+
+/* ---- RMSNorm prologue ---------------------------------------------------------
+ * xn[M, K] (fp16) = fp16_rne((fp32(x) * rrms) * fp32(norm_w)), rrms = rsqrt(var / K + eps),
+ * var = the fp32 sum of fp32(x)^2 over the row: the arithmetic of rmsnorm_awq_fused.py:108-131
+ * (the normalised row is fp16 whatever x's dtype, rmsnorm_awq_fused.py:168).
+ *   x: [M, K] act_dtype (F16 or BF16), row stride ldx; norm_w: [K] norm_dtype (F16 or BF16);
+ *   xn: [M, K] fp16, row stride ldxn.  K % 8 == 0; x, norm_w and xn 16-byte aligned, strides
+ *   multiples of 8. */
+int awq_w4a16_rmsnorm(const void* x, int64_t ldx, const void* norm_w, float eps, void* xn, int64_t ldxn,
+                      int64_t M, int64_t K, int32_t act_dtype, int32_t norm_dtype, void* stream);
+
+/* Workspace of awq_w4a16_rmsnorm_gemm: awq_w4a16_gemm's (same zeroing rule, at offset 0, and
+ * never less than its 64 KiB counter region, so one workspace can serve both functions), then
+ * the normalised rows [M, K] fp16, then for BF16 activations the fp16 product [M, N]; each
+ * part starts on a 256-byte boundary and the workspace itself on one. */
+size_t awq_w4a16_rmsnorm_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_size,
+                                              int32_t split_k, int32_t layout, int32_t act_dtype);
+
+/* C[M, N] = RMSNorm(x; norm_w, eps) . dequant(W)^T, rmsnorm_awq_fused_linear's result:
+ * awq_w4a16_rmsnorm into the workspace, then awq_w4a16_gemm on the fp16 rows (any layout it
+ * takes, no bias), C rounded to fp16; for BF16 activations that fp16 result is converted to
+ * bf16 (round to nearest even), as the reference's store into a bf16 output does
+ * (rmsnorm_awq_fused.py:170-175).  C: [M, N] act_dtype, row stride ldc.  Three launches at
+ * most, all on `stream`. */
+int awq_w4a16_rmsnorm_gemm(const void* x, int64_t ldx, const void* norm_w, float eps,
+                           const int32_t* qweight, const void* scales, const int32_t* qzeros, void* c,
+                           int64_t ldc, int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t split_k,
+                           int32_t layout, int32_t act_dtype, int32_t norm_dtype, int32_t scale_dtype,
+                           void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -33,6 +33,7 @@ from .moe import (  # noqa: F401
     gemma4_moe_int4_prefill_grouped_fused,
     moe_route,
 )
+from .rmsnorm_awq_fused import rmsnorm_awq_fused_linear  # noqa: F401
 from .tensor import AWQWeight, PackedInt4Weight  # noqa: F401
 
 __version__ = "0.1.0"

@@ -62,6 +62,12 @@ SIGNATURES = {
     "awq_w4a16_gate_up_act": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64,
                                              _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_p,
                                              _c_sz, _c_p]),
+    "awq_w4a16_rmsnorm": (ctypes.c_int, [_c_p, _c_i64, _c_p, ctypes.c_float, _c_p, _c_i64, _c_i64, _c_i64,
+                                         _c_i32, _c_i32, _c_p]),
+    "awq_w4a16_rmsnorm_gemm_workspace_bytes": (_c_sz, [_c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32]),
+    "awq_w4a16_rmsnorm_gemm": (ctypes.c_int, [_c_p, _c_i64, _c_p, ctypes.c_float, _c_p, _c_p, _c_p, _c_p,
+                                              _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32,
+                                              _c_i32, _c_i32, _c_p, _c_sz, _c_p]),
 }
 
 MOE_ACT_SILU = 0

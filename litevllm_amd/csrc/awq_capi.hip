@@ -347,4 +347,63 @@ int awq_w4a16_gate_up_act(const void* x, int64_t ldx, const int32_t* qweight, co
   return launch_status();
 }
 
+int awq_w4a16_rmsnorm(const void* x, int64_t ldx, const void* norm_w, float eps, void* xn, int64_t ldxn,
+                      int64_t M, int64_t K, int32_t act_dtype, int32_t norm_dtype, void* stream) {
+  if (M < 0 || K <= 0 || (K % 8) != 0) return AWQ_ERR_SHAPE;
+  if (M == 0) return AWQ_OK;
+  if (!x || !norm_w || !xn) return AWQ_ERR_NULL;
+  if (!dtype_16(act_dtype) || !dtype_16(norm_dtype)) return AWQ_ERR_UNSUPPORTED;
+  if (K > 0x7FFFFFFFLL) return AWQ_ERR_UNSUPPORTED;
+  if (ldx < K || ldxn < K || (ldx % 8) != 0 || (ldxn % 8) != 0) return AWQ_ERR_STRIDE;
+  if ((((uintptr_t)x) & 15) || (((uintptr_t)norm_w) & 15) || (((uintptr_t)xn) & 15)) return AWQ_ERR_STRIDE;
+  return launch_rmsnorm_rows(x, ldx, norm_w, eps, xn, ldxn, M, K, act_dtype, norm_dtype, (hipStream_t)stream);
+}
+
+static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+size_t awq_w4a16_rmsnorm_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_size,
+                                              int32_t split_k, int32_t layout, int32_t act_dtype) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  // the GEMM's part is never smaller than the counter region, so a workspace shared with
+  // awq_w4a16_gemm keeps its counters zero
+  const size_t g = align256(std::max(awq_w4a16_gemm_workspace_bytes(M, N, K, group_size, split_k, layout),
+                                     (size_t)kCounterBytes));
+  const size_t xn = align256((size_t)M * (size_t)K * 2);
+  const size_t c16 = act_dtype == AWQ_DTYPE_BF16 ? align256((size_t)M * (size_t)N * 2) : 0;
+  return g + xn + c16;
+}
+
+int awq_w4a16_rmsnorm_gemm(const void* x, int64_t ldx, const void* norm_w, float eps,
+                           const int32_t* qweight, const void* scales, const int32_t* qzeros, void* c,
+                           int64_t ldc, int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t split_k,
+                           int32_t layout, int32_t act_dtype, int32_t norm_dtype, int32_t scale_dtype,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+  if (M < 0 || N < 0 || K <= 0 || group_size <= 0 || split_k < 0) return AWQ_ERR_SHAPE;
+  if (M == 0 || N == 0) return AWQ_OK;
+  if (!x || !norm_w || !qweight || !scales || !c) return AWQ_ERR_NULL;
+  if (!workspace) return AWQ_ERR_WORKSPACE;
+  if (!dtype_16(act_dtype) || !dtype_16(norm_dtype) || !dtype_16(scale_dtype)) return AWQ_ERR_UNSUPPORTED;
+  if ((N % 8) != 0 || (K % 8) != 0 || (group_size % 32) != 0 || (K % group_size) != 0) return AWQ_ERR_SHAPE;
+  if (layout != AWQ_LAYOUT_AUTOAWQ && layout != AWQ_LAYOUT_KN_SEQ && layout != AWQ_LAYOUT_DECODE_STREAM &&
+      layout != AWQ_LAYOUT_DECODE_NARROW)
+    return AWQ_ERR_UNSUPPORTED;
+  if (ldx < K || (ldx % 8) != 0 || (((uintptr_t)x) & 15)) return AWQ_ERR_STRIDE;
+  if (ldc < N || (ldc % 8) != 0 || (((uintptr_t)c) & 15)) return AWQ_ERR_STRIDE;
+  const size_t gws = awq_w4a16_gemm_workspace_bytes(M, N, K, group_size, split_k, layout);
+  if (workspace_bytes < awq_w4a16_rmsnorm_gemm_workspace_bytes(M, N, K, group_size, split_k, layout, act_dtype))
+    return AWQ_ERR_WORKSPACE;
+  if ((((uintptr_t)workspace) & 255)) return AWQ_ERR_STRIDE;
+  char* xn = (char*)workspace + align256(std::max(gws, (size_t)kCounterBytes));
+  char* c16 = xn + align256((size_t)M * (size_t)K * 2);
+  const bool bf = act_dtype == AWQ_DTYPE_BF16;
+  if (bf && M > 65535) return AWQ_ERR_UNSUPPORTED;  // rows of the conversion grid
+  int rc = awq_w4a16_rmsnorm(x, ldx, norm_w, eps, xn, K, M, K, act_dtype, norm_dtype, stream);
+  if (rc != AWQ_OK) return rc;
+  rc = awq_w4a16_gemm(xn, K, qweight, scales, qzeros, nullptr, bf ? (void*)c16 : c, bf ? N : ldc, M, N, K,
+                      group_size, split_k, layout, AWQ_DTYPE_F16, scale_dtype, AWQ_DTYPE_NONE,
+                      gws ? workspace : nullptr, gws, stream);
+  if (rc != AWQ_OK || !bf) return rc;
+  return launch_f16_to_bf16(c16, N, c, ldc, M, N, (hipStream_t)stream);
+}
+
 }  // extern "C"

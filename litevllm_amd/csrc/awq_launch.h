@@ -70,6 +70,11 @@ int launch_repack_nk_to_autoawq(const int32_t* qweight_nk, const int32_t* qzeros
 int launch_gate_up_interleave(const void* gate, const void* up, void* out, int64_t rows, int64_t cols,
                               int elem_bytes, int64_t half, hipStream_t st);
 
+// RMSNorm prologue (one block per row, normalised fp16 rows out) and fp16 -> bf16 conversion.
+int launch_rmsnorm_rows(const void* x, int64_t ldx, const void* nw, float eps, void* xn, int64_t ldo, int64_t M,
+                        int64_t K, int act, int ndt, hipStream_t st);
+int launch_f16_to_bf16(const void* in, int64_t ldi, void* out, int64_t ldo, int64_t M, int64_t N, hipStream_t st);
+
 // ---- mixture of experts ----
 // Stream-packed expert stacks: gate_up (N = 2I) pairs 8 gate words with the 8 up words of the
 // same columns per tile (tiles = ceil(I / 64)); down (gate_up = 0) uses tiles of 16 words.

@@ -250,6 +250,25 @@ def _narrow_fits(M: int, N: int, K: int, split_k: int) -> bool:
     return M <= 16 and tiles <= L.num_cus() and K <= 4096
 
 
+def _kernel_weight(qweight, scales, qzeros, group_size, layout, M, N, K, split_k, decode_stream, decode_layout):
+    """The weight copy and layout code the kernels read for this call: a reference-layout
+    weight is repacked to AutoAWQ once (cached); decode-shaped calls take the cached narrow or
+    stream copy (see ``gemm``)."""
+    if layout == "ref":
+        qweight, scales, qzeros = REPACK_CACHE.get(qweight, scales, qzeros, args=(int(group_size),))
+        layout = "autoawq"
+    qweight, scales = qweight.contiguous(), scales.contiguous()
+    qzeros = qzeros.contiguous() if qzeros is not None else None
+    lc = layout_code(layout)
+    if decode_layout not in (None, "narrow", "stream"):
+        raise ValueError(f"unknown decode_layout {decode_layout!r}")
+    if _use_decode_stream(M, K, group_size, None, scales, layout, decode_stream):
+        narrow = decode_layout == "narrow" or (decode_layout is None and _narrow_fits(M, N, K, int(split_k)))
+        qweight = (NARROW_CACHE if narrow else STREAM_CACHE).get(qweight)
+        lc = L.LAYOUT_DECODE_NARROW if narrow else L.LAYOUT_DECODE_STREAM
+    return qweight, scales, qzeros, lc
+
+
 def gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, qzeros: torch.Tensor | None,
          group_size: int, bias: torch.Tensor | None = None, split_k: int = 0,
          layout: str = "ref", out: torch.Tensor | None = None,
@@ -270,25 +289,15 @@ def gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, qzeros: t
     M = int(a.shape[0])
     if int(a.shape[1]) != K:
         raise ValueError(f"K mismatch: a has {a.shape[1]}, weight has {K}")
-    if layout == "ref":
-        qweight, scales, qzeros = REPACK_CACHE.get(qweight, scales, qzeros, args=(int(group_size),))
-        layout = "autoawq"
+    qweight, scales, qzeros, lc = _kernel_weight(qweight, scales, qzeros, group_size, layout, M, N, K,
+                                                 split_k, decode_stream, decode_layout)
     a = a.contiguous()
-    qweight, scales = qweight.contiguous(), scales.contiguous()
-    qzeros = qzeros.contiguous() if qzeros is not None else None
     if out is None:
         out = torch.empty((M, N), dtype=a.dtype, device=a.device)
     if bias is not None:
         bias = bias.contiguous()
     dev = a.device
     stream = _stream_ptr(dev)
-    lc = layout_code(layout)
-    if _use_decode_stream(M, K, group_size, a, scales, layout, decode_stream):
-        narrow = decode_layout == "narrow" or (decode_layout is None and _narrow_fits(M, N, K, int(split_k)))
-        if decode_layout not in (None, "narrow", "stream"):
-            raise ValueError(f"unknown decode_layout {decode_layout!r}")
-        qweight = (NARROW_CACHE if narrow else STREAM_CACHE).get(qweight)
-        lc = L.LAYOUT_DECODE_NARROW if narrow else L.LAYOUT_DECODE_STREAM
     ws_bytes = int(lib.awq_w4a16_gemm_workspace_bytes(M, N, K, int(group_size), int(split_k), lc))
     ws = WORKSPACE.get(dev, ws_bytes) if ws_bytes else None
     rc = lib.awq_w4a16_gemm(
@@ -297,6 +306,55 @@ def gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, qzeros: t
         dtype_code(scales.dtype), dtype_code(bias.dtype) if bias is not None else L.DTYPE_NONE,
         _ptr(ws), ws_bytes if ws is not None else 0, stream)
     L.check("awq_w4a16_gemm", rc)
+    return out
+
+
+# ------------------------------------------------------------------ RMSNorm prologue
+def rmsnorm(x: torch.Tensor, norm_w: torch.Tensor, eps: float = 1e-6, out: torch.Tensor | None = None) -> torch.Tensor:
+    """The normalised rows ``fp16((x * rsqrt(mean(x^2) + eps)) * norm_w)`` the fused RMSNorm +
+    GEMM feeds its GEMM (fp32 arithmetic, one rounding; fp16 whatever ``x``'s dtype)."""
+    lib = L.load()
+    if x.dim() != 2 or norm_w.dim() != 1 or int(norm_w.shape[0]) != int(x.shape[1]):
+        raise ValueError("x must be [M, K] and norm_w [K]")
+    dev = _require_device(x, norm_w, out)
+    M, K = int(x.shape[0]), int(x.shape[1])
+    x, norm_w = x.contiguous(), norm_w.contiguous()
+    if out is None:
+        out = torch.empty((M, K), dtype=torch.float16, device=dev)
+    rc = lib.awq_w4a16_rmsnorm(_ptr(x), K, _ptr(norm_w), float(eps), _ptr(out), int(out.stride(0)), M, K,
+                               dtype_code(x.dtype), dtype_code(norm_w.dtype), _stream_ptr(dev))
+    L.check("awq_w4a16_rmsnorm", rc)
+    return out
+
+
+def rmsnorm_gemm(x: torch.Tensor, norm_w: torch.Tensor, eps: float, qweight: torch.Tensor,
+                 scales: torch.Tensor, qzeros: torch.Tensor | None, group_size: int, layout: str = "ref",
+                 split_k: int = 0, out: torch.Tensor | None = None, decode_stream: bool | None = None,
+                 decode_layout: str | None = None) -> torch.Tensor:
+    """``out[M, N] = rmsnorm(x, norm_w, eps) @ dequant(W)^T`` through ``awq_w4a16_rmsnorm_gemm``:
+    the normalised fp16 rows, the GEMM on them (same kernels and weight copies as ``gemm``),
+    the fp16 result, converted to bf16 for bf16 ``x``."""
+    lib = L.load()
+    if x.dim() != 2 or norm_w.dim() != 1:
+        raise ValueError("x must be [M, K] and norm_w [K]")
+    dev = _require_device(x, norm_w, qweight, scales, qzeros, out)
+    K, N = gemm_dims(qweight, layout)
+    M = int(x.shape[0])
+    if int(x.shape[1]) != K or int(norm_w.shape[0]) != K:
+        raise ValueError(f"K mismatch: x has {x.shape[1]}, norm_w {norm_w.shape[0]}, weight {K}")
+    qweight, scales, qzeros, lc = _kernel_weight(qweight, scales, qzeros, group_size, layout, M, N, K,
+                                                 split_k, decode_stream, decode_layout)
+    x, norm_w = x.contiguous(), norm_w.contiguous()
+    if out is None:
+        out = torch.empty((M, N), dtype=x.dtype, device=dev)
+    ws_bytes = int(lib.awq_w4a16_rmsnorm_gemm_workspace_bytes(M, N, K, int(group_size), int(split_k), lc,
+                                                              dtype_code(x.dtype)))
+    ws = WORKSPACE.get(dev, ws_bytes)
+    rc = lib.awq_w4a16_rmsnorm_gemm(
+        _ptr(x), K, _ptr(norm_w), float(eps), _ptr(qweight), _ptr(scales), _ptr(qzeros), _ptr(out),
+        int(out.stride(0)), M, N, K, int(group_size), int(split_k), lc, dtype_code(x.dtype),
+        dtype_code(norm_w.dtype), dtype_code(scales.dtype), _ptr(ws), ws_bytes, _stream_ptr(dev))
+    L.check("awq_w4a16_rmsnorm_gemm", rc)
     return out
 
 

@@ -295,3 +295,44 @@ def moe_grouped_exact(x_f16, topk_weights, topk_ids, w1, w2, activation="silu", 
         np.add.at(out, ts, h @ w2[e].astype(np.float64).T)
     return out
 
+
+
+def rmsnorm_rows(x, norm_w, eps):
+    """The RMSNorm phase of the fused RMSNorm + int4 GEMM in float32, returned as fp16:
+    ``var = sum(fp32(x)^2)``, ``rrms = rsqrt(var / K + eps)``,
+    ``xn = fp16((fp32(x) * rrms) * fp32(norm_w))`` -- ``vllm/kernels/triton/
+    rmsnorm_awq_fused.py:108-131`` (fp32 ``var`` and ``rrms``, two fp32 products, the cast to
+    fp16 at ``:168`` whatever the input dtype).  ``x`` holds the fp16 or bf16 values (any float
+    dtype), ``norm_w`` likewise.  ``var`` is the float32 rounding of the exact sum (the
+    reference adds 32-element ``tl.sum`` chunks in fp32; that order is not part of the
+    contract) and ``rsqrt`` is correctly rounded.
+
+    Pinned by: ``torch.nn.functional.rms_norm`` in float32 (to one fp16 ulp), the constant-row
+    case (``xn = sign(x)`` exactly for unit weights), bit-exact invariance under power-of-two
+    scaling of a row when ``eps = 0``, and a wrong-formula check (``sum`` in place of the mean
+    fails).
+    """
+    x32 = np.asarray(x, dtype=np.float32)
+    nw = np.asarray(norm_w, dtype=np.float32)
+    k = x32.shape[1]
+    var = np.sum(x32.astype(np.float64) ** 2, axis=1).astype(np.float32)
+    v = var / np.float32(k) + np.float32(eps)
+    rrms = (1.0 / np.sqrt(v.astype(np.float64))).astype(np.float32)
+    t = (x32 * rrms[:, None]).astype(np.float32)
+    return (t * nw[None, :]).astype(np.float32).astype(np.float16)
+
+
+def rmsnorm_awq_linear(x, norm_w, eps, qweight, scales, qzeros, group_size, weights="float16"):
+    """``rmsnorm_awq_fused_linear`` (``rmsnorm_awq_fused.py:43-189``) in float64, unrounded:
+    :func:`rmsnorm_rows`, then the reference-layout weights ``(q - z) * s`` (rounded to fp16
+    at ``:166-167`` for ``weights="float16"``; ``"float32"`` keeps the unrounded product the
+    decode kernels use), then the exact dot products.  The caller rounds to fp16 (``:177``)
+    and, for bf16 inputs, fp16 -> bf16 (the store into ``c``).
+
+    Pinned by: the unit-RMS special case (rows of +-1, unit weights, ``eps = 0``: the
+    normalised rows equal ``x`` and the result reduces to :func:`linear_exact` of the pinned
+    :func:`dequant_ref`) and :func:`rmsnorm_rows`' own checks.
+    """
+    xn = rmsnorm_rows(x, norm_w, eps)
+    w = dequant_ref(qweight, scales, qzeros, group_size, out_dtype=weights)
+    return linear_exact(xn, w)

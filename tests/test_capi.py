@@ -164,3 +164,39 @@ def test_decode_layout_choice():
     assert not ops._narrow_fits(1, 4096, 4096, 2)          # an explicit split asks for the stream kernel
     assert ops._narrow_fits(4, 16 * cus, 4096, 0) and not ops._narrow_fits(4, 16 * cus, 8192, 0)
     assert not ops._narrow_fits(16, 16 * cus + 16, 4096, 0) and not ops._narrow_fits(17, 4096, 4096, 0)
+
+
+def _rn_gemm(lib, **kw):
+    p = _fake(4096)
+    return lib.awq_w4a16_rmsnorm_gemm(
+        kw.get("x", p), kw.get("ldx", 64), kw.get("nw", p), 1e-6, kw.get("qw", p), kw.get("sc", p), None,
+        kw.get("c", p), kw.get("ldc", 64), kw.get("M", 1), kw.get("N", 64), kw.get("K", 64), kw.get("G", 32), 0,
+        kw.get("layout", 0), kw.get("act", L.DTYPE_F16), kw.get("ndt", L.DTYPE_F16), L.DTYPE_F16,
+        kw.get("ws", p), kw.get("ws_bytes", 0), None)
+
+
+def test_rmsnorm_rejects_bad_args_before_any_launch(lib):
+    p = _fake()
+    f = lib.awq_w4a16_rmsnorm
+    assert f(p, 64, p, 1e-6, p, 64, 1, 60, L.DTYPE_F16, L.DTYPE_F16, None) == L.ERR_SHAPE  # K % 8
+    assert f(p, 64, p, 1e-6, p, 64, -1, 64, L.DTYPE_F16, L.DTYPE_F16, None) == L.ERR_SHAPE
+    assert f(p, 64, p, 1e-6, p, 64, 0, 64, L.DTYPE_F16, L.DTYPE_F16, None) == L.OK
+    assert f(None, 64, p, 1e-6, p, 64, 1, 64, L.DTYPE_F16, L.DTYPE_F16, None) == L.ERR_NULL
+    assert f(p, 64, p, 1e-6, p, 64, 1, 64, L.DTYPE_F32, L.DTYPE_F16, None) == L.ERR_UNSUPPORTED
+    assert f(p, 32, p, 1e-6, p, 64, 1, 64, L.DTYPE_F16, L.DTYPE_F16, None) == L.ERR_STRIDE
+    assert _rn_gemm(lib, x=None) == L.ERR_NULL
+    assert _rn_gemm(lib, ws=None) == L.ERR_WORKSPACE
+    assert _rn_gemm(lib, N=60) == L.ERR_SHAPE
+    assert _rn_gemm(lib, G=48) == L.ERR_SHAPE
+    assert _rn_gemm(lib, layout=9) == L.ERR_UNSUPPORTED
+    assert _rn_gemm(lib, ndt=L.DTYPE_F32) == L.ERR_UNSUPPORTED
+    assert _rn_gemm(lib, M=0) == L.OK
+
+
+def test_rmsnorm_gemm_workspace_is_host_only(lib):
+    g = lib.awq_w4a16_gemm_workspace_bytes(1, 4096, 12288, 128, 8, 0)
+    w16 = lib.awq_w4a16_rmsnorm_gemm_workspace_bytes(1, 4096, 12288, 128, 8, 0, L.DTYPE_F16)
+    wbf = lib.awq_w4a16_rmsnorm_gemm_workspace_bytes(1, 4096, 12288, 128, 8, 0, L.DTYPE_BF16)
+    assert w16 >= g + 12288 * 2 and wbf >= w16 + 4096 * 2
+    # no GEMM workspace (prefill): the counter region is still kept clear
+    assert lib.awq_w4a16_rmsnorm_gemm_workspace_bytes(64, 4096, 4096, 128, 0, 0, L.DTYPE_F16) == 65536 + 64 * 4096 * 2

@@ -347,3 +347,53 @@ def test_moe_grouped_exact_single_expert_is_a_dense_mlp():
     gu = O.linear_exact(x.numpy(), w1.numpy()[0])
     h = (torch.nn.functional.silu(torch.from_numpy(gu[:, :I])).numpy() * gu[:, I:]).astype(np.float16)
     assert np.allclose(y, O.linear_exact(h, w2.numpy()[0]), rtol=1e-12, atol=1e-12)
+
+
+# ---------------------------------------------------------------- RMSNorm prologue oracle
+@pytest.mark.parametrize("K", [8, 128, 4096])
+def test_rmsnorm_rows_matches_torch_rms_norm(K):
+    g = torch.Generator().manual_seed(K)
+    x = (torch.randn(6, K, generator=g) * 3).to(torch.float16)
+    nw = (1 + 0.5 * torch.randn(K, generator=g)).to(torch.float16)
+    want = torch.nn.functional.rms_norm(x.float(), (K,), weight=nw.float(), eps=1e-6).to(torch.float16)
+    got = O.rmsnorm_rows(x.numpy(), nw.numpy(), 1e-6)
+    diff = np.abs(got.astype(np.float64) - want.numpy().astype(np.float64))
+    ulp = O.fp16_ulp(want.numpy().astype(np.float64), floor=2.0 ** -14)
+    assert (diff / ulp).max() <= 1.0
+    assert (diff == 0).mean() > 0.97
+    # a plausible mistake, the sum of squares in place of the mean, is far off
+    xd = x.double().numpy()
+    wrong = xd / np.sqrt((xd ** 2).sum(1, keepdims=True)) * nw.double().numpy()
+    assert np.abs(got.astype(np.float64) - wrong).max() > 0.1
+
+
+def test_rmsnorm_rows_special_cases():
+    K = 256
+    row = np.full((1, K), 3.0, dtype=np.float16)
+    assert np.array_equal(O.rmsnorm_rows(row, np.ones(K), 0.0), np.ones((1, K), np.float16))
+    assert np.array_equal(O.rmsnorm_rows(-row, np.ones(K), 0.0), -np.ones((1, K), np.float16))
+    # eps enters: a row of zeros normalises to zeros, a tiny row is damped
+    assert np.array_equal(O.rmsnorm_rows(np.zeros((1, K), np.float16), np.ones(K), 1e-6), np.zeros((1, K), np.float16))
+    tiny = np.full((1, K), 2.0 ** -10, dtype=np.float16)
+    assert O.rmsnorm_rows(tiny, np.ones(K), 1e-2).max() < 0.05
+    # power-of-two scaling of a row leaves the result unchanged, bit for bit (eps = 0)
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((4, K)).astype(np.float16)
+    nw = rng.uniform(0.5, 1.5, K).astype(np.float16)
+    base = O.rmsnorm_rows(x, nw, 0.0)
+    for j in (-4, 3):
+        assert np.array_equal(O.rmsnorm_rows((x.astype(np.float32) * 2.0 ** j).astype(np.float16), nw, 0.0), base)
+
+
+def test_rmsnorm_awq_linear_unit_rms_reduces_to_linear():
+    N, K, G = 24, 256, 32
+    rng = np.random.default_rng(5)
+    x = np.where(rng.random((3, K)) < 0.5, -1.0, 1.0).astype(np.float16)
+    qw = O.pack_ref(rng.integers(0, 16, (N, K)))
+    qz = O.pack_ref(rng.integers(0, 16, (N, K // G)))
+    sc = rng.uniform(0.001, 0.02, (N, K // G)).astype(np.float16)
+    got = O.rmsnorm_awq_linear(x, np.ones(K, np.float16), 0.0, qw, sc, qz, G)
+    want = O.linear_exact(x, O.dequant_ref(qw, sc, qz, G))
+    assert np.array_equal(got, want)
+    # the normalisation is not skipped: doubling x leaves the result unchanged
+    assert np.array_equal(O.rmsnorm_awq_linear(2 * x, np.ones(K, np.float16), 0.0, qw, sc, qz, G), want)
