@@ -173,6 +173,37 @@ def _bench_moe(torch, ops, dev, T, copies=3):
             "mfma_frac": round(tfl / MFMA_F16_PEAK_TFLOPS, 4)}
 
 
+def _bench_rmsnorm(torch, ops, dev, copies=24):
+    """rmsnorm_awq_fused_linear's device path (norm prologue + GEMM, fp16) against the GEMM
+    alone on the same rotated weights (24 x 12.6 MB, beyond the MALL), graph-replayed."""
+    K, N = K_DEC, 6144
+    W = _weights(torch, K, N, copies, dev, 31)
+    gen = torch.Generator(device=dev).manual_seed(32)
+    nw = (1 + 0.1 * torch.randn(K, device=dev, generator=gen)).half()
+    out = []
+    for M in (1, 16, 2048):
+        x = torch.randn((M, K), device=dev, generator=gen).half()
+        y = torch.empty((M, N), device=dev, dtype=torch.float16)
+        ws = W if M <= 32 else W[:3]
+
+        def fused():
+            for qw, qz, sc in ws:
+                ops.rmsnorm_gemm(x, nw, 1e-6, qw, sc, qz, G, layout="autoawq", out=y)
+
+        def plain():
+            for qw, qz, sc in ws:
+                ops.gemm(x, qw, sc, qz, G, layout="autoawq", out=y)
+        ms_f, g = _time_graph(torch, fused, 10)
+        del g
+        ms_p, g = _time_graph(torch, plain, 10)
+        del g
+        us_f, us_p = ms_f * 1e3 / len(ws), ms_p * 1e3 / len(ws)
+        out.append({"M": M, "K": K, "N": N, "us_fused": round(us_f, 2), "us_gemm_only": round(us_p, 2),
+                    "GBps_fused": round(alg_bytes(M, K, N) / (us_f * 1e-6) / 1e9, 1)})
+    del W
+    return out
+
+
 def _traffic():
     """HBM bytes per launch of the roofline kernel from the committed rocprofv3 PMC summary
     (FETCH_SIZE + WRITE_SIZE, each scaled by the copy-kernel calibration), or None."""
@@ -192,6 +223,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-moe", action="store_true")
+    ap.add_argument("--no-rmsnorm", action="store_true")
     ap.add_argument("--only", default="", help="profile mode: 'decode-m1n24576', 'prefill' or "
                     "'copy-64MiB' (counter calibration) launches only")
     args = ap.parse_args()
@@ -320,6 +352,11 @@ def main():
     if not args.no_moe:
         moe = {T: _bench_moe(torch, ops, dev, T) for T in (16, 512)}
 
+    # ---- fused RMSNorm + GEMM (the QKV projection after the input norm, K=4096, N=6144) ----
+    rms = None
+    if not args.no_rmsnorm:
+        rms = _bench_rmsnorm(torch, ops, dev)
+
     line = {
         "metric": "AWQ W4A16 decode GEMV sweep throughput (algorithmic GB/s, M=1-16)",
         "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": steps_timed,
@@ -333,6 +370,7 @@ def main():
         "per_shape": per_shape,
         "prefill": prefill,
         "moe": moe,
+        "rmsnorm_fused": rms,
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()

@@ -280,7 +280,8 @@ size_t awq_w4a16_rmsnorm_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, i
  * takes, no bias), C rounded to fp16; for BF16 activations that fp16 result is converted to
  * bf16 (round to nearest even), as the reference's store into a bf16 output does
  * (rmsnorm_awq_fused.py:170-175).  C: [M, N] act_dtype, row stride ldc.  Three launches at
- * most, all on `stream`. */
+ * most, all on `stream`; one for the DECODE_NARROW layout with F16 activations and scales and
+ * M = 1, whose kernel normalises the row it stages (when the row fits its LDS). */
 int awq_w4a16_rmsnorm_gemm(const void* x, int64_t ldx, const void* norm_w, float eps,
                            const int32_t* qweight, const void* scales, const int32_t* qzeros, void* c,
                            int64_t ldc, int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t split_k,

@@ -393,6 +393,29 @@ int awq_w4a16_rmsnorm_gemm(const void* x, int64_t ldx, const void* norm_w, float
   if (workspace_bytes < awq_w4a16_rmsnorm_gemm_workspace_bytes(M, N, K, group_size, split_k, layout, act_dtype))
     return AWQ_ERR_WORKSPACE;
   if ((((uintptr_t)workspace) & 255)) return AWQ_ERR_STRIDE;
+  if (layout == AWQ_LAYOUT_DECODE_NARROW && act_dtype == AWQ_DTYPE_F16 && scale_dtype == AWQ_DTYPE_F16 && M == 1 &&
+      decode_covers(M, group_size) && (K % 32) == 0 && decode_narrow_bytes(K, N) <= 0x7FFFFFFFLL &&
+      M * ldx * 2 <= 0x7FFFFFFFLL && !(((uintptr_t)qweight) & 15) && !(((uintptr_t)scales) & 15) &&
+      !(((uintptr_t)norm_w) & 15)) {
+    // one launch: the narrow kernel normalises its staged rows itself
+    GemmArgs ga{};
+    ga.a = (const uint16_t*)x;
+    ga.qw = (const uint32_t*)qweight;
+    ga.sc = (const uint16_t*)scales;
+    ga.qz = (const uint32_t*)qzeros;
+    ga.c = (uint16_t*)c;
+    ga.lda = ldx;
+    ga.ldc = ldc;
+    ga.M = (int)M;
+    ga.N = (int)N;
+    ga.K = (int)K;
+    ga.G = group_size;
+    ga.bias_dtype = AWQ_DTYPE_NONE;
+    ga.norm_w = (const uint16_t*)norm_w;
+    ga.eps = eps;
+    ga.norm_bf16 = norm_dtype == AWQ_DTYPE_BF16;
+    if (launch_decode_narrow_norm(ga, qzeros != nullptr, (hipStream_t)stream)) return launch_status();
+  }
   char* xn = (char*)workspace + align256(std::max(gws, (size_t)kCounterBytes));
   char* c16 = xn + align256((size_t)M * (size_t)K * 2);
   const bool bf = act_dtype == AWQ_DTYPE_BF16;

@@ -150,6 +150,45 @@ __device__ __forceinline__ float gated_act(float g, int kind) {
 }
 
 // Shared argument block of the GEMM kernels.
+// The fp32 value as computed (rounded to fp32): the empty asm keeps the compiler from fusing
+// the operation that produced it into a following fp16 conversion (a multiply and the
+// conversion become one mixed-precision FMA that rounds once, not twice).
+__device__ __forceinline__ float fp32_rounded(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// Sum of an fp64 value over the 64 lanes of a wave, returned in every lane: DPP steps within
+// quads, half rows, rows, then the row broadcasts (both 32-bit halves moved together), and
+// lane 63's total read out.  Lanes disabled by a step's row mask add zero.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, ROWS, 0xF, false);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, ROWS, 0xF, false);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ double wave_sum_f64(double v) {
+  v += dpp_f64<0xB1, 0xF>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp_f64<0x4E, 0xF>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp_f64<0x141, 0xF>(v);  // row_half_mirror
+  v += dpp_f64<0x140, 0xF>(v);  // row_mirror
+  v += dpp_f64<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+  v += dpp_f64<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, 63);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), 63);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// 1 / sqrt(var / K + eps) of the RMSNorm prologue: var / K + eps in fp32 as the reference
+// computes it (rmsnorm_awq_fused.py:118), the reciprocal square root correctly rounded (fp64
+// square root and division, rounded once to fp32).
+__device__ __forceinline__ float rms_scale(float var, int K, float eps) {
+  const float v = var / (float)K + eps;
+  return (float)(1.0 / sqrt((double)v));
+}
+
 struct GemmArgs {
   const uint16_t* a;
   const uint32_t* qw;
@@ -166,6 +205,11 @@ struct GemmArgs {
   // then holds 64 gate columns and the 64 up columns of the same outputs, and output column
   // 64 t + j (j < 64, below n_out) is act(gate) * up of tile t's columns j and 64 + j.
   int gate_act, n_out;
+  // narrow decode kernel only: non-NULL = normalise the staged activation rows first
+  // (RMSNorm prologue, fp16 rows; norm_w [K] fp16, or bf16 when norm_bf16)
+  const uint16_t* norm_w;
+  float eps;
+  int norm_bf16;
 };
 
 // Work decomposition of the decode kernel: tiles x ksteps units; each tile's k-steps are cut

@@ -22,9 +22,9 @@
 namespace awq {
 
 // LDS of one block (bytes): the waves' sums [NWV][MROWS][16] fp32, then the tile's scales
-// [groups][16] (2 B each), zero words [groups][2], and with XL the activation row [K] (2 B).
-// Each region spans whole DMA instructions (a 64-lane DMA writes all 64 lanes' slots, those
-// past the data as zeros), so no instruction reaches into the next region.
+// [groups][16] (2 B each), zero words [groups][2], and with XL the activation rows [xrows][K]
+// (2 B).  Each region spans whole DMA instructions (a 64-lane DMA writes all 64 lanes' slots,
+// those past the data as zeros), so no instruction reaches into the next region.
 struct NarrowLds {
   uint32_t sc, zw, x, total;
 };
@@ -38,14 +38,120 @@ __host__ __device__ inline NarrowLds narrow_lds(int nwv, int mrows, int ngroups,
   return l;
 }
 
+// RMSNorm prologue (rmsnorm_awq_fused.py:108-131), for XL with fp16 rows, M <= 4: the rows
+// arrive in registers instead of by DMA -- lane tid holds 16-byte column pieces pc = tid,
+// tid + NT, .. (at most kNormCols(MR) of them) of every row, with the matching 16 bytes of the
+// norm weights, read once for all rows.  Per row the sum of squares (exact squares added in
+// fp64: lanes by DPP, then the waves through `red`) is rounded once to fp32, rrms =
+// rsqrt(var / K + eps) correctly rounded, and each element is written to the staged rows in
+// LDS as fp16((x * rrms) * norm_w).
+__host__ __device__ constexpr int kNormCols(int mr) { return mr == 1 ? 6 : 1; }
+
+template <int NT, int MR>
+struct NormPieces {
+  static constexpr int PC = kNormCols(MR);
+  u32x4 x[PC][MR], g[PC];
+
+  __device__ __forceinline__ void load(const GemmArgs& p, int tid) {
+    const int kp = p.K >> 3;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.a, (uint32_t)((uint64_t)p.M * (uint64_t)p.lda * 2u));
+    const __amdgpu_buffer_rsrc_t gr = make_rsrc(p.norm_w, (uint32_t)p.K * 2u);
+#pragma unroll
+    for (int u = 0; u < PC; ++u) {
+      if (u * NT < kp) {  // block-uniform
+        const int pc = tid + u * NT;
+        const bool ok = pc < kp;  // past the row, and rows past M: the loads read zeros
+        g[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                   gr, ok ? (int)(16u * (uint32_t)pc) : (int)0x80000000, 0, 0));
+#pragma unroll
+        for (int r = 0; r < MR; ++r)
+          x[u][r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                        xr, ok && r < p.M ? (int)(((uint32_t)r * (uint32_t)p.lda + 8u * (uint32_t)pc) * 2u) : (int)0x80000000,
+                        0, 0));
+      }
+    }
+  }
+
+  // after the loads have landed: the rows' sums, then (one barrier) the normalised pieces
+  __device__ __forceinline__ void normalise(const GemmArgs& p, uint16_t* xs, float* red, int wave, int lane, int tid) {
+    const int kp = p.K >> 3;
+    double ss[MR];
+#pragma unroll
+    for (int r = 0; r < MR; ++r) ss[r] = 0.0;
+#pragma unroll
+    for (int u = 0; u < PC; ++u) {
+      if (u * NT < kp) {
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+          double s0 = 0.0, s1 = 0.0;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const double lo = h_bits2f((uint16_t)(x[u][r][j] & 0xFFFF)), hi = h_bits2f((uint16_t)(x[u][r][j] >> 16));
+            s0 += lo * lo;
+            s1 += hi * hi;
+          }
+          ss[r] += s0 + s1;
+        }
+      }
+    }
+    double* rd = (double*)red;
+#pragma unroll
+    for (int r = 0; r < MR; ++r) {
+      const double t = wave_sum_f64(ss[r]);
+      if (lane == 0) rd[r * (NT / 64) + wave] = t;
+    }
+    __syncthreads();
+    float rr[MR];
+#pragma unroll
+    for (int r = 0; r < MR; ++r) {
+      double var = 0.0;
+#pragma unroll
+      for (int w = 0; w < NT / 64; ++w) var += rd[r * (NT / 64) + w];
+      rr[r] = rms_scale((float)var, p.K, p.eps);
+    }
+    const bool nbf = p.norm_bf16 != 0;
+#pragma unroll
+    for (int u = 0; u < PC; ++u) {
+      const int pc = tid + u * NT;
+      if (u * NT < kp && pc < kp) {
+        float gw[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint16_t glo = (uint16_t)(g[u][j] & 0xFFFF), ghi = (uint16_t)(g[u][j] >> 16);
+          gw[2 * j] = nbf ? bf_bits2f(glo) : h_bits2f(glo);
+          gw[2 * j + 1] = nbf ? bf_bits2f(ghi) : h_bits2f(ghi);
+        }
+#pragma unroll
+        for (int r = 0; r < MR; ++r) {
+          if (r < p.M) {
+            u32x4 o;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const float lo = fp32_rounded((h_bits2f((uint16_t)(x[u][r][j] & 0xFFFF)) * rr[r]) * gw[2 * j]);
+              const float hi = fp32_rounded((h_bits2f((uint16_t)(x[u][r][j] >> 16)) * rr[r]) * gw[2 * j + 1]);
+              o[j] = (uint32_t)f2h_bits(lo) | ((uint32_t)f2h_bits(hi) << 16);
+            }
+            *(u32x4*)(xs + r * p.K + 8 * pc) = o;
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+};
+
 // XL (one token tile): the M activation rows are staged in LDS once ([M][K]) and every lane
 // reads its k-slice of row min(r, M - 1) from there (the MFMA's rows past M repeat a real row
 // and are never read back); otherwise each k-step loads the token rows per lane.
-template <int MT, int NWV, int SPG, bool ZP, typename T, bool SBF, bool ONE, bool XL>
+// NORM (fp16 rows staged by XL, K / 8 <= kNormCols * NWV * 64; the launcher uses it for
+// M = 1): the rows come through registers and are staged normalised (RMSNorm prologue)
+// before the first k-step.
+template <int MT, int NWV, int SPG, bool ZP, typename T, bool SBF, bool ONE, bool XL, bool NORM = false>
 __global__ void __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(4, 4)))
 decode_narrow_kernel(const GemmArgs p, int tiles) {
   static_assert(!ONE || MT == 1, "");
   static_assert(!XL || MT == 1, "");
+  static_assert(!NORM || (XL && std::is_same<T, f16>::value), "");
   constexpr int D = 8;
   constexpr int MROWS = ONE ? 1 : 16 * MT;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -75,7 +181,7 @@ decode_narrow_kernel(const GemmArgs p, int tiles) {
     const int n_s = (ngroups * 2 + 63) / 64;      // 16-byte pieces: group i / 2, half i % 2
     const int n_z = ZP ? (ngroups * 2 + 63) / 64 : 0;  // words: group i / 2, word 2t + i % 2
     const int kp = p.K / 8;                            // 16-byte pieces per activation row
-    const int n_x = XL ? (p.M * kp + 63) / 64 : 0;
+    const int n_x = (XL && !NORM) ? (p.M * kp + 63) / 64 : 0;
     for (int j = wave; j < n_s + n_z + n_x; j += NWV) {
       if (j < n_s) {
         const int i = j * 64 + lane;
@@ -95,6 +201,8 @@ decode_narrow_kernel(const GemmArgs p, int tiles) {
       }
     }
   }
+  NormPieces<NWV * 64, ONE ? 1 : 4> npc;
+  if constexpr (NORM) npc.load(p, tid);
 
   f32x4 acc[MT], tot[MT];
   float tot1 = 0.f;
@@ -132,9 +240,10 @@ decode_narrow_kernel(const GemmArgs p, int tiles) {
 #pragma unroll
   for (int u = 0; u < D; ++u) issue(u);
   // this wave's DMA (issued before the ring) has landed once at most the ring is in flight;
-  // the barrier then covers every wave's
+  // the barrier then covers every wave's (with NORM the first barrier of the prologue)
   AWQ_WAIT_VMCNT(XL ? D : D * (1 + MT));
-  __syncthreads();
+  if constexpr (NORM) npc.normalise(p, (uint16_t*)(smem + L.x), red, wave, lane, tid);
+  else __syncthreads();
 
   uint32_t zm0 = 0, zm1 = 0;  // biased zero of the current group (even / odd nibble forms)
   float sf = 0.f;             // scale of the current group
@@ -287,7 +396,7 @@ int launch_pack_decode_narrow(const int32_t* qweight_kn, int32_t* out, int64_t K
 // faster at one tile per CU); one token tile stages its activation rows in LDS when they fit
 constexpr uint32_t kNarrowLdsMax = 65536;
 
-template <int MT, bool ZP, typename T, bool SBF, bool ONE, bool XL>
+template <int MT, bool ZP, typename T, bool SBF, bool ONE, bool XL, bool NORM = false>
 static bool launch_narrow_t(const GemmArgs& a, hipStream_t st) {
   const int tiles = (int)cdiv(a.N, 16);
   const int spg = a.G / 32;
@@ -295,8 +404,9 @@ static bool launch_narrow_t(const GemmArgs& a, hipStream_t st) {
   const int nwv = (tiles <= num_cus() && XL) ? 16 : 8;
   const NarrowLds L = narrow_lds(nwv, ONE ? 1 : 16 * MT, a.K / a.G, a.K, ZP, XL ? a.M : 0);
   if (L.total > kNarrowLdsMax) return false;
+  if (NORM && a.K / 8 > (int64_t)kNormCols(ONE ? 1 : 4) * nwv * 64) return false;
 #define AWQ_NARROW_L(NWV, SPG_) \
-  hipLaunchKernelGGL((decode_narrow_kernel<MT, NWV, SPG_, ZP, T, SBF, ONE, XL>), grid, dim3((NWV) * 64), L.total, st, a, tiles)
+  hipLaunchKernelGGL((decode_narrow_kernel<MT, NWV, SPG_, ZP, T, SBF, ONE, XL, NORM>), grid, dim3((NWV) * 64), L.total, st, a, tiles)
   if (nwv == 16) {
     if (spg == 4) AWQ_NARROW_L(16, 4);
     else if (spg == 2) AWQ_NARROW_L(16, 2);
@@ -316,6 +426,16 @@ static bool launch_narrow_m(const GemmArgs& a, hipStream_t st) {
   if (a.M > 1)
     return launch_narrow_t<1, ZP, T, SBF, false, true>(a, st) || launch_narrow_t<1, ZP, T, SBF, false, false>(a, st);
   return launch_narrow_t<1, ZP, T, SBF, true, true>(a, st) || launch_narrow_t<1, ZP, T, SBF, true, false>(a, st);
+}
+
+// The RMSNorm prologue variant: one fp16 row, fp16 scales, the row staged in LDS (false when
+// it does not fit; the caller then normalises in a launch of its own).  Only M = 1: for 2 .. 4
+// rows the prologue measured no faster on MI355X than the separate row-norm launch (K = 4096,
+// N = 6144: 11.0 us against 10.2 us of kernels plus the launch gap).
+bool launch_decode_narrow_norm(const GemmArgs& a, bool zp, hipStream_t st) {
+  if (a.M != 1 || !a.norm_w) return false;
+  return zp ? launch_narrow_t<1, true, f16, false, true, true, true>(a, st)
+            : launch_narrow_t<1, false, f16, false, true, true, true>(a, st);
 }
 
 bool launch_decode_narrow(const GemmArgs& a, bool zp, int act, int sdt, hipStream_t st) {

@@ -53,6 +53,7 @@ int launch_pack_decode_stream(const int32_t* qweight_kn, int32_t* out, int64_t K
 int64_t decode_narrow_bytes(int64_t K, int64_t N);
 int launch_pack_decode_narrow(const int32_t* qweight_kn, int32_t* out, int64_t K, int64_t N, hipStream_t st);
 bool launch_decode_narrow(const awq::GemmArgs& a, bool zp, int act, int sdt, hipStream_t st);
+bool launch_decode_narrow_norm(const awq::GemmArgs& a, bool zp, hipStream_t st);
 
 // Prefill GEMM (M > 32 or group sizes the decode kernel does not cover).
 bool launch_prefill(const awq::GemmArgs& a, bool seq, bool zp, int act, int sdt, hipStream_t st);

@@ -6,9 +6,11 @@
 // N / 64 programs reads the row twice).  Here one block per row reduces the row once and
 // writes the normalised fp16 row; the GEMM kernels then read it like any activation.
 //
-// Arithmetic of the reference (rmsnorm_awq_fused.py:108-131), kept step for step:
-//   var  = sum over k of fp32(x)^2                       (fp32 accumulation)
-//   rrms = rsqrt(var / K + eps)                          (fp32)
+// Arithmetic of the reference (rmsnorm_awq_fused.py:108-131), step for step:
+//   var  = sum over k of fp32(x)^2       (fp32 in the reference, in 32-element chunks; here the
+//                                         exact squares are added in fp64 and rounded once to
+//                                         fp32, which makes the order of the adds invisible)
+//   rrms = rsqrt(var / K + eps)          (var / K + eps in fp32; the rsqrt correctly rounded)
 //   xn   = fp16_rne((fp32(x) * rrms) * fp32(norm_w))     (two fp32 products, one rounding)
 #include "awq_common.h"
 #include "awq_launch.h"
@@ -21,28 +23,30 @@ template <typename T, typename NT>
 __global__ void __launch_bounds__(kNormThreads) rmsnorm_rows_kernel(const uint16_t* __restrict__ x, int64_t ldx,
                                                                     const uint16_t* __restrict__ nw, float eps,
                                                                     uint16_t* __restrict__ xn, int64_t ldo, int K) {
-  __shared__ float part[kNormThreads / 64];
+  __shared__ double part[kNormThreads / 64];
   const uint16_t* row = x + (int64_t)blockIdx.x * ldx;
   const int t = threadIdx.x;
-  // pass 1: sum of squares, 8 elements (16 bytes) per lane and step
-  float ss = 0.f;
+  // pass 1: sum of squares, 8 elements (16 bytes) per lane and step; the squares are exact
+  // in fp64 and the fp64 sum is within about K * 2^-53 of the exact one, so rounding it once to
+  // fp32 gives the correctly rounded var (whatever the order of the adds) unless the exact sum
+  // lies that close to an fp32 rounding boundary
+  double ss = 0.0;
   for (int k = t * 8; k < K; k += kNormThreads * 8) {
     const u32x4 v = *(const u32x4*)(row + k);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float lo = from_bits<T>((uint16_t)(v[j] & 0xFFFF)), hi = from_bits<T>((uint16_t)(v[j] >> 16));
+      const double lo = from_bits<T>((uint16_t)(v[j] & 0xFFFF)), hi = from_bits<T>((uint16_t)(v[j] >> 16));
       ss += lo * lo;
       ss += hi * hi;
     }
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+  ss = wave_sum_f64(ss);
   if ((t & 63) == 0) part[t >> 6] = ss;
   __syncthreads();
-  float var = 0.f;
+  double var = 0.0;
 #pragma unroll
   for (int w = 0; w < kNormThreads / 64; ++w) var += part[w];  // same order in every lane
-  const float rrms = rsqrtf(var / (float)K + eps);
+  const float rrms = rms_scale((float)var, K, eps);
   // pass 2: the row again (cache-resident), scaled and rounded once to fp16
   uint16_t* orow = xn + (int64_t)blockIdx.x * ldo;
   for (int k = t * 8; k < K; k += kNormThreads * 8) {
@@ -51,8 +55,8 @@ __global__ void __launch_bounds__(kNormThreads) rmsnorm_rows_kernel(const uint16
     u32x4 r;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float lo = (from_bits<T>((uint16_t)(v[j] & 0xFFFF)) * rrms) * from_bits<NT>((uint16_t)(g[j] & 0xFFFF));
-      const float hi = (from_bits<T>((uint16_t)(v[j] >> 16)) * rrms) * from_bits<NT>((uint16_t)(g[j] >> 16));
+      const float lo = fp32_rounded((from_bits<T>((uint16_t)(v[j] & 0xFFFF)) * rrms) * from_bits<NT>((uint16_t)(g[j] & 0xFFFF)));
+      const float hi = fp32_rounded((from_bits<T>((uint16_t)(v[j] >> 16)) * rrms) * from_bits<NT>((uint16_t)(g[j] >> 16)));
       r[j] = (uint32_t)f2h_bits(lo) | ((uint32_t)f2h_bits(hi) << 16);
     }
     *(u32x4*)(orow + k) = r;

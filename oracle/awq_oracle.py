@@ -303,9 +303,10 @@ def rmsnorm_rows(x, norm_w, eps):
     ``xn = fp16((fp32(x) * rrms) * fp32(norm_w))`` -- ``vllm/kernels/triton/
     rmsnorm_awq_fused.py:108-131`` (fp32 ``var`` and ``rrms``, two fp32 products, the cast to
     fp16 at ``:168`` whatever the input dtype).  ``x`` holds the fp16 or bf16 values (any float
-    dtype), ``norm_w`` likewise.  ``var`` is the float32 rounding of the exact sum (the
-    reference adds 32-element ``tl.sum`` chunks in fp32; that order is not part of the
-    contract) and ``rsqrt`` is correctly rounded.
+    dtype), ``norm_w`` likewise.  ``var`` is the float32 rounding of the float64 sum of the
+    (exact) squares -- the correctly rounded sum but in vanishingly rare cases; the reference
+    adds 32-element ``tl.sum`` chunks in fp32, an order that is not part of the contract -- and
+    ``rsqrt`` is correctly rounded.
 
     Pinned by: ``torch.nn.functional.rms_norm`` in float32 (to one fp16 ulp), the constant-row
     case (``xn = sign(x)`` exactly for unit weights), bit-exact invariance under power-of-two
