@@ -127,6 +127,8 @@ CASES = [
     (64, 4, 256, 128, 2, 32, False, "silu"),                # 32 routes/expert, 2 groups per k-stage
     (128, 8, 512, 192, 4, 64, True, "gelu_pytorch_tanh"),   # partial gate tile (I = 192)
     (300, 16, 256, 256, 4, 128, True, "silu"),              # ~75 routes/expert: 2 row tiles
+    # Gemma4's symmetric group-32 experts (z = 8, tanh GELU) at a decode batch
+    (16, 64, 512, 256, 8, 32, False, "gelu_pytorch_tanh"),
 ]
 
 
