@@ -38,102 +38,72 @@ __host__ __device__ inline NarrowLds narrow_lds(int nwv, int mrows, int ngroups,
   return l;
 }
 
-// RMSNorm prologue (rmsnorm_awq_fused.py:108-131), for XL with fp16 rows, M <= 4: the rows
-// arrive in registers instead of by DMA -- lane tid holds 16-byte column pieces pc = tid,
-// tid + NT, .. (at most kNormCols(MR) of them) of every row, with the matching 16 bytes of the
-// norm weights, read once for all rows.  Per row the sum of squares (exact squares added in
-// fp64: lanes by DPP, then the waves through `red`) is rounded once to fp32, rrms =
-// rsqrt(var / K + eps) correctly rounded, and each element is written to the staged rows in
-// LDS as fp16((x * rrms) * norm_w).
-__host__ __device__ constexpr int kNormCols(int mr) { return mr == 1 ? 6 : 1; }
+// RMSNorm prologue (rmsnorm_awq_fused.py:108-131) for one fp16 row staged by XL: the row
+// arrives in registers instead of by DMA -- lane tid holds the 16-byte pieces pc = tid,
+// tid + NT, .. (at most kNormCols of them) with the matching 16 bytes of the norm weights.
+// The sum of squares (exact squares added in fp64: lanes by DPP, then the waves through
+// `red`) is rounded once to fp32, rrms = rsqrt(var / K + eps) correctly rounded, and each
+// element is written to the staged row in LDS as fp16((x * rrms) * norm_w).
+constexpr int kNormCols = 6;
 
-template <int NT, int MR>
-struct NormPieces {
-  static constexpr int PC = kNormCols(MR);
-  u32x4 x[PC][MR], g[PC];
+template <int NT>
+struct NormRow {
+  u32x4 x[kNormCols], g[kNormCols];
 
   __device__ __forceinline__ void load(const GemmArgs& p, int tid) {
     const int kp = p.K >> 3;
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.a, (uint32_t)((uint64_t)p.M * (uint64_t)p.lda * 2u));
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.a, (uint32_t)p.K * 2u);
     const __amdgpu_buffer_rsrc_t gr = make_rsrc(p.norm_w, (uint32_t)p.K * 2u);
 #pragma unroll
-    for (int u = 0; u < PC; ++u) {
+    for (int u = 0; u < kNormCols; ++u) {
       if (u * NT < kp) {  // block-uniform
         const int pc = tid + u * NT;
-        const bool ok = pc < kp;  // past the row, and rows past M: the loads read zeros
-        g[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                   gr, ok ? (int)(16u * (uint32_t)pc) : (int)0x80000000, 0, 0));
-#pragma unroll
-        for (int r = 0; r < MR; ++r)
-          x[u][r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                        xr, ok && r < p.M ? (int)(((uint32_t)r * (uint32_t)p.lda + 8u * (uint32_t)pc) * 2u) : (int)0x80000000,
-                        0, 0));
+        const int off = pc < kp ? (int)(16u * (uint32_t)pc) : (int)0x80000000;  // past the row: zeros
+        x[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+        g[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(gr, off, 0, 0));
       }
     }
   }
 
-  // after the loads have landed: the rows' sums, then (one barrier) the normalised pieces
+  // after the loads have landed: the row's sum, then (one barrier) the normalised pieces
   __device__ __forceinline__ void normalise(const GemmArgs& p, uint16_t* xs, float* red, int wave, int lane, int tid) {
     const int kp = p.K >> 3;
-    double ss[MR];
+    double ss = 0.0;
 #pragma unroll
-    for (int r = 0; r < MR; ++r) ss[r] = 0.0;
-#pragma unroll
-    for (int u = 0; u < PC; ++u) {
+    for (int u = 0; u < kNormCols; ++u) {
       if (u * NT < kp) {
+        double s0 = 0.0, s1 = 0.0;
 #pragma unroll
-        for (int r = 0; r < MR; ++r) {
-          double s0 = 0.0, s1 = 0.0;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const double lo = h_bits2f((uint16_t)(x[u][r][j] & 0xFFFF)), hi = h_bits2f((uint16_t)(x[u][r][j] >> 16));
-            s0 += lo * lo;
-            s1 += hi * hi;
-          }
-          ss[r] += s0 + s1;
+        for (int j = 0; j < 4; ++j) {
+          const double lo = h_bits2f((uint16_t)(x[u][j] & 0xFFFF)), hi = h_bits2f((uint16_t)(x[u][j] >> 16));
+          s0 += lo * lo;
+          s1 += hi * hi;
         }
+        ss += s0 + s1;
       }
     }
     double* rd = (double*)red;
-#pragma unroll
-    for (int r = 0; r < MR; ++r) {
-      const double t = wave_sum_f64(ss[r]);
-      if (lane == 0) rd[r * (NT / 64) + wave] = t;
-    }
+    ss = wave_sum_f64(ss);
+    if (lane == 0) rd[wave] = ss;
     __syncthreads();
-    float rr[MR];
+    double var = 0.0;
 #pragma unroll
-    for (int r = 0; r < MR; ++r) {
-      double var = 0.0;
-#pragma unroll
-      for (int w = 0; w < NT / 64; ++w) var += rd[r * (NT / 64) + w];
-      rr[r] = rms_scale((float)var, p.K, p.eps);
-    }
+    for (int w = 0; w < NT / 64; ++w) var += rd[w];
+    const float rr = rms_scale((float)var, p.K, p.eps);
     const bool nbf = p.norm_bf16 != 0;
 #pragma unroll
-    for (int u = 0; u < PC; ++u) {
+    for (int u = 0; u < kNormCols; ++u) {
       const int pc = tid + u * NT;
       if (u * NT < kp && pc < kp) {
-        float gw[8];
+        u32x4 o;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const uint16_t glo = (uint16_t)(g[u][j] & 0xFFFF), ghi = (uint16_t)(g[u][j] >> 16);
-          gw[2 * j] = nbf ? bf_bits2f(glo) : h_bits2f(glo);
-          gw[2 * j + 1] = nbf ? bf_bits2f(ghi) : h_bits2f(ghi);
+          const float lo = fp32_rounded((h_bits2f((uint16_t)(x[u][j] & 0xFFFF)) * rr) * (nbf ? bf_bits2f(glo) : h_bits2f(glo)));
+          const float hi = fp32_rounded((h_bits2f((uint16_t)(x[u][j] >> 16)) * rr) * (nbf ? bf_bits2f(ghi) : h_bits2f(ghi)));
+          o[j] = (uint32_t)f2h_bits(lo) | ((uint32_t)f2h_bits(hi) << 16);
         }
-#pragma unroll
-        for (int r = 0; r < MR; ++r) {
-          if (r < p.M) {
-            u32x4 o;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const float lo = fp32_rounded((h_bits2f((uint16_t)(x[u][r][j] & 0xFFFF)) * rr[r]) * gw[2 * j]);
-              const float hi = fp32_rounded((h_bits2f((uint16_t)(x[u][r][j] >> 16)) * rr[r]) * gw[2 * j + 1]);
-              o[j] = (uint32_t)f2h_bits(lo) | ((uint32_t)f2h_bits(hi) << 16);
-            }
-            *(u32x4*)(xs + r * p.K + 8 * pc) = o;
-          }
-        }
+        *(u32x4*)(xs + 8 * pc) = o;
       }
     }
     __syncthreads();
@@ -143,15 +113,14 @@ struct NormPieces {
 // XL (one token tile): the M activation rows are staged in LDS once ([M][K]) and every lane
 // reads its k-slice of row min(r, M - 1) from there (the MFMA's rows past M repeat a real row
 // and are never read back); otherwise each k-step loads the token rows per lane.
-// NORM (fp16 rows staged by XL, K / 8 <= kNormCols * NWV * 64; the launcher uses it for
-// M = 1): the rows come through registers and are staged normalised (RMSNorm prologue)
-// before the first k-step.
+// NORM (one fp16 row staged by XL, K / 8 <= kNormCols * NWV * 64): the row comes through
+// registers and is staged normalised (RMSNorm prologue) before the first k-step.
 template <int MT, int NWV, int SPG, bool ZP, typename T, bool SBF, bool ONE, bool XL, bool NORM = false>
 __global__ void __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(4, 4)))
 decode_narrow_kernel(const GemmArgs p, int tiles) {
   static_assert(!ONE || MT == 1, "");
   static_assert(!XL || MT == 1, "");
-  static_assert(!NORM || (XL && std::is_same<T, f16>::value), "");
+  static_assert(!NORM || (XL && ONE && std::is_same<T, f16>::value), "");
   constexpr int D = 8;
   constexpr int MROWS = ONE ? 1 : 16 * MT;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -201,7 +170,7 @@ decode_narrow_kernel(const GemmArgs p, int tiles) {
       }
     }
   }
-  NormPieces<NWV * 64, ONE ? 1 : 4> npc;
+  NormRow<NWV * 64> npc;
   if constexpr (NORM) npc.load(p, tid);
 
   f32x4 acc[MT], tot[MT];
@@ -404,7 +373,7 @@ static bool launch_narrow_t(const GemmArgs& a, hipStream_t st) {
   const int nwv = (tiles <= num_cus() && XL) ? 16 : 8;
   const NarrowLds L = narrow_lds(nwv, ONE ? 1 : 16 * MT, a.K / a.G, a.K, ZP, XL ? a.M : 0);
   if (L.total > kNarrowLdsMax) return false;
-  if (NORM && a.K / 8 > (int64_t)kNormCols(ONE ? 1 : 4) * nwv * 64) return false;
+  if (NORM && a.K / 8 > (int64_t)kNormCols * nwv * 64) return false;
 #define AWQ_NARROW_L(NWV, SPG_) \
   hipLaunchKernelGGL((decode_narrow_kernel<MT, NWV, SPG_, ZP, T, SBF, ONE, XL, NORM>), grid, dim3((NWV) * 64), L.total, st, a, tiles)
   if (nwv == 16) {
