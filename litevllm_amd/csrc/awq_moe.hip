@@ -101,18 +101,23 @@ __global__ void __launch_bounds__(256) moe_pack_stream_kernel(const uint32_t* __
   }
 }
 
-// Route lists: block e collects the routes r (in increasing order) whose id is e.
+// Route lists: block e collects the routes r (in increasing order) whose id is e.  The ids of
+// the first kAlignPre rounds of 256 are all requested before the first round runs (one memory
+// wait instead of one per round); later rounds load their own.
+constexpr int kAlignPre = 16;
 __global__ void __launch_bounds__(256) moe_align_kernel(const void* ids, int id64, int R, int* lists,
                                                         int* counts) {
   __shared__ int s_wcnt[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int e = blockIdx.x;
   int* list = lists + (int64_t)e * R;
+  auto load_id = [&](int idx) -> int {
+    if (idx >= R) return -1;
+    return id64 ? (int)((const int64_t*)ids)[idx] : ((const int32_t*)ids)[idx];
+  };
   int count = 0;
-  for (int base = 0; base < R; base += 256) {
+  auto round = [&](int base, int id) {
     const int idx = base + tid;
-    int id = -1;
-    if (idx < R) id = id64 ? (int)((const int64_t*)ids)[idx] : ((const int32_t*)ids)[idx];
     const bool hit = id == e;
     const uint64_t m = __ballot(hit);
     if (lane == 0) s_wcnt[wave] = __popcll(m);
@@ -126,7 +131,14 @@ __global__ void __launch_bounds__(256) moe_align_kernel(const void* ids, int id6
     if (hit) list[off + __popcll(m & ((1ull << lane) - 1ull))] = idx;
     __syncthreads();  // s_wcnt is read by every wave before the next round writes it
     count = tot;
-  }
+  };
+  int pre[kAlignPre];
+#pragma unroll
+  for (int u = 0; u < kAlignPre; ++u) pre[u] = load_id(u * 256 + tid);
+#pragma unroll
+  for (int u = 0; u < kAlignPre; ++u)
+    if (u * 256 < R) round(u * 256, pre[u]);  // block-uniform
+  for (int base = kAlignPre * 256; base < R; base += 256) round(base, load_id(base + tid));
   if (tid == 0) counts[e] = count;
 }
 
@@ -141,7 +153,25 @@ __global__ void __launch_bounds__(256) moe_combine_kernel(const float* __restric
   if (idx >= T_tok * hq) return;
   const int64_t t = idx / hq, c = idx - t * hq;
   f32x4 s = {0.f, 0.f, 0.f, 0.f};
-  for (int j = 0; j < topk; ++j) {
+  int j = 0;
+  // eight routes at a time: their ids and rows are all requested before any is added (the
+  // rows of every route exist, so the loads need not wait for the id checks); the sum still
+  // runs in j order
+  for (; j + 8 <= topk; j += 8) {
+    int id[8];
+    f32x4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t rt = t * topk + j + u;
+      id[u] = id64 ? (int)((const int64_t*)ids)[rt] : ((const int32_t*)ids)[rt];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = *(const f32x4*)(y + (t * topk + j + u) * H + 4 * c);
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (id[u] >= 0 && id[u] < E) s += v[u];
+  }
+  for (; j < topk; ++j) {
     const int64_t rt = t * topk + j;
     const int id = id64 ? (int)((const int64_t*)ids)[rt] : ((const int32_t*)ids)[rt];
     if (id < 0 || id >= E) continue;
