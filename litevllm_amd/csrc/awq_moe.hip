@@ -52,7 +52,28 @@ __global__ void __launch_bounds__(256) moe_route_kernel(const void* logits, int6
   for (int j = 0; j < 4; ++j) v[j] = (lane + 64 * j) < E ? v[j] / s : -1.f;  // -1: not selectable
   float mine = 0.f, sel_sum = 0.f;
   int mine_id = 0;
-  for (int k = 0; k < topk; ++k) {
+  if (E <= 64) {
+    // one probability per lane: its rank among the E (larger first, equal ones by lower id)
+    // in one pass over the lanes, then slot k is the lane of rank k -- the same choices, in
+    // the same order, as the repeated arg-max below
+    const int vb = __float_as_int(v[0]);
+    const float vi = v[0];
+    int rank = 0;
+    for (int j = 0; j < E; ++j) {  // wave-uniform
+      const float vj = __int_as_float(__builtin_amdgcn_readlane(vb, j));
+      rank += (vj > vi || (vj == vi && j < lane)) ? 1 : 0;
+    }
+    for (int k = 0; k < topk; ++k) {
+      const uint64_t m = __ballot(lane < E && rank == k);
+      const int src = m ? __ffsll((unsigned long long)m) - 1 : 0;
+      const float bv = __int_as_float(__builtin_amdgcn_readlane(vb, src));
+      if (lane == k) {
+        mine = bv;
+        mine_id = src;
+      }
+      sel_sum += bv;
+    }
+  } else for (int k = 0; k < topk; ++k) {
     float bv = -1.f;
     int bi = 0x7fffffff;
 #pragma unroll

@@ -97,7 +97,7 @@ def test_dequant_matches_oracle_for_expert_slices():
         assert np.array_equal(w.view(np.uint16), ref.view(np.uint16))
 
 
-@pytest.mark.parametrize("T,E,topk", [(1, 8, 2), (37, 64, 8), (300, 16, 4)])
+@pytest.mark.parametrize("T,E,topk", [(1, 8, 2), (37, 64, 8), (300, 16, 4), (20, 128, 8), (9, 256, 6)])
 def test_route_matches_fp32_torch(T, E, topk):
     g = torch.Generator().manual_seed(T)
     logits = torch.randn(T, E, generator=g).half()
@@ -114,6 +114,20 @@ def test_route_ties_pick_lower_expert():
     w, ids = ops.moe_route(logits.to(DEV), 4)
     assert ids.cpu().tolist() == [[0, 1, 2, 3]] * 3
     assert torch.allclose(w.cpu(), torch.full((3, 4), 0.25))
+
+
+def test_route_partial_ties_straddle_the_cut():
+    """Equal probabilities on both sides of the k-th place: the lower expert ids are taken, in
+    id order among equals (E <= 64 ranks lanes in one pass, larger E repeats the arg-max)."""
+    for E in (32, 64, 96):
+        logits = torch.zeros(4, E, dtype=torch.float16)
+        logits[:, [5, 9, 17, 30]] = 2.0
+        logits[:, [3, 12, 20, 25]] = 1.0  # three of these four make the top 7
+        w, ids = ops.moe_route(logits.to(DEV), 7)
+        sel = [5, 9, 17, 30, 3, 12, 20]
+        assert ids.cpu().tolist() == [sel] * 4, E
+        p = torch.softmax(logits.float(), dim=-1)[:, sel]  # torch.topk leaves tie order open
+        assert torch.allclose(w.cpu(), p / p.sum(-1, keepdim=True), rtol=2e-6, atol=1e-7)
 
 
 CASES = [
