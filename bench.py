@@ -79,42 +79,146 @@ def _time_graph(torch, fn, reps, warmup=3):
     return start.elapsed_time(end) / reps, g
 
 
-def cpu_baseline(sample_seconds=12.0):
-    """The reference CPU path restated (oracle/ref_cpu.py), cold: dequant + F.linear per call,
-    cycling over the decode sweep shapes until ~sample_seconds of timed CPU work.  Returns
-    GB/s of algorithmic bytes."""
+def _cpu_host():
+    """Host CPU facts for the CPU baseline: os.cpu_count(), the cores this process may run on
+    (affinity), the cgroup CPU quota, the model name (lscpu), and the thread count used: all
+    cores (os.cpu_count()), or fewer when the affinity mask or the quota allows fewer."""
+    import subprocess
+    count = os.cpu_count() or 1
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else count
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, period = f.read().split()[:2]
+            if q != "max":
+                quota = max(1, int(int(q) // int(period)))
+    except (OSError, ValueError):
+        pass
+    model = None
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        model = next((l.split(":", 1)[1].strip() for l in out.splitlines() if l.startswith("Model name")), None)
+    except (OSError, subprocess.SubprocessError):
+        pass
+    threads = min(c for c in (count, affinity, quota) if c)
+    return {"os_cpu_count": count, "affinity_cores": affinity, "cgroup_quota_cpus": quota,
+            "model": model, "threads": threads}
+
+
+def _median_time(fn, reps):
+    """Median wall time of fn() over `reps` calls after one warm-up call."""
+    fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
+def cpu_baseline(reps=5):
+    """The reference's CPU path restated (oracle/ref_cpu.py), timed on the host cores with
+    torch.set_num_threads(all cores), median of `reps` after one warm-up, per configuration:
+      * cold = dequant (int64 shifts, fp32 math, tensor.py:835-860) + F.linear in fp16 per
+        call; warm = F.linear on the cached fp16 weight only (the reference's LRU steady
+        state, tensor.py:1125-1129, 1142);
+      * configs[1] (the headline: the nine decode shapes, algorithmic GB/s), configs[0],
+        configs[2] (M in {1, 8, 32}; split-K is a GPU knob), configs[3] on a 64-row sample of
+        M = 2048 (TFLOP/s), configs[4] through the restated fused_moe over dense fp16 experts
+        (T = 16 grouped branch; T = 512 serialized per-token branch, fused_moe.py:21, on a
+        64-token sample scaled to 512; cold adds the dequantization of the experts touched).
+    Returns the cpu_baseline object (value = configs[1] cold GB/s) with the per-config legs."""
     import numpy as np
     import torch
     from oracle import ref_cpu as R
 
-    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    cores = max(1, min(cores, 16))
-    torch.set_num_threads(cores)
+    host = _cpu_host()
+    torch.set_num_threads(host["threads"])
     rng = np.random.default_rng(0)
-    probs = {}
+    t_start = time.perf_counter()
+
+    def ref_weight(K, N):
+        qw = torch.from_numpy(rng.integers(-2**31, 2**31 - 1, size=(N, K // 8), dtype=np.int64).astype(np.int32))
+        qz = torch.from_numpy(rng.integers(-2**31, 2**31 - 1, size=(N, K // G // 8), dtype=np.int64).astype(np.int32))
+        sc = torch.from_numpy((np.abs(rng.standard_normal((N, K // G))) * 0.02 + 1e-4).astype(np.float16))
+        return qw, sc, qz  # awq_linear_cpu argument order
+
+    def x_of(M, K):
+        return torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16))
+
+    def cold_warm(M, K, N, wts):
+        x = x_of(M, K)
+        cold = _median_time(lambda: R.awq_linear_cpu(x, *wts, G), reps)
+        dense = R.dequantize_awq_cpu(*wts, G)
+        warm = _median_time(lambda: R.awq_linear_cpu(x, *wts, G, dense_weight=dense), reps)
+        return cold, warm
+
+    legs = {}
+    # configs[1]: the headline sweep
+    W1 = {n: ref_weight(K_DEC, n) for n in (4096, 6144, 24576)}
+    per = {}
+    tc = tw = 0.0
     for M, N in SWEEP:
-        K = K_DEC
-        if N not in probs:
-            qw = torch.from_numpy(rng.integers(-2**31, 2**31 - 1, size=(N, K // 8), dtype=np.int64).astype(np.int32))
-            qz = torch.from_numpy(rng.integers(-2**31, 2**31 - 1, size=(N, K // G // 8), dtype=np.int64).astype(np.int32))
-            sc = torch.from_numpy((np.abs(rng.standard_normal((N, K // G))) * 0.02 + 1e-4).astype(np.float16))
-            probs[N] = (qw, sc, qz)  # awq_linear_cpu argument order
-    xs = {m: torch.from_numpy(rng.standard_normal((m, K_DEC)).astype(np.float16)) for m in (1, 4, 16)}
-    R.awq_linear_cpu(xs[1], *probs[4096], G)  # warm-up
-    done_bytes, t_total, calls = 0, 0.0, 0
-    while t_total < sample_seconds:
-        for M, N in SWEEP:
-            t0 = time.perf_counter()
-            R.awq_linear_cpu(xs[M], *probs[N], G)
-            t_total += time.perf_counter() - t0
-            done_bytes += alg_bytes(M, K_DEC, N)
-            calls += 1
+        c, w = cold_warm(M, K_DEC, N, W1[N])
+        per[f"M{M}_N{N}"] = {"cold_ms": round(c * 1e3, 3), "warm_ms": round(w * 1e3, 3)}
+        tc += c
+        tw += w
+    step = sum(alg_bytes(m, K_DEC, n) for m, n in SWEEP)
+    legs["config1"] = {"cold_GBps": round(step / tc / 1e9, 4), "warm_GBps": round(step / tw / 1e9, 4),
+                       "per_shape": per}
+    del W1
+    # configs[0]
+    c, w = cold_warm(1, 2048, 5632, ref_weight(2048, 5632))
+    legs["config0"] = {"M": 1, "K": 2048, "N": 5632, "cold_ms": round(c * 1e3, 3), "warm_ms": round(w * 1e3, 3),
+                       "cold_GBps": round(alg_bytes(1, 2048, 5632) / c / 1e9, 4),
+                       "warm_GBps": round(alg_bytes(1, 2048, 5632) / w / 1e9, 4)}
+    # configs[2]
+    W2 = ref_weight(12288, 4096)
+    legs["config2"] = {}
+    for M in (1, 8, 32):
+        c, w = cold_warm(M, 12288, 4096, W2)
+        legs["config2"][f"M{M}"] = {"cold_ms": round(c * 1e3, 3), "warm_ms": round(w * 1e3, 3)}
+    del W2
+    # configs[3]: 64 of the 2048 rows
+    rows, K3, N3 = 64, K_DEC, 24576
+    c, w = cold_warm(rows, K3, N3, ref_weight(K3, N3))
+    fl = 2.0 * rows * K3 * N3
+    legs["config3"] = {"sample": f"{rows} rows of M=2048, K={K3}, N={N3}", "cold_ms": round(c * 1e3, 2),
+                       "warm_ms": round(w * 1e3, 2), "cold_TFLOPs": round(fl / c / 1e12, 5),
+                       "warm_TFLOPs": round(fl / w / 1e12, 5)}
+    # configs[4]: fused_moe over dense fp16 experts (distinct storage per expert)
+    E, H, I, topk = MOE_E, MOE_H, MOE_I, MOE_TOPK
+    w1 = torch.empty((E, 2 * I, H), dtype=torch.float16)
+    w2 = torch.empty((E, H, I), dtype=torch.float16)
+    w1.copy_(torch.randn((1, 2 * I, H)).mul_(0.02).half().expand(E, -1, -1))
+    w2.copy_(torch.randn((1, H, I)).mul_(0.02).half().expand(E, -1, -1))
+    expert_wts = [ref_weight(H, 2 * I), ref_weight(I, H)]
+    deq_one = _median_time(lambda: [R.dequantize_awq_cpu(*wt, G) for wt in expert_wts], 3)
+    legs["config4"] = {}
+    for T, sample in ((16, 16), (512, 64)):
+        x = torch.from_numpy(rng.standard_normal((sample, H)).astype(np.float16))
+        logits = torch.from_numpy(rng.standard_normal((sample, E)).astype(np.float16))
+        if T == 512:  # the serialized branch for all T > 128 (fused_moe.py:21): force it on the sample
+            tw_, tid_ = R.moe_routing_cpu(logits, topk)
+            run = lambda: R.fused_moe_cpu(x, w1, w2, topk_weights=tw_, topk_ids=tid_, serialized=True)
+        else:
+            run = lambda: R.fused_moe_cpu(x, w1, w2, logits, topk)
+        t_s = _median_time(run, reps) * (T / sample)
+        distinct = 64 if T == 512 else int(torch.unique(R.moe_routing_cpu(logits, topk)[1]).numel())
+        fl = 2.0 * T * topk * (H * 2 * I + I * H)
+        legs["config4"][f"T{T}"] = {"warm_ms": round(t_s * 1e3, 2), "cold_ms": round((t_s + distinct * deq_one) * 1e3, 2),
+                                    "warm_TFLOPs": round(fl / t_s / 1e12, 5),
+                                    "sample": f"{sample} tokens" + (" scaled to 512 (serialized branch)" if T == 512 else "")}
+    del w1, w2
     return {
-        "value": round(done_bytes / t_total / 1e9, 3), "unit": "GB/s", "cores": int(torch.get_num_threads()),
-        "kind": "port",
-        "sample": f"{calls} cold calls (reference CPU path restated: int64-shift dequant + fp32 math + "
-                  f"F.linear in fp16, K=4096, G=128) cycling over the nine decode sweep shapes, "
-                  f"{t_total:.1f} s of CPU work",
+        "value": legs["config1"]["cold_GBps"], "unit": "GB/s", "cores": int(torch.get_num_threads()),
+        "kind": "port", "warm_value": legs["config1"]["warm_GBps"], "host": host,
+        "sample": "reference CPU path restated (dequant with int64 shifts and fp32 math, F.linear in fp16), "
+                  f"median of {reps} after a warm-up per shape; value = configs[1] nine-shape sweep, cold "
+                  f"(dequant + matmul per call); warm_value = cached fp16 weights; {time.perf_counter() - t_start:.1f} s "
+                  "of CPU work in all legs",
+        "legs": legs,
     }
 
 
@@ -215,6 +319,35 @@ def _traffic():
         return None
 
 
+ROT_BYTES = 1 << 30  # every timed rotation reads at least this many distinct weight bytes
+
+
+def weight_bytes(K, N, g=G):
+    return K * N // 2 + (K // g) * N * 2 + (K // g) * (N // 8) * 4
+
+
+def rot_copies(K, N):
+    """Weight copies whose rotation reads >= 1 GiB (beyond the 256 MB Infinity Cache)."""
+    return max(2, -(-ROT_BYTES // weight_bytes(K, N)))
+
+
+def _time_rotation(torch, ops, X, pool, Y, reps, **kw):
+    """us per launch of gemm(X, w) over every weight copy of `pool` (a graph of back-to-back
+    launches, replayed `reps` times)."""
+    def run():
+        for qw, qz, sc in pool:
+            ops.gemm(X, qw, sc, qz, G, layout="autoawq", out=Y, **kw)
+    ms, g = _time_graph(torch, run, reps)
+    del g
+    return ms * 1e3 / len(pool)
+
+
+def _hbm_entry(us, M, K, N):
+    b = alg_bytes(M, K, N)
+    gbs = b / (us * 1e-6) / 1e9
+    return {"us": round(us, 3), "GBps": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -224,8 +357,9 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--no-rmsnorm", action="store_true")
-    ap.add_argument("--only", default="", help="profile mode: 'decode-m1n24576', 'prefill' or "
-                    "'copy-64MiB' (counter calibration) launches only")
+    ap.add_argument("--no-configs", action="store_true", help="skip the configs[0], [2], [3] entries")
+    ap.add_argument("--only", default="", help="profile mode: 'decode-m1n24576', 'prefill', 'moe-t16', "
+                    "'moe-t512' or 'copy-64MiB' (counter calibration) launches only")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -241,7 +375,7 @@ def main():
     gen = torch.Generator(device=dev).manual_seed(1)
 
     if args.only == "decode-m1n24576":
-        W = _weights(torch, K_DEC, 24576, 24, dev, 7)
+        W = _weights(torch, K_DEC, 24576, rot_copies(K_DEC, 24576), dev, 7)
         x = torch.randn((1, K_DEC), device=dev, generator=gen).half()
         for qw, qz, sc in W:
             ops.prepare_decode_stream(qw)
@@ -278,19 +412,24 @@ def main():
         torch.cuda.synchronize()
         return
 
-    # ---- decode sweep: rotate >= 1 GiB of weights ----
+    # ---- configs[1] decode sweep (the metric) ----
+    # one weight pool per N whose rotation alone reads >= 1 GiB; step c gives shape (m, n) its
+    # own copy 3 c + (index of m), so a step reads nine distinct weights and the steps rotate
+    # through >= 1 GiB before any copy comes back
     step_bytes = sum(alg_bytes(m, K_DEC, n) for m, n in SWEEP)
-    wbytes_step = sum(K_DEC * n // 2 + (K_DEC // G) * n * 2 + (K_DEC // G) * (n // 8) * 4 for _, n in SWEEP)
-    copies = max(2, -(-(1 << 30) // wbytes_step))
-    W = {}
-    for i, (m, n) in enumerate(SWEEP):
-        W[(m, n)] = _weights(torch, K_DEC, n, copies, dev, 100 + i)
-    X = {m: torch.randn((m, K_DEC), device=dev, generator=gen).half() for m in (1, 4, 16)}
+    wbytes_step = sum(weight_bytes(K_DEC, n) for _, n in SWEEP)
+    copies = max(2, -(-ROT_BYTES // wbytes_step))
+    Ms = (1, 4, 16)
+    pools = {n: _weights(torch, K_DEC, n, max(rot_copies(K_DEC, n), 3 * copies), dev, 100 + n) for n in (4096, 6144, 24576)}
+    for n, pool in pools.items():
+        for qw, _, _ in pool:
+            ops.prepare_decode_stream(qw)
+    X = {m: torch.randn((m, K_DEC), device=dev, generator=gen).half() for m in Ms}
     Y = {(m, n): torch.empty((m, n), device=dev, dtype=torch.float16) for m, n in SWEEP}
 
     def step_fn(c):
         for m, n in SWEEP:
-            qw, qz, sc = W[(m, n)][c]
+            qw, qz, sc = pools[n][3 * c + Ms.index(m)]
             ops.gemm(X[m], qw, sc, qz, G, layout="autoawq", out=Y[(m, n)])
 
     def rotation():
@@ -307,41 +446,61 @@ def main():
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     del graph
 
-    # ---- per-shape launch durations (graph of back-to-back launches, rotated copies) ----
+    # ---- per-shape launch durations: back-to-back launches over each pool (>= 1 GiB) ----
     per_shape = {}
     for m, n in SWEEP:
-        def one(m=m, n=n):
-            for c in range(copies):
-                qw, qz, sc = W[(m, n)][c]
-                ops.gemm(X[m], qw, sc, qz, G, layout="autoawq", out=Y[(m, n)])
-        ms, g = _time_graph(torch, one, 20)
-        del g
-        us = ms * 1e3 / copies
-        b = alg_bytes(m, K_DEC, n)
-        per_shape[f"M{m}_N{n}"] = {"us": round(us, 3), "GBps": round(b / (us * 1e-6) / 1e9, 1),
-                                   "hbm_frac": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        us = _time_rotation(torch, ops, X[m], pools[n], Y[(m, n)], 20)
+        per_shape[f"M{m}_N{n}"] = _hbm_entry(us, m, K_DEC, n)
+        per_shape[f"M{m}_N{n}"]["copies"] = len(pools[n])
     r = per_shape["M1_N24576"]
-    roof_bytes = alg_bytes(1, K_DEC, 24576)
     roofline = {"bound": "hbm", "achieved": r["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(r["GBps"] / HBM_PEAK_GBS, 4), "traffic": _traffic(),
                 "kernel": "decode_kn_kernel (decode stream layout) M=1 K=4096 N=24576",
-                "bytes_per_launch": roof_bytes, "avg_launch_us": r["us"]}
-    del W
+                "bytes_per_launch": alg_bytes(1, K_DEC, 24576), "avg_launch_us": r["us"],
+                "rotation_bytes": len(pools[24576]) * weight_bytes(K_DEC, 24576)}
+    del pools, X, Y
 
-    # ---- prefill (configs[3], M=2048, N=24576) ----
+    # ---- configs[0], configs[2] (split-K 1/4/8), configs[3] (all four shapes) ----
+    configs = None
+    if not args.no_configs:
+        configs = {}
+        W0 = _weights(torch, 2048, 5632, rot_copies(2048, 5632), dev, 50)
+        x0 = torch.randn((1, 2048), device=dev, generator=gen).half()
+        y0 = torch.empty((1, 5632), device=dev, dtype=torch.float16)
+        configs["config0"] = _hbm_entry(_time_rotation(torch, ops, x0, W0, y0, 20), 1, 2048, 5632)
+        configs["config0"]["copies"] = len(W0)
+        del W0
+        W2 = _weights(torch, 12288, 4096, rot_copies(12288, 4096), dev, 51)
+        c2 = {}
+        for m in (1, 8, 32):
+            x2 = torch.randn((m, 12288), device=dev, generator=gen).half()
+            y2 = torch.empty((m, 4096), device=dev, dtype=torch.float16)
+            for sk in (1, 4, 8):
+                c2[f"M{m}_split{sk}"] = _hbm_entry(_time_rotation(torch, ops, x2, W2, y2, 20, split_k=sk), m, 12288, 4096)
+        c2["copies"] = len(W2)
+        configs["config2"] = c2
+        del W2
+        c3 = {}
+        for n in (12288, 24576):
+            W3 = _weights(torch, K_DEC, n, 3, dev, 52 + n)
+            for m in (512, 2048):
+                x3 = torch.randn((m, K_DEC), device=dev, generator=gen).half()
+                y3 = torch.empty((m, n), device=dev, dtype=torch.float16)
+                us = _time_rotation(torch, ops, x3, W3, y3, 5)
+                tfl = 2.0 * m * n * K_DEC / (us * 1e-6) / 1e12
+                c3[f"M{m}_N{n}"] = {"us": round(us, 1), "TFLOPs": round(tfl, 1),
+                                    "mfma_frac": round(tfl / MFMA_F16_PEAK_TFLOPS, 4)}
+            del W3
+        configs["config3"] = c3
+
+    # ---- prefill headline (configs[3], M=2048, N=24576) ----
     prefill = None
     if not args.no_prefill:
         M, N = 2048, 24576
         Wp = _weights(torch, K_DEC, N, 3, dev, 9)
         xp = torch.randn((M, K_DEC), device=dev, generator=gen).half()
         yp = torch.empty((M, N), device=dev, dtype=torch.float16)
-
-        def pf():
-            for qw, qz, sc in Wp:
-                ops.gemm(xp, qw, sc, qz, G, layout="autoawq", out=yp)
-        ms, g = _time_graph(torch, pf, 3)
-        del g
-        us = ms * 1e3 / len(Wp)
+        us = _time_rotation(torch, ops, xp, Wp, yp, 5)
         tflops = 2.0 * M * N * K_DEC / (us * 1e-6) / 1e12
         prefill = {"M": M, "K": K_DEC, "N": N, "us": round(us, 1), "TFLOPs": round(tflops, 1),
                    "mfma_frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "peak_TFLOPs": MFMA_F16_PEAK_TFLOPS}
@@ -368,6 +527,7 @@ def main():
                    "bytes_per_step": step_bytes},
         "roofline": roofline,
         "per_shape": per_shape,
+        "configs": configs,
         "prefill": prefill,
         "moe": moe,
         "rmsnorm_fused": rms,

@@ -28,6 +28,11 @@
  *                         that zero-point AWQ experts take after dequantizing
  *                         (vllm/model_executor/models/gemma4/moe.py:566-623)
  *   awq_w4a16_moe_route <- the routing of fused_moe.py:12-15 / gemma4/moe.py:106-116
+ *   awq_w4a16_moe_route_ex <- the same with the reference's dtype flows: fused_moe's softmax in
+ *                         the logits dtype (fused_moe.py:12-15) and the Gemma4 router's fp32
+ *                         softmax with weights cast to the hidden dtype (gemma4/moe.py:106-123)
+ *   awq_w4a16_gemm_rows_exact <- _packed_int4_symmetric_group32_gemv_rows_exact_msmall
+ *                         (vllm/kernels/triton/awq_fused_gemm.py:1066-1143, 2925-2998)
  *   awq_w4a16_moe_pack_stream <- no kernel in the reference: the expert-major weight prepack the
  *                         grouped kernels read (the reference reads its [E, N, K/8] stacks directly)
  *   awq_w4a16_rmsnorm_gemm <- rmsnorm_awq_fused_linear / rmsnorm_awq_fused_kernel
@@ -139,6 +144,21 @@ int awq_w4a16_gemm(const void* a, int64_t lda, const int32_t* qweight, const voi
                    int32_t act_dtype, int32_t scale_dtype, int32_t bias_dtype, void* workspace,
                    size_t workspace_bytes, void* stream);
 
+/* Row-exact GEMM: C[m, :] for every m < M equals, bit for bit, what awq_w4a16_gemm computes for
+ * the single row A[m, :] with the same arguments (M = 1): each row goes through the M = 1 plan,
+ * kernel and reduction order, whatever M is, so a row's result never depends on the batch it
+ * rides in.  Replaces _packed_int4_symmetric_group32_gemv_rows_exact_msmall (launched by
+ * packed_int4_symmetric_group32_rows_exact_msmall_safe, vllm/kernels/triton/awq_fused_gemm.py:
+ * 1066-1143, 2925-2998), whose contract is that M = 2 / 4 rows equal independent M = 1 calls
+ * (tests/test_awq_fused_gemm_numerics.py:128-161); here for any M, group size and layout the
+ * M = 1 call takes.  Arguments and requirements as awq_w4a16_gemm; the workspace is the M = 1
+ * call's (awq_w4a16_gemm_workspace_bytes(1, ...)).  One launch per row, in row order. */
+int awq_w4a16_gemm_rows_exact(const void* a, int64_t lda, const int32_t* qweight, const void* scales,
+                              const int32_t* qzeros, const void* bias, void* c, int64_t ldc, int64_t M,
+                              int64_t N, int64_t K, int32_t group_size, int32_t split_k, int32_t layout,
+                              int32_t act_dtype, int32_t scale_dtype, int32_t bias_dtype, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
 /* Lossless repack of a reference-layout (NK_SEQ) weight into the AUTOAWQ layout:
  *   qweight_nk [N, K/8] -> qweight_kn [K, N/8];  qzeros_nk [N, ceil(K/G/8)] -> qzeros_kn [K/G, N/8]
  *   (qzeros may be NULL);  scales_nk [N, K/G] -> scales_kn [K/G, N] (2-byte elements). */
@@ -194,6 +214,27 @@ int awq_w4a16_moe_pack_stream(const int32_t* qweight_ekn, int32_t* out, int64_t 
 int awq_w4a16_moe_route(const void* logits, int64_t ld, int32_t logits_dtype, int64_t T, int32_t E,
                         int32_t top_k, int32_t renormalize, float* topk_weights, int32_t* topk_ids,
                         void* stream);
+
+/* Routing flags of awq_w4a16_moe_route_ex. */
+#define AWQ_ROUTE_RENORMALIZE 1u             /* w = p / (sum of the selected p) */
+#define AWQ_ROUTE_SOFTMAX_IN_LOGITS_DTYPE 2u /* fused_moe's flow for 16-bit logits (below) */
+#define AWQ_ROUTE_CLAMP_SUM 4u               /* renormalise by max(sum, 1e-8) (the Gemma4 router) */
+
+/* Routing with the reference's two dtype flows:
+ *  - without AWQ_ROUTE_SOFTMAX_IN_LOGITS_DTYPE (or for F32 logits): the Gemma4 router
+ *    (vllm/model_executor/models/gemma4/moe.py:106-123): p = softmax(fp32(logits)) in fp32,
+ *    top_k in descending order (equal p: lower expert id first), w = p / sum (with
+ *    AWQ_ROUTE_CLAMP_SUM: / max(sum, 1e-8)) in fp32, then w converted to weights_dtype
+ *    (round to nearest even; the router casts to the hidden dtype, moe.py:123);
+ *  - with it: fused_moe (vllm/model_executor/layers/fused_moe/fused_moe.py:12-15) on 16-bit
+ *    logits: p = softmax(logits) rounded once to the logits dtype (correctly rounded: exp and
+ *    sum in fp64), top_k on those values (ties: lower expert id first), and with
+ *    AWQ_ROUTE_RENORMALIZE w = dt(fp32(p) / fp32(dt(sum of the selected p))), torch's 16-bit
+ *    arithmetic; stored in weights_dtype (exactly, for the logits dtype or F32).
+ * topk_weights: [T, top_k] of weights_dtype (F32, F16 or BF16); topk_ids: [T, top_k] int32. */
+int awq_w4a16_moe_route_ex(const void* logits, int64_t ld, int32_t logits_dtype, int64_t T, int32_t E,
+                           int32_t top_k, uint32_t flags, void* topk_weights, int32_t weights_dtype,
+                           int32_t* topk_ids, void* stream);
 
 /* Workspace bytes of awq_w4a16_moe (route lists, the intermediate and per-route fp32 rows). */
 size_t awq_w4a16_moe_workspace_bytes(int64_t T, int64_t H, int64_t I, int32_t E, int32_t top_k);

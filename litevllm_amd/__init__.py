@@ -17,6 +17,7 @@ from .awq_fused_gemm import (  # noqa: F401
     packed_int4_symmetric_fused_qkv_m2_safe,
     packed_int4_symmetric_fused_gemm,
     packed_int4_symmetric_fused_gemm_safe,
+    packed_int4_symmetric_group32_rows_exact_msmall_safe,
 )
 from .awq_triton import (  # noqa: F401
     awq_dequantize_triton,

@@ -53,6 +53,11 @@ SIGNATURES = {
     "awq_w4a16_moe_pack_stream": (ctypes.c_int, [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_p]),
     "awq_w4a16_moe_route": (ctypes.c_int, [_c_p, _c_i64, _c_i32, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_p,
                                            _c_p]),
+    "awq_w4a16_moe_route_ex": (ctypes.c_int, [_c_p, _c_i64, _c_i32, _c_i64, _c_i32, _c_i32, ctypes.c_uint32,
+                                              _c_p, _c_i32, _c_p, _c_p]),
+    "awq_w4a16_gemm_rows_exact": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64,
+                                                 _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
+                                                 _c_i32, _c_p, _c_sz, _c_p]),
     "awq_w4a16_moe_workspace_bytes": (_c_sz, [_c_i64, _c_i64, _c_i64, _c_i32, _c_i32]),
     "awq_w4a16_moe": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_i32, _c_p, _c_i32, _c_p, _c_p, _c_p, _c_p, _c_p,
                                      _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32,
@@ -72,6 +77,10 @@ SIGNATURES = {
 
 MOE_ACT_SILU = 0
 MOE_ACT_GELU_TANH = 1
+
+ROUTE_RENORMALIZE = 1
+ROUTE_SOFTMAX_IN_LOGITS_DTYPE = 2
+ROUTE_CLAMP_SUM = 4
 
 _lock = threading.Lock()
 _lib = None

@@ -155,6 +155,10 @@ def awq_fused_gemm_safe(a, qweight, scales, qzeros, group_size, out=None, bias=N
         return a, False, r
     m = int(a.shape[0])
     n = ops.gemm_dims(qweight, layout)[1]
+    if out is not None:
+        r = ops.out_problem(out, m, n, a)
+        if r:  # checked before the launch: the kernels would write M x N values into it
+            return a, False, r
     try:
         c = awq_fused_gemm(a.contiguous(), qweight.contiguous(), scales.contiguous(),
                            qzeros.contiguous(), group_size=group_size, out=out,
@@ -179,6 +183,10 @@ def packed_int4_symmetric_fused_gemm_safe(a, qweight, scales, group_size, out=No
         return a, False, r
     m = int(a.shape[0])
     n = ops.gemm_dims(qweight, layout)[1]
+    if out is not None:
+        r = ops.out_problem(out, m, n, a)
+        if r:
+            return a, False, r
     try:
         c = packed_int4_symmetric_fused_gemm(
             a.contiguous(), qweight.contiguous(), scales.contiguous(), group_size=group_size,
@@ -186,6 +194,42 @@ def packed_int4_symmetric_fused_gemm_safe(a, qweight, scales, group_size, out=No
             policy=policy, layout=layout)
         if c.shape != (m, n):
             return c, False, "bad_output_shape"
+        return c, True, "ok"
+    except Exception:
+        return a, False, "kernel_exception"
+
+
+def packed_int4_symmetric_group32_rows_exact_msmall_safe(a, qweight, scales, group_size, out=None, bias=None
+                                                         ) -> tuple[torch.Tensor, bool, str]:
+    """Row-exact M = 2 / 4 symmetric group-32 GEMM (``awq_fused_gemm.py:2925-2998``): every row
+    equals, bit for bit, the M = 1 call on that row alone (``ops.gemm_rows_exact``: each row
+    runs the M = 1 plan and kernel).  Same checks, order and reasons as the reference; never
+    raises.  Reference layout (``qweight [N, K/8]``, ``scales [N, K/32]``)."""
+    if a.dim() != 2 or int(a.shape[0]) not in (2, 4):
+        return a, False, "input_not_m2_or_m4_2d"
+    if qweight.dim() != 2 or scales.dim() != 2:
+        return a, False, "weight_or_scales_not_2d"
+    m, k = int(a.shape[0]), int(a.shape[1])
+    n = int(qweight.shape[0])
+    if int(group_size) != 32 or k % 32 != 0:
+        return a, False, "unsupported_group_layout"
+    if k != int(qweight.shape[1]) * 8:
+        return a, False, "k_mismatch"
+    if tuple(scales.shape) != (n, k // 32):
+        return a, False, "scales_shape_mismatch"
+    if a.device != qweight.device or a.device != scales.device or a.dtype not in (torch.float16, torch.bfloat16):
+        return a, False, "tensor_device_or_dtype"
+    if bias is not None and (bias.dim() != 1 or int(bias.numel()) != n or bias.device != a.device
+                             or bias.dtype not in (torch.float16, torch.bfloat16, torch.float32)):
+        return a, False, "bias_layout_or_dtype"
+    if not (a.is_contiguous() and qweight.is_contiguous() and scales.is_contiguous()):
+        return a, False, "noncontiguous_input"
+    if out is not None and (tuple(out.shape) != (m, n) or out.device != a.device or out.dtype != a.dtype
+                            or out.stride(1) != 1):
+        return a, False, "bad_output"
+    try:
+        qw = qweight if qweight.dtype == torch.int32 else qweight.to(torch.int32)
+        c = ops.gemm_rows_exact(a, qw, scales, None, 32, bias=bias, layout="ref", out=out)
         return c, True, "ok"
     except Exception:
         return a, False, "kernel_exception"

@@ -146,6 +146,26 @@ int awq_w4a16_gemm(const void* a, int64_t lda, const int32_t* qweight, const voi
   return launch_status();
 }
 
+int awq_w4a16_gemm_rows_exact(const void* a, int64_t lda, const int32_t* qweight, const void* scales,
+                              const int32_t* qzeros, const void* bias, void* c, int64_t ldc, int64_t M,
+                              int64_t N, int64_t K, int32_t group_size, int32_t split_k, int32_t layout,
+                              int32_t act_dtype, int32_t scale_dtype, int32_t bias_dtype, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  if (!a || !c) return AWQ_ERR_NULL;
+  if (M < 0) return AWQ_ERR_SHAPE;
+  if (M == 0 || N == 0) return AWQ_OK;
+  if (M > 1 && (lda < K || ldc < N)) return AWQ_ERR_STRIDE;
+  const int64_t ebytes = 2;  // both activation dtypes are 16-bit
+  for (int64_t m = 0; m < M; ++m) {
+    // row m as an M = 1 call: the same plan, kernel and reduction order as a lone row
+    const int rc = awq_w4a16_gemm((const char*)a + m * lda * ebytes, lda, qweight, scales, qzeros, bias,
+                                  (char*)c + m * ldc * ebytes, ldc, 1, N, K, group_size, split_k, layout,
+                                  act_dtype, scale_dtype, bias_dtype, workspace, workspace_bytes, stream);
+    if (rc != AWQ_OK) return rc;
+  }
+  return AWQ_OK;
+}
+
 int awq_w4a16_repack_nk_to_autoawq(const int32_t* qweight_nk, const int32_t* qzeros_nk,
                                    const void* scales_nk, int32_t* qweight_kn, int32_t* qzeros_kn,
                                    void* scales_kn, int64_t N, int64_t K, int32_t group_size,
@@ -202,7 +222,24 @@ int awq_w4a16_moe_route(const void* logits, int64_t ld, int32_t logits_dtype, in
     return AWQ_ERR_UNSUPPORTED;
   if (T < 0 || E <= 0 || E > 256 || top_k <= 0 || top_k > E || top_k > 64) return AWQ_ERR_SHAPE;
   if (ld < E) return AWQ_ERR_STRIDE;
-  return launch_moe_route(logits, ld, logits_dtype, T, E, top_k, renormalize ? 1 : 0, topk_weights, topk_ids,
+  return launch_moe_route(logits, ld, logits_dtype, T, E, top_k,
+                          renormalize ? (uint32_t)(AWQ_ROUTE_RENORMALIZE | AWQ_ROUTE_CLAMP_SUM) : 0u, topk_weights,
+                          AWQ_DTYPE_F32, topk_ids, (hipStream_t)stream);
+}
+
+int awq_w4a16_moe_route_ex(const void* logits, int64_t ld, int32_t logits_dtype, int64_t T, int32_t E,
+                           int32_t top_k, uint32_t flags, void* topk_weights, int32_t weights_dtype,
+                           int32_t* topk_ids, void* stream) {
+  if (!logits || !topk_weights || !topk_ids) return AWQ_ERR_NULL;
+  if (logits_dtype != AWQ_DTYPE_F16 && logits_dtype != AWQ_DTYPE_BF16 && logits_dtype != AWQ_DTYPE_F32)
+    return AWQ_ERR_UNSUPPORTED;
+  if (weights_dtype != AWQ_DTYPE_F16 && weights_dtype != AWQ_DTYPE_BF16 && weights_dtype != AWQ_DTYPE_F32)
+    return AWQ_ERR_UNSUPPORTED;
+  if ((flags & ~(uint32_t)(AWQ_ROUTE_RENORMALIZE | AWQ_ROUTE_SOFTMAX_IN_LOGITS_DTYPE | AWQ_ROUTE_CLAMP_SUM)) != 0)
+    return AWQ_ERR_UNSUPPORTED;
+  if (T < 0 || E <= 0 || E > 256 || top_k <= 0 || top_k > E || top_k > 64) return AWQ_ERR_SHAPE;
+  if (ld < E) return AWQ_ERR_STRIDE;
+  return launch_moe_route(logits, ld, logits_dtype, T, E, top_k, flags, topk_weights, weights_dtype, topk_ids,
                           (hipStream_t)stream);
 }
 

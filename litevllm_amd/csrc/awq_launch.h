@@ -83,8 +83,8 @@ int64_t moe_tiles(int64_t N, int gate_up);
 int64_t moe_stream_bytes(int64_t E, int64_t K, int64_t N, int gate_up);
 int launch_moe_pack_stream(const int32_t* in, int32_t* out, int64_t E, int64_t K, int64_t N, int gate_up,
                            hipStream_t st);
-int launch_moe_route(const void* logits, int64_t ld, int dtype, int64_t T, int E, int topk, int renorm,
-                     float* out_w, int32_t* out_ids, hipStream_t st);
+int launch_moe_route(const void* logits, int64_t ld, int dtype, int64_t T, int E, int topk, uint32_t flags,
+                     void* out_w, int w_dtype, int32_t* out_ids, hipStream_t st);
 
 // Workspace of one MoE call (byte offsets): route counts [E] and lists [E][R] (int32), the
 // intermediate [R][I] (activation dtype) and the per-route down outputs [R][H] (fp32).

@@ -22,15 +22,41 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// Routing of one token per wave, in fp32 as the Gemma4 router does (models/gemma4/moe.py:106-116):
-// p = softmax(logits); the top_k largest p (ties: lower expert id first) in descending order;
-// with renormalize, w = p / max(sum of the selected p in that order, 1e-8).  E <= 256.
+// x (> 0, finite) rounded once to fp16 (dt F16) or bf16 (dt BF16), returned as fp32: the double
+// is first rounded to fp32 toward zero with the inexact bit kept in the last place (round to
+// odd), which leaves the second rounding to nearest-even the correctly rounded result (fp32
+// carries more than two bits beyond either 16-bit format, subnormal fp16 included).
+__device__ __forceinline__ float round_prob(double x, int dt) {
+  float f = (float)x;
+  if ((double)f != x) {
+    uint32_t b = __float_as_uint(f);
+    if ((double)f > x) b -= 1;  // positive: the nearest fp32 at or below x
+    f = __uint_as_float(b | 1u);
+  }
+  return dt == AWQ_DTYPE_F16 ? h_bits2f(f2h_bits(f)) : bf_bits2f(f2bf_bits(f));
+}
+__device__ __forceinline__ float round_to(float x, int dt) {
+  if (dt == AWQ_DTYPE_F16) return h_bits2f(f2h_bits(x));
+  if (dt == AWQ_DTYPE_BF16) return bf_bits2f(f2bf_bits(x));
+  return x;
+}
+
+// Routing of one token per wave (E <= 256), two dtype flows:
+//  * fp32 (the Gemma4 router, models/gemma4/moe.py:106-116): p = softmax(fp32(logits)) in fp32;
+//    the top_k largest p (ties: lower expert id first) in descending order; with renormalize,
+//    w = p / sum (or / max(sum, 1e-8) with AWQ_ROUTE_CLAMP_SUM), the sum taken in slot order;
+//  * AWQ_ROUTE_SOFTMAX_IN_LOGITS_DTYPE (fused_moe.py:12-15, 16-bit logits): p = softmax(logits)
+//    rounded once to the logits dtype (exp and sum in fp64, so p is the correctly rounded
+//    quotient), top-k on those values, and w = dt(fp32(p) / fp32(dt(sum of the selected p))),
+//    torch's arithmetic for 16-bit tensors (fp32 math, one rounding per operation).
+// out_w receives w in w_dtype (F32, F16 or BF16; RNE from fp32).
 __global__ void __launch_bounds__(256) moe_route_kernel(const void* logits, int64_t ld, int dtype, int64_t T,
-                                                        int E, int topk, int renorm, float* out_w,
+                                                        int E, int topk, uint32_t flags, void* out_w, int w_dtype,
                                                         int32_t* out_ids) {
   const int lane = threadIdx.x & 63;
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;  // whole wave
+  const bool in_dt = (flags & AWQ_ROUTE_SOFTMAX_IN_LOGITS_DTYPE) && dtype != AWQ_DTYPE_F32;
   float v[4];
   float mx = -INFINITY;
 #pragma unroll
@@ -40,16 +66,29 @@ __global__ void __launch_bounds__(256) moe_route_kernel(const void* logits, int6
     mx = fmaxf(mx, v[j]);
   }
   mx = wave_max(mx);
-  float s = 0.f;
+  if (in_dt) {
+    double ev[4], sd = 0.0;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int e = lane + 64 * j;
-    v[j] = e < E ? expf(v[j] - mx) : 0.f;
-    s += v[j];
+    for (int j = 0; j < 4; ++j) {
+      const int e = lane + 64 * j;
+      ev[j] = e < E ? exp((double)v[j] - (double)mx) : 0.0;  // v - mx exact in fp64
+      sd += ev[j];
+    }
+    sd = wave_sum_f64(sd);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = (lane + 64 * j) < E ? round_prob(ev[j] / sd, dtype) : -1.f;
+  } else {
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = lane + 64 * j;
+      v[j] = e < E ? expf(v[j] - mx) : 0.f;
+      s += v[j];
+    }
+    s = wave_sum(s);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = (lane + 64 * j) < E ? v[j] / s : -1.f;  // -1: not selectable
   }
-  s = wave_sum(s);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) v[j] = (lane + 64 * j) < E ? v[j] / s : -1.f;  // -1: not selectable
   float mine = 0.f, sel_sum = 0.f;
   int mine_id = 0;
   if (E <= 64) {
@@ -92,8 +131,18 @@ __global__ void __launch_bounds__(256) moe_route_kernel(const void* logits, int6
     sel_sum += bv;
   }
   if (lane < topk) {
-    out_w[t * topk + lane] = renorm ? mine / fmaxf(sel_sum, 1e-8f) : mine;
-    out_ids[t * topk + lane] = mine_id;
+    float w = mine;
+    if (flags & AWQ_ROUTE_RENORMALIZE) {
+      if (in_dt) {
+        w = round_to(mine / round_to(sel_sum, dtype), dtype);
+      } else {
+        w = mine / ((flags & AWQ_ROUTE_CLAMP_SUM) ? fmaxf(sel_sum, 1e-8f) : sel_sum);
+      }
+    }
+    const int64_t o = t * topk + lane;
+    if (w_dtype == AWQ_DTYPE_F32) ((float*)out_w)[o] = w;
+    else ((uint16_t*)out_w)[o] = w_dtype == AWQ_DTYPE_F16 ? f2h_bits(w) : f2bf_bits(w);
+    out_ids[o] = mine_id;
   }
 }
 
@@ -232,11 +281,11 @@ int launch_moe_pack_stream(const int32_t* in, int32_t* out, int64_t E, int64_t K
   return launch_status();
 }
 
-int launch_moe_route(const void* logits, int64_t ld, int dtype, int64_t T, int E, int topk, int renorm,
-                     float* out_w, int32_t* out_ids, hipStream_t st) {
+int launch_moe_route(const void* logits, int64_t ld, int dtype, int64_t T, int E, int topk, uint32_t flags,
+                     void* out_w, int w_dtype, int32_t* out_ids, hipStream_t st) {
   if (T == 0) return AWQ_OK;
   hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)cdiv(T, 4)), dim3(256), 0, st, logits, ld, dtype, T, E, topk,
-                     renorm, out_w, out_ids);
+                     flags, out_w, w_dtype, out_ids);
   return launch_status();
 }
 

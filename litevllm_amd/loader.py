@@ -57,11 +57,31 @@ def detect_layout(qweight: torch.Tensor, scales: torch.Tensor) -> tuple[str, int
     raise ValueError(f"cannot tell the layout of qweight {tuple(qweight.shape)} with scales {tuple(scales.shape)}")
 
 
+def unsigned_zero_points(z: torch.Tensor) -> torch.Tensor:
+    """Unpacked zero points as the unsigned nibbles 0..15 the packed weights are offset to.
+
+    An ``int8`` tensor holds the signed int4 convention of compressed-tensors checkpoints (zero
+    points in [-8, 7], the packed weights stored with +8): each value is shifted by +8, so that
+    ``q_u - z_u == q - z``.  Any other integer dtype holds unsigned values, which must lie in
+    [0, 15].  Out-of-range values raise ``ValueError`` (they cannot be packed into a nibble)."""
+    if z.dtype.is_floating_point or z.dtype == torch.bool:
+        raise ValueError(f"zero points must be an integer tensor, got {z.dtype}")
+    zi = z.to(torch.int64)
+    if z.dtype == torch.int8:
+        lo, hi, off = -8, 7, 8
+    else:
+        lo, hi, off = 0, 15, 0
+    if zi.numel() and (int(zi.min()) < lo or int(zi.max()) > hi):
+        raise ValueError(f"unpacked zero points of dtype {z.dtype} must lie in [{lo}, {hi}], got "
+                         f"[{int(zi.min())}, {int(zi.max())}]")
+    return zi + off
+
+
 def _pack_groups(z: torch.Tensor) -> torch.Tensor:
     """Unpacked zero points [N, K/G] -> the reference's packed [N, ceil(K/G/8)] (nibble i of
-    word j is group 8j + i)."""
+    word j is group 8j + i), after :func:`unsigned_zero_points`."""
     n, g = int(z.shape[0]), int(z.shape[1])
-    z = z.to(torch.int64) & 0xF
+    z = unsigned_zero_points(z)
     pad = (-g) % 8
     if pad:
         z = torch.cat([z, z.new_zeros((n, pad))], 1)

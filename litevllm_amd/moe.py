@@ -8,7 +8,9 @@
   AutoAWQ expert layout.
 * :func:`fused_moe` mirrors ``vllm/model_executor/layers/fused_moe/fused_moe.py:4-77`` for
   int4 AWQ experts (:class:`AWQExperts`): routing, the gated expert MLP, the weighted sum.
-* :func:`moe_route` is the routing alone (``fused_moe.py:12-15``, ``gemma4/moe.py:106-116``).
+* :func:`moe_route` is the routing alone: ``flow="logits"`` is ``fused_moe.py:12-15``'s dtype flow,
+  ``flow="fp32"`` the Gemma4 router's (``gemma4/moe.py:106-123``, weights cast to the hidden
+  dtype with ``weights_dtype``).
 
 Every byte of arithmetic runs in ``libawq_w4a16.so``; there is no CPU or eager fallback.
 """
@@ -193,9 +195,10 @@ def fused_moe(hidden_states: torch.Tensor, w1: AWQExperts, w2: AWQExperts, gatin
     """``fused_moe`` (``fused_moe.py:4-77``) for int4 AWQ experts: ``w1`` the gate_up stack
     ``[E, 2I, H]`` (unpacked orientation), ``w2`` the down stack ``[E, H, I]``.
 
-    Routing runs in fp32 (:func:`moe_route`); the reference's ``fused_moe`` takes the softmax
-    in the logits dtype.  Dense fp16 expert tensors are outside the W4A16 path and raise
-    ``TypeError``."""
+    Routing follows the reference's dtype flow (``fused_moe.py:12-15``): the softmax rounded to
+    the logits dtype, top-k on those values, renormalisation in that dtype, weights in that
+    dtype (:func:`moe_route` with ``flow="logits"``).  Dense fp16 expert tensors are outside the
+    W4A16 path and raise ``TypeError``."""
     if not isinstance(w1, AWQExperts) or not isinstance(w2, AWQExperts):
         raise TypeError("fused_moe here takes int4 AWQ expert stacks (AWQExperts) for w1 and w2")
     _, _, n1 = w1.dims()
@@ -206,5 +209,5 @@ def fused_moe(hidden_states: torch.Tensor, w1: AWQExperts, w2: AWQExperts, gatin
                          "of fused_moe.py:52-53 is not provided")
     if n2 != int(hidden_states.shape[1]):
         raise ValueError("w2 rows must equal the hidden size")
-    tw, tid = moe_route(gating_output, topk, renormalize)
+    tw, tid = moe_route(gating_output, topk, renormalize, flow="logits")
     return awq_moe(hidden_states, tw, tid, w1, w2, intermediate_dim=inter, activation="silu")

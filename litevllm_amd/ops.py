@@ -201,10 +201,16 @@ class _Workspace:
     region at zero, so a buffer is zeroed only when it is (re)allocated.  Calls are
     serialised on the caller's stream (the reference issues every AWQ matmul from one
     engine thread on the current stream); work on two streams at once needs
-    ``reserve(device, nbytes, key)`` with distinct keys."""
+    ``reserve(device, nbytes, key)`` with distinct keys.
+
+    A buffer that has been handed out is never freed: when a larger one is needed, the old
+    one stays alive (``_retired``), because HIP graphs captured earlier hold its address and
+    write their counters and partials into it on every replay.  ``reserve`` the largest size
+    up front to avoid regrowth altogether."""
 
     def __init__(self):
         self._bufs: dict = {}
+        self._retired: list = []
         self._lock = threading.Lock()
 
     def get(self, device: torch.device, nbytes: int, key=None) -> torch.Tensor:
@@ -212,6 +218,8 @@ class _Workspace:
         with self._lock:
             buf = self._bufs.get(k)
             if buf is None or buf.numel() < nbytes:
+                if buf is not None:
+                    self._retired.append(buf)
                 size = max(nbytes, 16 << 20)
                 buf = torch.zeros(size, dtype=torch.uint8, device=device)
                 self._bufs[k] = buf
@@ -224,6 +232,26 @@ WORKSPACE = _Workspace()
 
 
 # ------------------------------------------------------------------ GEMM
+def out_problem(out: torch.Tensor, M: int, N: int, a: torch.Tensor) -> str | None:
+    """Why a caller-supplied ``out`` cannot take an ``[M, N]`` result of ``a``'s dtype (the
+    kernels write M x N 16-bit values at row stride ``out.stride(0)``), or None."""
+    if tuple(out.shape) != (M, N):
+        return "bad_output_shape"
+    if out.dtype != a.dtype or out.device != a.device:
+        return "bad_output"
+    if N > 0 and M > 0 and (out.stride(1) != 1 or (M > 1 and out.stride(0) < N)):
+        return "bad_output"
+    return None
+
+
+def check_out(out: torch.Tensor, M: int, N: int, a: torch.Tensor) -> None:
+    """Raise ``ValueError`` before any launch when ``out`` cannot take the result."""
+    why = out_problem(out, M, N, a)
+    if why is not None:
+        raise ValueError(f"{why}: out must be [{M}, {N}] {a.dtype} on {a.device} with unit column "
+                         f"stride, got {tuple(out.shape)} {out.dtype} on {out.device}, strides {out.stride()}")
+
+
 DECODE_MAX_M = 32
 DECODE_GROUPS = (32, 64, 128)
 
@@ -294,6 +322,8 @@ def gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, qzeros: t
     a = a.contiguous()
     if out is None:
         out = torch.empty((M, N), dtype=a.dtype, device=a.device)
+    else:
+        check_out(out, M, N, a)
     if bias is not None:
         bias = bias.contiguous()
     dev = a.device
@@ -306,6 +336,43 @@ def gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, qzeros: t
         dtype_code(scales.dtype), dtype_code(bias.dtype) if bias is not None else L.DTYPE_NONE,
         _ptr(ws), ws_bytes if ws is not None else 0, stream)
     L.check("awq_w4a16_gemm", rc)
+    return out
+
+
+def gemm_rows_exact(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, qzeros: torch.Tensor | None,
+                    group_size: int, bias: torch.Tensor | None = None, split_k: int = 0, layout: str = "ref",
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """``gemm`` with every row computed exactly as a lone ``M = 1`` call computes it (the same
+    weight copy, plan, kernel and reduction order), so ``out[m]`` equals ``gemm(a[m:m+1], ...)``
+    bit for bit whatever the batch -- the contract of the reference's row-exact small-batch
+    kernel (``awq_fused_gemm.py:1066-1143``)."""
+    lib = L.load()
+    if a.dim() != 2:
+        raise ValueError("a must be 2-D")
+    _require_device(a, qweight, scales, qzeros, bias, out)
+    K, N = gemm_dims(qweight, layout)
+    M = int(a.shape[0])
+    if int(a.shape[1]) != K:
+        raise ValueError(f"K mismatch: a has {a.shape[1]}, weight has {K}")
+    # the weight copy and plan of an M = 1 call
+    qweight, scales, qzeros, lc = _kernel_weight(qweight, scales, qzeros, group_size, layout, 1, N, K,
+                                                 split_k, None, None)
+    a = a.contiguous()
+    if out is None:
+        out = torch.empty((M, N), dtype=a.dtype, device=a.device)
+    else:
+        check_out(out, M, N, a)
+    if bias is not None:
+        bias = bias.contiguous()
+    dev = a.device
+    ws_bytes = int(lib.awq_w4a16_gemm_workspace_bytes(1, N, K, int(group_size), int(split_k), lc))
+    ws = WORKSPACE.get(dev, ws_bytes) if ws_bytes else None
+    rc = lib.awq_w4a16_gemm_rows_exact(
+        _ptr(a), int(a.stride(0)), _ptr(qweight), _ptr(scales), _ptr(qzeros), _ptr(bias), _ptr(out),
+        int(out.stride(0)), M, N, K, int(group_size), int(split_k), lc, dtype_code(a.dtype),
+        dtype_code(scales.dtype), dtype_code(bias.dtype) if bias is not None else L.DTYPE_NONE,
+        _ptr(ws), ws_bytes if ws is not None else 0, _stream_ptr(dev))
+    L.check("awq_w4a16_gemm_rows_exact", rc)
     return out
 
 
@@ -347,6 +414,8 @@ def rmsnorm_gemm(x: torch.Tensor, norm_w: torch.Tensor, eps: float, qweight: tor
     x, norm_w = x.contiguous(), norm_w.contiguous()
     if out is None:
         out = torch.empty((M, N), dtype=x.dtype, device=dev)
+    else:
+        check_out(out, M, N, x)
     ws_bytes = int(lib.awq_w4a16_rmsnorm_gemm_workspace_bytes(M, N, K, int(group_size), int(split_k), lc,
                                                               dtype_code(x.dtype)))
     ws = WORKSPACE.get(dev, ws_bytes)
@@ -458,8 +527,8 @@ def gate_up_act(x: torch.Tensor, gate_qweight: torch.Tensor, up_qweight: torch.T
     x = x if x.stride(1) == 1 and x.stride(0) % 8 == 0 else x.contiguous()
     if out is None:
         out = torch.empty((M, I), dtype=x.dtype, device=dev)
-    if out.stride(1) != 1:
-        raise ValueError("out must have unit column stride")
+    else:
+        check_out(out, M, I, x)
     ws_bytes = int(lib.awq_w4a16_gate_up_workspace_bytes(M, I, K, int(group_size), int(split_k), lc))
     ws = WORKSPACE.get(dev, ws_bytes) if ws_bytes else None
     rc = lib.awq_w4a16_gate_up_act(
@@ -475,20 +544,36 @@ MOE_ACTIVATIONS = {"silu": L.MOE_ACT_SILU, "swish": L.MOE_ACT_SILU,
                    "gelu": L.MOE_ACT_GELU_TANH, "gelu_pytorch_tanh": L.MOE_ACT_GELU_TANH}
 
 
-def moe_route(gating_output: torch.Tensor, topk: int, renormalize: bool = True):
-    """softmax -> top-k -> renormalise in fp32 on the device: ``(weights fp32, ids int32)``,
-    each ``[T, topk]``; equal probabilities select the lower expert id first."""
+def moe_route(gating_output: torch.Tensor, topk: int, renormalize: bool = True, *, flow: str = "fp32",
+              weights_dtype: torch.dtype | None = None, clamp: bool | None = None):
+    """softmax -> top-k -> renormalise on the device: ``(weights, ids int32)``, each ``[T, topk]``;
+    equal probabilities select the lower expert id first.
+
+    ``flow="fp32"``: the Gemma4 router (``models/gemma4/moe.py:106-123``): fp32 softmax and
+    renormalisation by ``max(sum, 1e-8)`` (``clamp``, default on), weights in ``weights_dtype``
+    (default fp32; the router casts them to the hidden dtype).  ``flow="logits"``: ``fused_moe``
+    (``fused_moe.py:12-15``): the softmax rounded to the logits dtype, top-k on those values,
+    renormalisation in that dtype without a clamp; weights default to the logits dtype."""
     lib = L.load()
     dev = _require_device(gating_output)
     if gating_output.dim() != 2:
         raise ValueError("gating_output must be [T, E]")
+    if flow not in ("fp32", "logits"):
+        raise ValueError(f"unknown routing flow {flow!r}")
     g = gating_output if gating_output.stride(1) == 1 else gating_output.contiguous()
     T, E = int(g.shape[0]), int(g.shape[1])
-    w = torch.empty((T, int(topk)), dtype=torch.float32, device=dev)
+    in_dt = flow == "logits"
+    if weights_dtype is None:
+        weights_dtype = g.dtype if in_dt else torch.float32
+    if clamp is None:
+        clamp = not in_dt
+    flags = (L.ROUTE_RENORMALIZE if renormalize else 0) | (L.ROUTE_SOFTMAX_IN_LOGITS_DTYPE if in_dt else 0)
+    flags |= L.ROUTE_CLAMP_SUM if (clamp and renormalize) else 0
+    w = torch.empty((T, int(topk)), dtype=weights_dtype, device=dev)
     ids = torch.empty((T, int(topk)), dtype=torch.int32, device=dev)
-    rc = lib.awq_w4a16_moe_route(_ptr(g), int(g.stride(0)), dtype_code(g.dtype), T, E, int(topk),
-                                 1 if renormalize else 0, _ptr(w), _ptr(ids), _stream_ptr(dev))
-    L.check("awq_w4a16_moe_route", rc)
+    rc = lib.awq_w4a16_moe_route_ex(_ptr(g), int(g.stride(0)), dtype_code(g.dtype), T, E, int(topk), flags,
+                                    _ptr(w), dtype_code(weights_dtype), _ptr(ids), _stream_ptr(dev))
+    L.check("awq_w4a16_moe_route_ex", rc)
     return w, ids
 
 
@@ -569,6 +654,8 @@ def moe(x: torch.Tensor, topk_weights: torch.Tensor, topk_ids: torch.Tensor,
     dn = prepare_moe_stream(down_qweight, False)
     if out is None:
         out = torch.empty((T, H), dtype=x.dtype, device=dev)
+    else:
+        check_out(out, T, H, x)
     if T == 0:
         return out
     ws_bytes = int(lib.awq_w4a16_moe_workspace_bytes(T, H, I, E, topk))

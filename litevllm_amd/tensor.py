@@ -20,7 +20,8 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import ops
-from .awq_fused_gemm import awq_fused_gemm_safe, packed_int4_symmetric_fused_gemm_safe
+from .awq_fused_gemm import (awq_fused_gemm_safe, packed_int4_symmetric_fused_gemm_safe,
+                             packed_int4_symmetric_group32_rows_exact_msmall_safe)
 
 _STATS: dict[str, int] = defaultdict(int)
 _PREFIX_STATS: dict[str, dict[str, int]] = defaultdict(lambda: defaultdict(int))
@@ -94,6 +95,12 @@ def _kernel_policy_value(config: Any | None, name: str, default=None):
 
 def _truthy(v) -> bool:
     return v if isinstance(v, bool) else str(v).strip().lower() in ("1", "true", "yes", "on")
+
+
+def awq_rows_exact_msmall_enabled(config: object | None = None) -> bool:
+    """Policy key ``awq_rows_exact_msmall`` (``tensor.py:401-405``), default off: M = 2 / 4 keep
+    the per-row M = 1 arithmetic."""
+    return _truthy(_kernel_policy_value(config, "awq_rows_exact_msmall", False))
 
 
 class QuantizedLinearWeight(nn.Module, ABC):
@@ -186,6 +193,25 @@ class PackedInt4Weight(AWQWeight):
         super().__init__(qweight.to(torch.int32) if qweight.dtype != torch.int32 else qweight,
                          scales, None, group_size, prefix, high_fidelity, profile_hint, layout)
         self.original_shape = original_shape
+
+    def matmul(self, x, bias=None, *, config: object | None = None):
+        """With ``awq_rows_exact_msmall`` on and M in {2, 4}, the row-exact kernel path, or on its
+        refusal one M = 1 call per row -- never the generic batched GEMM (``tensor.py:1200-1234``)."""
+        x2 = x.reshape(-1, x.shape[-1])
+        if awq_rows_exact_msmall_enabled(config) and int(x2.shape[0]) in (2, 4):
+            try:
+                out, used, reason = packed_int4_symmetric_group32_rows_exact_msmall_safe(
+                    x2.contiguous(), self.qweight, self.scales, int(self.group_size), bias=bias)
+                if used:
+                    _stat("awq_rows_exact_msmall_success")
+                    _stat("rows_exact_msmall_success", self.prefix)
+                    return out.view(*x.shape[:-1], out.shape[-1])
+                _stat(f"rows_exact_msmall_fallback:{reason}", self.prefix)
+            except Exception as exc:
+                _stat(f"rows_exact_msmall_exception:{type(exc).__name__}", self.prefix)
+            rows = [self.matmul(x2[r:r + 1], bias, config=config) for r in range(int(x2.shape[0]))]
+            return torch.cat(rows, dim=0).view(*x.shape[:-1], rows[0].shape[-1])
+        return super().matmul(x, bias, config=config)
 
     def dense_weight(self, dtype: torch.dtype = torch.float16) -> torch.Tensor:
         w = super().dense_weight(dtype)

@@ -76,13 +76,15 @@ def _expert_mlp(tokens, w1e, w2e):
 
 
 def fused_moe_cpu(hidden_states, w1, w2, gating_output=None, topk=8, renormalize=True,
-                  topk_weights=None, topk_ids=None):
+                  topk_weights=None, topk_ids=None, serialized=None):
     """Restatement of ``fused_moe`` over dense experts ``w1 [E, 2I, H]``, ``w2 [E, H, I]``.
 
     Routing may be given precomputed (``topk_weights``/``topk_ids``) so a GPU kernel
     and this oracle can be compared on identical routes. Output accumulates in the
     hidden dtype with ``index_add_`` in expert-sorted order (M <= 128, E < 256,
     H <= 4096) or per token in top-k order otherwise (``fused_moe.py:21``).
+    ``serialized`` overrides that choice (a timing sample of a large batch keeps the
+    large batch's per-token branch).
     """
     M, K = hidden_states.shape
     E = w1.shape[0]
@@ -90,7 +92,8 @@ def fused_moe_cpu(hidden_states, w1, w2, gating_output=None, topk=8, renormalize
         topk_weights, topk_ids = moe_routing_cpu(gating_output, topk, renormalize)
     topk = topk_ids.shape[1]
     out = torch.zeros_like(hidden_states)
-    serialized = E >= 256 or K > 4096 or M > 128
+    if serialized is None:
+        serialized = E >= 256 or K > 4096 or M > 128
     if not serialized:
         ids = topk_ids.reshape(-1)
         wts = topk_weights.reshape(-1)

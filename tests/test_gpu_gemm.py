@@ -247,12 +247,17 @@ def test_split_k_config2_bit_stable(M):
     p = make_awq_problem(M=M, K=K, N=N, group_size=G, seed=2)
     t = _to_dev(p)
     ye = O.linear_exact(p["x"], _w_used(p, M, G).T)
+    qr, zr, sr = O.repack_awq_to_ref(p["qweight"], p["qzeros"], p["scales"])
+    yr = R.awq_linear_cpu(torch.from_numpy(p["x"]), torch.from_numpy(qr), torch.from_numpy(sr),
+                          torch.from_numpy(zr), G).numpy()
     for sk in (1, 4, 8):
         _note(f"split-K M={M} split={sk} (AutoAWQ layout read directly)")
         y1 = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, split_k=sk, layout="autoawq", decode_stream=False)
         y2 = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, split_k=sk, layout="autoawq", decode_stream=False)
         assert torch.equal(y1.view(torch.int16), y2.view(torch.int16)), f"split {sk} not bit-stable"
         _check_vs_exact(y1.cpu().numpy(), ye, f"split {sk}")
+        # the reference's own CPU path (dequant + F.linear): max-abs / mean-relative bars
+        _check_vs_ref(y1.cpu().numpy(), yr, f"config2 M={M} split {sk} vs reference CPU path")
 
 
 @pytest.mark.parametrize("M,K,sk", [(1, 4096, 3), (4, 2080, 5), (16, 1024, 200)])
@@ -291,7 +296,7 @@ def test_config1_decode_sweep(M, N, stream):
     _check_vs_ref(y, yr, f"config1 M={M} N={N}")
 
 
-@pytest.mark.parametrize("M,N", [(512, 12288), (2048, 24576)])
+@pytest.mark.parametrize("M,N", [(512, 12288), (512, 24576), (2048, 12288), (2048, 24576)])
 def test_config3_prefill(M, N):
     """Full-size prefill: every output against a torch fp32 GEMM on the (bit-exact
     checked) dequantized weight; 128 sampled rows against the exact oracle."""
@@ -311,6 +316,12 @@ def test_config3_prefill(M, N):
     rows = np.random.default_rng(0).choice(M, size=128, replace=False)
     ye = O.linear_exact(p["x"][rows], w.T)
     _check_vs_exact(y.cpu().numpy()[rows], ye, f"config3 M={M} N={N}")
+    # 8 sampled rows against the reference's own CPU path (dequant + F.linear in fp16)
+    r8 = rows[:8]
+    qr, zr, sr = O.repack_awq_to_ref(p["qweight"], p["qzeros"], p["scales"])
+    yr = R.awq_linear_cpu(torch.from_numpy(p["x"][r8]), torch.from_numpy(qr), torch.from_numpy(sr),
+                          torch.from_numpy(zr), G).numpy()
+    _check_vs_ref(y.cpu().numpy()[r8], yr, f"config3 M={M} N={N} vs reference CPU path")
 
 
 # ------------------------------------------------------------------ decode stream layout

@@ -46,7 +46,8 @@ def test_symmetric_module_gives_packed_int4_weight():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("fmt", ["compressed_packed_zp", "compressed_unpacked_zp", "autoawq", "symmetric"])
+@pytest.mark.parametrize("fmt", ["compressed_packed_zp", "compressed_unpacked_zp", "unpacked_zp_u8", "autoawq",
+                                 "symmetric"])
 @pytest.mark.parametrize("M", [1, 40])
 def test_adapted_weight_matmul(fmt, M):
     from litevllm_amd import loader
@@ -60,7 +61,11 @@ def test_adapted_weight_matmul(fmt, M):
     elif fmt == "compressed_packed_zp":
         comps = {"qweight": t(qr), "scales": t(sr), "qzeros": t(zr)}
     elif fmt == "compressed_unpacked_zp":
-        comps = {"qweight": t(qr), "scales": t(sr), "qzeros": t(O.unpack_ref(zr)[:, : K // G].astype(np.int8))}
+        # compressed-tensors' signed int4 convention: int8 zero points in [-8, 7], weights stored +8
+        zs = O.unpack_ref(zr)[:, : K // G].astype(np.int64) - 8
+        comps = {"qweight": t(qr), "scales": t(sr), "qzeros": t(zs.astype(np.int8))}
+    elif fmt == "unpacked_zp_u8":
+        comps = {"qweight": t(qr), "scales": t(sr), "qzeros": t(O.unpack_ref(zr)[:, : K // G].astype(np.uint8))}
     else:
         comps = {"qweight": t(qr), "scales": t(sr)}
     w = loader.make_awq_weight(comps, device=DEV, prepare_decode=True)
