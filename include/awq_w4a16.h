@@ -144,6 +144,23 @@ int awq_w4a16_gemm(const void* a, int64_t lda, const int32_t* qweight, const voi
                    int32_t act_dtype, int32_t scale_dtype, int32_t bias_dtype, void* workspace,
                    size_t workspace_bytes, void* stream);
 
+/* Allocation-free GEMM: awq_w4a16_gemm's computation, bit for bit, with its split-K counters and
+ * partials in a fixed scratch array the library holds on every GPU it runs on (static device
+ * memory, awq_w4a16_gemm_noalloc_max_workspace() bytes, kept until the process ends) instead of
+ * a caller's workspace.  No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc); it calls
+ * no hipMalloc / hipFree or allocating routine.  Returns AWQ_ERR_WORKSPACE when the call would
+ * need more workspace than that array holds (awq_w4a16_gemm_workspace_bytes of the same
+ * arguments; the library's own split-K plans stay within it).  The first call on a device looks
+ * the array up and clears its counters (a kernel on `stream`).  Every call on one GPU shares
+ * that GPU's array: calls that may overlap on one GPU (other streams, other threads) race and
+ * must be serialised by the caller. */
+size_t awq_w4a16_gemm_noalloc_max_workspace(void);
+int awq_w4a16_gemm_noalloc(const void* a, int64_t lda, const int32_t* qweight, const void* scales,
+                           const int32_t* qzeros, const void* bias, void* c, int64_t ldc, int64_t M, int64_t N,
+                           int64_t K, int32_t group_size, int32_t split_k, int32_t layout, int32_t act_dtype,
+                           int32_t scale_dtype, int32_t bias_dtype, void* stream);
+
 /* Row-exact GEMM: C[m, :] for every m < M equals, bit for bit, what awq_w4a16_gemm computes for
  * the single row A[m, :] with the same arguments (M = 1): each row goes through the M = 1 plan,
  * kernel and reduction order, whatever M is, so a row's result never depends on the batch it

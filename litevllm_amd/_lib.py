@@ -58,6 +58,9 @@ SIGNATURES = {
     "awq_w4a16_gemm_rows_exact": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64,
                                                  _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
                                                  _c_i32, _c_p, _c_sz, _c_p]),
+    "awq_w4a16_gemm_noalloc_max_workspace": (_c_sz, []),
+    "awq_w4a16_gemm_noalloc": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i64,
+                                              _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_p]),
     "awq_w4a16_moe_workspace_bytes": (_c_sz, [_c_i64, _c_i64, _c_i64, _c_i32, _c_i32]),
     "awq_w4a16_moe": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_i32, _c_p, _c_i32, _c_p, _c_p, _c_p, _c_p, _c_p,
                                      _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32,

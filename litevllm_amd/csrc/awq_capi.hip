@@ -38,6 +38,60 @@ static bool decode_covers(int64_t M, int64_t G) {
 
 }  // namespace awq_host
 
+// ---- scratch of the allocation-free GEMM ------------------------------------------------
+// awq_w4a16_gemm_noalloc keeps the split-K arrival counters and fp32 partials that
+// awq_w4a16_gemm takes through `workspace` in this file-scope device array instead: one copy
+// per GPU, held until the process ends, laid out like a workspace (counters first).  Host
+// code never passes the array's name to a kernel or a copy (on the host it only stands in for
+// the symbol): each device's address comes from hipGetSymbolAddress, taken once per device
+// with that device current, and only that address is used.
+constexpr size_t kNoallocScratchBytes = awq_host::kCounterBytes + ((size_t)8 << 20);
+static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
+
+namespace awq_host {
+
+constexpr int kMaxDevices = 64;
+static void* g_scratch_ptr[kMaxDevices];
+static int g_scratch_rc[kMaxDevices];
+static std::once_flag g_scratch_once[kMaxDevices];
+
+// Zeroes n 32-bit words (a kernel, not hipMemsetAsync, so a caller may capture it in a graph).
+__global__ void __launch_bounds__(256) zero_words_kernel(uint32_t* p, int n) {
+  const int i = (int)(blockIdx.x * 256 + threadIdx.x);
+  if (i < n) p[i] = 0u;
+}
+
+// The current device's scratch address: looked up once per device, when the counter region is
+// also cleared on `st` (the kernels leave it zero after every call).
+static int noalloc_scratch(void** out, hipStream_t st) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    return AWQ_ERR_LAUNCH;
+  }
+  std::call_once(g_scratch_once[dev], [dev, st] {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) {
+      (void)hipGetLastError();
+      g_scratch_rc[dev] = AWQ_ERR_LAUNCH;
+      return;
+    }
+    const int words = (int)(kCounterBytes / 4);
+    hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)cdiv(words, 256)), dim3(256), 0, st, (uint32_t*)p, words);
+    if (hipGetLastError() != hipSuccess) {
+      g_scratch_rc[dev] = AWQ_ERR_LAUNCH;
+      return;
+    }
+    g_scratch_ptr[dev] = p;
+    g_scratch_rc[dev] = AWQ_OK;
+  });
+  if (g_scratch_rc[dev] != AWQ_OK) return g_scratch_rc[dev];
+  *out = g_scratch_ptr[dev];
+  return AWQ_OK;
+}
+
+}  // namespace awq_host
+
 using namespace awq_host;
 
 extern "C" {
@@ -144,6 +198,25 @@ int awq_w4a16_gemm(const void* a, int64_t lda, const int32_t* qweight, const voi
   if ((K % 32) != 0) return AWQ_ERR_SHAPE;
   if (!launch_prefill(ga, seq, zp, act_dtype, scale_dtype, st)) return AWQ_ERR_UNSUPPORTED;
   return launch_status();
+}
+
+size_t awq_w4a16_gemm_noalloc_max_workspace(void) { return kNoallocScratchBytes; }
+
+int awq_w4a16_gemm_noalloc(const void* a, int64_t lda, const int32_t* qweight, const void* scales,
+                           const int32_t* qzeros, const void* bias, void* c, int64_t ldc, int64_t M, int64_t N,
+                           int64_t K, int32_t group_size, int32_t split_k, int32_t layout, int32_t act_dtype,
+                           int32_t scale_dtype, int32_t bias_dtype, void* stream) {
+  if (M < 0 || N < 0 || K <= 0 || group_size <= 0 || split_k < 0) return AWQ_ERR_SHAPE;
+  if (M == 0 || N == 0) return AWQ_OK;
+  const size_t need = awq_w4a16_gemm_workspace_bytes(M, N, K, group_size, split_k, layout);
+  if (need > kNoallocScratchBytes) return AWQ_ERR_WORKSPACE;  // beyond the fixed scratch
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = noalloc_scratch(&ws, (hipStream_t)stream);
+    if (rc != AWQ_OK) return rc;
+  }
+  return awq_w4a16_gemm(a, lda, qweight, scales, qzeros, bias, c, ldc, M, N, K, group_size, split_k, layout,
+                        act_dtype, scale_dtype, bias_dtype, ws, need > 0 ? kNoallocScratchBytes : 0, stream);
 }
 
 int awq_w4a16_gemm_rows_exact(const void* a, int64_t lda, const int32_t* qweight, const void* scales,
