@@ -61,8 +61,9 @@ extern "C" {
  *                      the group axis; scales [N, K/G]  (tensor.py:842-858).
  * AWQ_LAYOUT_DECODE_STREAM : an AUTOAWQ qweight re-ordered by awq_w4a16_pack_decode_stream so
  *                      that the decode kernel reads it as contiguous 2 KiB runs; qzeros and
- *                      scales stay in the AUTOAWQ layout.  Accepted by awq_w4a16_gemm for
- *                      M <= 32 and group sizes 32/64/128.
+ *                      scales stay in the AUTOAWQ layout.  Accepted by awq_w4a16_gemm for every
+ *                      M (K % 32 == 0): the decode kernel serves M <= 32 with group sizes
+ *                      32/64/128, the prefill kernel the rest, so one copy serves both.
  * AWQ_LAYOUT_DECODE_NARROW : an AUTOAWQ qweight re-ordered by awq_w4a16_pack_decode_narrow
  *                      into 16-column tiles (one 32-bit word per column and 8 rows), read by
  *                      the narrow decode kernel: one block per 16 columns over the whole K,
@@ -123,7 +124,7 @@ size_t awq_w4a16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t g
  * awq_fused_gemm.py:1966-1971.  Otherwise (the prefill kernel): W rounded once to act_dtype,
  * as awq_w4a16_dequant computes it (the reference's tl.dot branch, 1973-1976).
  *   a: [M, K] act_dtype (F16 or BF16), row stride lda (elements).
- *   layout: AUTOAWQ or KN_SEQ (qweight [K, N/8]), or DECODE_STREAM / DECODE_NARROW
+ *   layout: AUTOAWQ or KN_SEQ (qweight [K, N/8]), DECODE_STREAM (any M) or DECODE_NARROW
  *           (M <= 32).  An NK_SEQ
  *           weight is converted once with awq_w4a16_repack_nk_to_autoawq; passing NK_SEQ
  *           here returns AWQ_ERR_UNSUPPORTED.

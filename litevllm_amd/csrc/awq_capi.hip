@@ -155,8 +155,9 @@ int awq_w4a16_gemm(const void* a, int64_t lda, const int32_t* qweight, const voi
   if (layout != AWQ_LAYOUT_AUTOAWQ && layout != AWQ_LAYOUT_KN_SEQ && layout != AWQ_LAYOUT_DECODE_STREAM &&
       layout != AWQ_LAYOUT_DECODE_NARROW)
     return AWQ_ERR_UNSUPPORTED;
-  const bool stream_layout = layout == AWQ_LAYOUT_DECODE_STREAM || layout == AWQ_LAYOUT_DECODE_NARROW;
-  if (stream_layout && (!decode_covers(M, group_size) || (K % 32) != 0)) return AWQ_ERR_UNSUPPORTED;
+  if (layout == AWQ_LAYOUT_DECODE_NARROW && !decode_covers(M, group_size)) return AWQ_ERR_UNSUPPORTED;
+  if ((layout == AWQ_LAYOUT_DECODE_NARROW || layout == AWQ_LAYOUT_DECODE_STREAM) && (K % 32) != 0)
+    return AWQ_ERR_UNSUPPORTED;
   // 32-bit buffer offsets: weights, activations and the output must stay below 2 GiB
   if (decode_stream_bytes(K, N) > 0x7FFFFFFFLL || M * lda * 2 > 0x7FFFFFFFLL) return AWQ_ERR_UNSUPPORTED;
   hipStream_t st = (hipStream_t)stream;
@@ -196,7 +197,11 @@ int awq_w4a16_gemm(const void* a, int64_t lda, const int32_t* qweight, const voi
     return launch_status();
   }
   if ((K % 32) != 0) return AWQ_ERR_SHAPE;
-  if (!launch_prefill(ga, seq, zp, act_dtype, scale_dtype, st)) return AWQ_ERR_UNSUPPORTED;
+  if (layout == AWQ_LAYOUT_DECODE_STREAM) {
+    if (!launch_prefill_stream(ga, zp, act_dtype, scale_dtype, st)) return AWQ_ERR_UNSUPPORTED;
+  } else if (!launch_prefill(ga, seq, zp, act_dtype, scale_dtype, st)) {
+    return AWQ_ERR_UNSUPPORTED;
+  }
   return launch_status();
 }
 

@@ -52,8 +52,12 @@ __global__ void __launch_bounds__(128 * NWN, 2) prefill_kn_kernel(const GemmArgs
   constexpr int ACH = BM * CPR / NT;     // activation chunks per thread per stage
   constexpr int BW = BN / 8;             // packed words per row of the tile
   static_assert(BW * (BK / 4) == NT, "one packed word x 4 k-rows per thread");
-  __shared__ u32x4 lds_a[2][BM * CPR];
-  __shared__ u32x4 lds_b[2][BN * CPR];
+  // one LDS block: activation stages [2][BM][CPR], weight stages [2][BN][CPR]; after the k loop
+  // the same bytes hold the output tile [BM][BN] fp16
+  __shared__ u32x4 lds_all[2 * BM * CPR + 2 * BN * CPR];
+  static_assert(BM * BN * 2 <= (int)sizeof(lds_all), "output tile fits the stage buffers");
+  u32x4(&lds_a)[2][BM * CPR] = *reinterpret_cast<u32x4(*)[2][BM * CPR]>(&lds_all[0]);
+  u32x4(&lds_b)[2][BN * CPR] = *reinterpret_cast<u32x4(*)[2][BN * CPR]>(&lds_all[2 * BM * CPR]);
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform by construction
@@ -240,20 +244,39 @@ __global__ void __launch_bounds__(128 * NWN, 2) prefill_kn_kernel(const GemmArgs
     __syncthreads();
   }
 
-  // lane (q, r) holds acc[mt][nt][v] = C[m0 + wave_m*WM + mt*16 + 4q + v][n0 + wave_n*WN + nt*16 + r]
+  // Epilogue through LDS (the k loop's last barrier has passed, so every stage buffer is free):
+  // lane (q, r) holds acc[mt][nt][v] = C[wave_m WM + 16 mt + 4 q + v][wave_n WN + 16 nt + r] of
+  // the tile; each value (+ bias, rounded once) goes to the row-major fp16 tile in LDS, whose
+  // 16-byte chunks are XOR-swizzled by row, and the block then writes whole rows with 16-byte
+  // stores (instead of 2-byte stores scattered over 4 rows each).
+  constexpr int CCH = BN / 8;  // 16-byte chunks per output row
+  auto c_chunk = [&](int row, int ch) { return ch ^ (row & 15 & (CCH - 1)); };
+  __attribute__((address_space(3))) uint16_t* cl = (__attribute__((address_space(3))) uint16_t*)(uintptr_t)(uint32_t)(
+      uintptr_t)(__attribute__((address_space(3))) u32x4*)&lds_all[0];
 #pragma unroll
   for (int nt = 0; nt < NTL; ++nt) {
-    const int col = n0 + wave_n * WN + nt * 16 + r;
-    if (col >= p.N) continue;
-    const float bv = p.bias ? load_bias(p.bias, p.bias_dtype, col) : 0.0f;
+    const int cc = wave_n * WN + nt * 16 + r;  // tile column
+    const int colg = n0 + cc;
+    const float bv = (p.bias && colg < p.N) ? load_bias(p.bias, p.bias_dtype, colg) : 0.0f;
 #pragma unroll
     for (int mt = 0; mt < MTL; ++mt) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int row = m0 + wave_m * WM + mt * 16 + 4 * q + v;
-        if (row < p.M) p.c[(int64_t)row * p.ldc + col] = to_bits<T>(acc[mt][nt][v] + bv);
+        const int row = wave_m * WM + mt * 16 + 4 * q + v;
+        cl[row * BN + c_chunk(row, cc >> 3) * 8 + (cc & 7)] = to_bits<T>(acc[mt][nt][v] + bv);
       }
     }
+  }
+  __syncthreads();
+  constexpr int CHUNKS = BM * CCH;
+  static_assert(CHUNKS % NT == 0, "");
+#pragma unroll
+  for (int j = 0; j < CHUNKS / NT; ++j) {
+    const int i = j * NT + tid;
+    const int row = i / CCH, ch = i % CCH;
+    const int grow = m0 + row, gcol = n0 + 8 * ch;
+    const u32x4 val = lds_all[row * CCH + c_chunk(row, ch)];
+    if (grow < p.M && gcol < p.N) *(u32x4*)(p.c + (int64_t)grow * p.ldc + gcol) = val;
   }
 }
 

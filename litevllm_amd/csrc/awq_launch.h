@@ -57,6 +57,8 @@ bool launch_decode_narrow_norm(const awq::GemmArgs& a, bool zp, hipStream_t st);
 
 // Prefill GEMM (M > 32 or group sizes the decode kernel does not cover).
 bool launch_prefill(const awq::GemmArgs& a, bool seq, bool zp, int act, int sdt, hipStream_t st);
+// Prefill GEMM on the decode stream layout (awq_prefill.hip): M > 32, K % 32 == 0.
+bool launch_prefill_stream(const awq::GemmArgs& a, bool zp, int act, int sdt, hipStream_t st);
 
 // Standalone dequant and repack.
 int launch_dequant(const int32_t* qweight, const void* scales, const int32_t* qzeros, void* out,

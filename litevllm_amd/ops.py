@@ -256,12 +256,30 @@ DECODE_MAX_M = 32
 DECODE_GROUPS = (32, 64, 128)
 
 
-def _use_decode_stream(M, K, group_size, a, scales, layout, decode_stream):
+def _decode_shaped(M, group_size):
+    return M <= DECODE_MAX_M and int(group_size) in DECODE_GROUPS
+
+
+def _prefill_tiles_fill_chip(M: int, N: int) -> bool:
+    """Whether 256 x 256 output tiles give every CU a block: the prefill kernel on the AutoAWQ
+    tensor serves those grids best (measured on MI355X, M = 2048, K = 4096, N = 12288 / 24576);
+    smaller grids run faster on the stream copy's prefill kernel (M = 512)."""
+    return -(-M // 256) * -(-N // 256) >= L.num_cus()
+
+
+def _use_decode_stream(M, K, N, group_size, layout, decode_stream):
+    """Whether the call reads the stream copy of an AutoAWQ weight: the decode kernel's layout
+    for decode shapes, and the layout the prefill kernel for grids below one block per CU reads
+    (K % 32 == 0, power-of-two group size).  ``decode_stream=False`` keeps the AutoAWQ tensor."""
     if decode_stream is False or layout != "autoawq":
         return False
-    eligible = M <= DECODE_MAX_M and int(group_size) in DECODE_GROUPS and K % 32 == 0
+    g = int(group_size)
+    if _decode_shaped(M, g):
+        eligible = K % 32 == 0
+    else:
+        eligible = K % 32 == 0 and g & (g - 1) == 0 and (decode_stream is True or not _prefill_tiles_fill_chip(M, N))
     if decode_stream is True and not eligible:
-        raise ValueError("the decode stream layout needs M <= 32 and group 32/64/128")
+        raise ValueError("the stream layout needs K % 32 == 0 (and a power-of-two group size for M > 32)")
     return eligible
 
 
@@ -290,8 +308,11 @@ def _kernel_weight(qweight, scales, qzeros, group_size, layout, M, N, K, split_k
     lc = layout_code(layout)
     if decode_layout not in (None, "narrow", "stream"):
         raise ValueError(f"unknown decode_layout {decode_layout!r}")
-    if _use_decode_stream(M, K, group_size, None, scales, layout, decode_stream):
-        narrow = decode_layout == "narrow" or (decode_layout is None and _narrow_fits(M, N, K, int(split_k)))
+    if _use_decode_stream(M, K, N, group_size, layout, decode_stream):
+        if decode_layout == "narrow" and not _decode_shaped(M, group_size):
+            raise ValueError("the narrow layout needs M <= 32 and group 32/64/128")
+        narrow = _decode_shaped(M, group_size) and (
+            decode_layout == "narrow" or (decode_layout is None and _narrow_fits(M, N, K, int(split_k))))
         qweight = (NARROW_CACHE if narrow else STREAM_CACHE).get(qweight)
         lc = L.LAYOUT_DECODE_NARROW if narrow else L.LAYOUT_DECODE_STREAM
     return qweight, scales, qzeros, lc
