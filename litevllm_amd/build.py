@@ -20,7 +20,8 @@ BUILD_DIR = os.path.join(ROOT, "_build")
 OUT = os.path.join(HERE, "libawq_w4a16.so")
 ARCH = "gfx950"
 SOURCES = ["awq_capi.hip", "awq_dequant.hip", "awq_decode.hip", "awq_decode_misc.hip", "awq_decode_narrow.hip",
-           "awq_gemm.hip", "awq_prefill.hip", "awq_moe.hip", "awq_moe_misc.hip", "awq_moe_mfma.hip", "awq_rmsnorm.hip"]
+           "awq_gemm.hip", "awq_prefill.hip", "awq_moe.hip", "awq_moe_misc.hip", "awq_moe_mfma.hip", "awq_moe_mfma_down.hip",
+           "awq_rmsnorm.hip"]
 
 # hipcc's host pass does not know the packed-fp32 target feature and says so: harmless
 _NOISE = "is not a recognized feature for this target"

@@ -84,6 +84,13 @@ __device__ __forceinline__ MagicK magic_consts() {
   asm volatile("" : "+v"(k.lo_mask), "+v"(k.hi_mask), "+v"(k.lo_magic), "+v"(k.hi_magic));
   return k;
 }
+// The same with the magic exponents in SGPRs (a VOP3 operation may read one SGPR), for
+// kernels short of VGPRs.
+__device__ __forceinline__ MagicK magic_consts_s() {
+  MagicK k{0x000F000Fu, 0x00F000F0u, 0x64006400u, 0x54005400u};
+  asm volatile("" : "+v"(k.lo_mask), "+v"(k.hi_mask), "+s"(k.lo_magic), "+s"(k.hi_magic));
+  return k;
+}
 template <int P>
 __device__ __forceinline__ uint32_t magic_bits(uint32_t m, const MagicK& k) {
   const uint32_t v = (P >= 2) ? (m >> 8) : m;
@@ -147,6 +154,16 @@ __device__ __forceinline__ float gated_act(float g, int kind) {
     return g / (1.0f + expf(-2.0f * inner));
   }
   return g / (1.0f + expf(-g));
+}
+// The same activations from the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32: about
+// one ulp each), for epilogues whose result is rounded to fp16 / bf16 right after: the fp32
+// error (a few 1e-7 relative) is far below that rounding.  KIND is the compile-time kind.
+template <int KIND>
+__device__ __forceinline__ float gated_act_fast(float g) {
+  constexpr float kLog2e = 1.4426950408889634f;
+  float t = g;
+  if constexpr (KIND == 1) t = 2.0f * 0.7978845608028654f * (g + 0.044715f * g * g * g);
+  return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-t * kLog2e));
 }
 
 // Shared argument block of the GEMM kernels.
@@ -466,7 +483,25 @@ __device__ __forceinline__ void lds_dma4(const u32x4& rsrc, uint32_t lds, uint32
                : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
                : "memory", "m0");
 }
+// Buffer loads into registers issued as assembly, like the LDS DMA: the compiler does not
+// track them, so a kernel waits for them itself (s_waitcnt vmcnt) and then passes every
+// destination register through pin_after_wait(), which keeps uses after that wait and keeps
+// the register live until then (a load still in flight must not land in a reused register).
+__device__ __forceinline__ u32x4 asm_load16(const u32x4& rsrc, uint32_t voff, uint32_t soff) {
+  u32x4 v;
+  asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(rsrc), "s"(soff) : "memory");
+  return v;
+}
+__device__ __forceinline__ uint32_t asm_load4(const u32x4& rsrc, uint32_t voff) {
+  uint32_t v;
+  asm volatile("buffer_load_dword %0, %1, %2, 0 offen" : "=v"(v) : "v"(voff), "s"(rsrc) : "memory");
+  return v;
+}
 #pragma clang diagnostic pop
+template <typename V>
+__device__ __forceinline__ void pin_after_wait(V& v) {
+  asm volatile("" : "+v"(v));
+}
 
 // Buffer resource over a whole tensor (raw addressing, bounds = nbytes).  Range checks
 // cover the VGPR offset only (the SGPR offset is excluded), so anything that must read as

@@ -370,8 +370,8 @@ int launch_moe(const MoeCall& c, hipStream_t st) {
   dn.rows_a = (int)R;
 
   const int sbf = c.scale_dtype == AWQ_DTYPE_BF16 ? 1 : 0;
-  if (R >= (int64_t)kMoeMfmaMinRoutes * c.E && (c.H % 64) == 0 && (c.I % 64) == 0) {
-    // many routes per expert: weights dequantized once per 64-route tile into LDS
+  if (R >= (int64_t)kMoeMfmaMinRoutes * c.E && (c.H % 64) == 0 && (c.I % 64) == 0 && (c.G & (c.G - 1)) == 0) {
+    // many routes per expert: each dequantized weight operand feeds up to six 16-route tiles
     launch_moe_mfma(gu, dn, c.E, zp, c.act_dtype, sbf, st);
   } else if (c.act_dtype == AWQ_DTYPE_F16 && !sbf) {
     launch_gemm_f16<0>(gu, c.E, mt, zp, st);

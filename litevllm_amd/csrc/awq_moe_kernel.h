@@ -357,9 +357,11 @@ inline void launch_moe_gemm_t(const MoeArgs& a, int E, hipStream_t st) {
     hipLaunchKernelGGL((moe_gemm_kernel<MODE, MT, 2, 1, ZP, T, SBF>), grid, dim3(512), 0, st, a);
 }
 
-// grouped MFMA kernels for many routes per expert (awq_moe_mfma.hip); both K dims % 64 == 0
+// grouped MFMA kernels for many routes per expert (awq_moe_mfma.hip, awq_moe_mfma_down.hip);
+// both K dims % 64 == 0
 void launch_moe_mfma(const awq::MoeArgs& gu, const awq::MoeArgs& dn, int E, bool zp, int act, int sbf,
                      hipStream_t st);
+void launch_moe_tile_down(const awq::MoeArgs& dn, int E, bool zp, int act, int sbf, hipStream_t st);
 // bf16 activations or bf16 scales (awq_moe_misc.hip); false if the dtype is not provided
 bool launch_moe_misc(const awq::MoeArgs& gu, const awq::MoeArgs& dn, int E, bool zp, int act, int sbf,
                      hipStream_t st);

@@ -1,0 +1,460 @@
+// Grouped MoE GEMMs for many routes per expert (prefill-sized batches) on gfx950: the work of
+// moe_gemm_kernel (awq_moe_kernel.h) restructured so that each dequantized weight operand feeds
+// up to six 16-route MFMA tiles (moe_tile_kernel).  Instantiated by awq_moe_mfma.hip (gate_up)
+// and awq_moe_mfma_down.hip (down).
+#pragma once
+
+#include "awq_moe_kernel.h"
+
+namespace awq {
+
+// routes per row tile (six 16-route MFMA tiles), k per stage (one MFMA k-step), stream tiles
+// per block, stage slots
+constexpr int kTBM = 96, kTBK = 32, kTST = 4, kTPD = 5;
+
+// Row tile t of the grid: first every expert's full kTBM-route tiles (expert order), then
+// every expert's last partial tile, so the heavy tiles are dispatched first.  Computed by one
+// wave from the per-expert route counts, 64 experts per pass (one count per lane, prefix sums
+// across the wave), so a block spends one round of count loads on it.  e = -1 past the end.
+__device__ inline void moe_row_tile_wave(const int* counts, int E, int t, int& e, int& m0, int& rows) {
+  const int lane = threadIdx.x & 63;
+  auto prefix = [&](int v) {  // inclusive prefix sum over the wave
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int u = __shfl_up(v, d);
+      if (lane >= d) v += u;
+    }
+    return v;
+  };
+  e = -1;
+  m0 = 0;
+  rows = 0;
+  // phase 0: full tiles, phase 1: partial tiles
+  for (int phase = 0; phase < 2 && e < 0; ++phase) {
+    int base = 0;
+    for (int c0 = 0; c0 < E; c0 += 64) {
+      const int ex = c0 + lane;
+      const int cnt = ex < E ? counts[ex] : 0;
+      const int n = phase == 0 ? cnt / kTBM : (cnt % kTBM != 0 ? 1 : 0);
+      const int incl = prefix(n);
+      const int tot = __shfl(incl, 63);
+      if (t < base + tot) {  // wave-uniform
+        const uint64_t hit = __ballot(base + incl > t);
+        const int l = __ffsll((long long)hit) - 1;
+        const int excl = __shfl(incl - n, l);
+        const int c = __shfl(cnt, l);
+        e = c0 + l;
+        if (phase == 0) {
+          m0 = (t - base - excl) * kTBM;
+          rows = kTBM;
+        } else {
+          rows = c % kTBM;
+          m0 = c - rows;
+        }
+        break;
+      }
+      base += tot;
+    }
+    t -= base;
+  }
+}
+
+// One block: one row tile of an expert's route list (up to 96 routes: six 16-route MFMA tiles)
+// times kTST consecutive stream tiles (128 weight columns each), 8 waves: wave w owns stream
+// tile w % 4 and K-half w / 4, so two waves share each SIMD (each with at least 32 independent
+// accumulators at four token tiles, which keeps the MFMA pipe issuing) and one's memory and
+// LDS waits are covered by the other's work.
+//  * Per 32-row k-step a lane reads its 32-byte piece of the stream layout (one packed word
+//    over 8 k-rows), pairs the rows, dequantizes each nibble position to one MFMA operand (the
+//    exact magic-number dequant, (q - z) * s rounded once to the activation dtype) and
+//    multiplies it into every token tile (v_mfma_f32_16x16x32): one dequant feeds up to six
+//    MFMAs, and at T = 512 every expert's routes (about 64, at most 84 in the benchmark) fit one
+//    row tile, so each weight is dequantized once per K-half wave and the grid is one block
+//    per CU (a second, partial tile of an expert would start a second round of blocks).
+//  * Everything a k-step needs comes into LDS by DMA four k-steps ahead (five slots): each
+//    K-half's activation rows (gathered from the route rows, shared by its 4 waves) and each
+//    wave's weight pieces, scales and zeros; the request's DMA instructions are spread over
+//    the k-step's MFMAs.  One barrier per k-step: it marks the k-step's data complete and the
+//    slot read in the previous k-step free for the next request.
+//  * The route ids and weights of the tile sit in LDS, so the epilogue waits on no global load;
+//    the activation comes from the hardware exp2 and reciprocal (gated_act_fast), rounded to
+//    the activation dtype right after.
+//  * The K-halves meet in LDS (fixed order: first half + second half), then lane (q, r) of the
+//    first-half wave holds the 8 columns 8 w .. 8 w + 7 of its word w for rows 4 q .. 4 q + 3 of
+//    each token tile, so the epilogue stores 8 contiguous values per row: for gate_up the up
+//    sums come from lane r + 8 (a row rotation by 8 lanes) and act(gate) * up * route_weight is
+//    rounded once into the intermediate; down writes fp32 rows per route.
+// fp32 sums; the intermediate is rounded once to the activation dtype and down writes fp32
+// route rows, as in moe_gemm_kernel.  Every row is computed independently of its tile mates, so
+// results are bitwise reproducible.
+template <int MODE, bool ZP, typename T, bool FAST>
+__global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, int scale_bf16, int E, int col_groups) {
+  constexpr int BM = kTBM, BK = kTBK, PD = kTPD, NWV = 2 * kTST;
+  constexpr int CPR = BK / 8;                 // 16-byte chunks per activation row (4)
+  constexpr int A_INSTR = BM * CPR / 64;      // activation DMAs per K-half per k-step (6)
+  constexpr int A_TWO = A_INSTR - kTST;       // waves of a half that issue two of them (2)
+  static_assert(A_TWO > 0 && A_TWO <= kTST && A_INSTR * 64 == BM * CPR, "activation DMA split");
+  // one slot (16-byte chunks): A [2 halves][BM rows][CPR], W [NWV][2 pieces][64 lanes],
+  // S [NWV][16 words], Z [NWV][16] (uint32)
+  constexpr int A_OFF = 0, W_OFF = A_OFF + 2 * BM * CPR, S_OFF = W_OFF + NWV * 2 * 64;
+  constexpr int Z_OFF = S_OFF + NWV * 16, SLOT = Z_OFF + NWV * 16 / 4;
+  constexpr uint32_t SLOT_BYTES = (uint32_t)SLOT * 16u;
+  __shared__ u32x4 lds_all[PD * SLOT];
+  __shared__ int s_rt[BM];
+  __shared__ float s_w[BM];
+  __shared__ int s_tile[3];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) u32x4*)&lds_all[0];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int stl = wave & (kTST - 1), kh = wave / kTST;
+  const int q = lane >> 4, r = lane & 15;
+
+  const int cg = blockIdx.x % col_groups;
+  if (wave == 0) {
+    int te, tm0, trows;
+    moe_row_tile_wave(p.counts, E, blockIdx.x / col_groups, te, tm0, trows);
+    if (lane == 0) {
+      s_tile[0] = te;
+      s_tile[1] = tm0;
+      s_tile[2] = trows;
+    }
+  }
+  __syncthreads();
+  const int e = __builtin_amdgcn_readfirstlane(s_tile[0]);
+  const int m0 = __builtin_amdgcn_readfirstlane(s_tile[1]);
+  const int rows = __builtin_amdgcn_readfirstlane(s_tile[2]);
+  if (e < 0) return;  // past the last row tile (whole block)
+  const int n_mt = (rows + 15) >> 4;  // token tiles holding routes (block-uniform)
+  {
+    const int* list = p.lists + (int64_t)e * p.R;
+    if (tid < rows) {
+      const int rt = list[m0 + tid];
+      s_rt[tid] = rt;
+      s_w[tid] = MODE == 0 ? load_route_weight(p.rw, p.rw_dtype, rt) : 0.f;
+    }
+  }
+  __syncthreads();
+
+  const int KS = p.K >> 5;
+  const int NW = p.N >> 3;
+  const int ngroups = p.K / p.G;
+  const int lg = __builtin_ctz((unsigned)p.G);  // the launcher takes power-of-two group sizes only
+  const int st = cg * kTST + stl;              // this wave's stream tile
+  const bool wave_on = st < p.tiles;
+  const int word = wave_on ? moe_word(st, r, p.half, NW) : -1;
+  const uint32_t wc = word < 0 ? 0u : (uint32_t)word;
+  // K-halves in k-steps: the first half takes the odd one when there is one
+  const int n0 = (KS + 1) >> 1;
+  const int n_my = kh == 0 ? n0 : KS - n0;
+  const int s_first = kh == 0 ? 0 : n0;  // first global k-step of this wave's half
+
+  // ---- activation gather: DMA i (0..5) of a half fills its chunks 64 i + lane: row
+  // 16 i + lane / 4, slot lane % 4, holding k-chunk slot ^ ((row / 2) & 3); wave (stl, kh)
+  // issues DMA stl of its half, and waves stl < 2 also DMA 4 + stl ----
+  const u32x4 ars = rsrc_words(p.a, (uint32_t)((uint64_t)p.rows_a * (uint64_t)p.lda * 2u));
+  auto a_off = [&](int i) {
+    const int row = 16 * i + (lane >> 2);
+    const int kc = (lane & 3) ^ ((row >> 1) & 3);
+    uint32_t off = 0x80000000u;  // rows past the tile's routes read as zero
+    if (row < rows) {
+      const int rt = s_rt[row];
+      const int src = MODE == 0 ? rt / p.topk : rt;
+      off = ((uint32_t)src * (uint32_t)p.lda + (uint32_t)(kc * 8)) * 2u;
+    }
+    return off;
+  };
+  const uint32_t a_voff0 = a_off(stl);
+  const uint32_t a_voff4 = stl < A_TWO ? a_off(kTST + stl) : 0x80000000u;
+
+  // ---- weights: the lane's piece of run (st, k-step): rows 8 q .. 8 q + 3 of word r at byte
+  // 16 lane of the run, rows 8 q + 4 .. 8 q + 7 at 1024 + 16 lane; the DMA puts them at the
+  // same lane's place in LDS.  Scales (16 bytes: the word's 8 columns) and zeros (the word)
+  // of the k-step's group likewise, by lanes 0..15 ----
+  const uint32_t stream_bytes = (uint32_t)p.tiles * (uint32_t)KS * 2048u;
+  const u32x4 wrs = rsrc_words((const char*)p.qw + (int64_t)e * stream_bytes, wave_on ? stream_bytes : 0u);
+  const uint32_t w_run = (uint32_t)(wave_on ? st : 0) * (uint32_t)KS * 2048u;  // + 16 lane
+  const u32x4 srs = rsrc_words(p.sc + (int64_t)e * ngroups * p.N, (uint32_t)ngroups * (uint32_t)p.N * 2u);
+  const u32x4 zrs = rsrc_words(ZP ? (const void*)(p.qz + (int64_t)e * ngroups * NW) : (const void*)p.sc,
+                               ZP ? (uint32_t)ngroups * (uint32_t)NW * 4u : 0u);
+  // DMA instructions per k-step: activation (1, or 2 for waves stl < A_TWO), weight (2),
+  // scales (1), zeros (1)
+  constexpr int NB_REST = 2 + 1 + (ZP ? 1 : 0);
+
+  // piece `part` (0..3) of the request for this half's k-step s, into slot s % PD
+  // (ln: the lane index, passed in so that a caller short of registers can have the lane
+  // offsets formed anew each time)
+  auto issue_part = [&](int s, int part, int ln) __attribute__((always_inline)) {
+    const int ks = s_first + s;
+    const uint32_t slot = lds0 + (uint32_t)(s % PD) * SLOT_BYTES;
+    if (part == 0) {
+      const uint32_t abase = slot + (uint32_t)(A_OFF + kh * BM * CPR) * 16u;
+      lds_dma16(ars, abase + (uint32_t)(stl * 64) * 16u, a_voff0, (uint32_t)(ks * BK * 2));
+      if (stl < A_TWO) lds_dma16(ars, abase + (uint32_t)((kTST + stl) * 64) * 16u, a_voff4, (uint32_t)(ks * BK * 2));
+    } else if (part == 1 || part == 2) {
+      const int e2 = part - 1;
+      lds_dma16(wrs, slot + (uint32_t)(W_OFF + (wave * 2 + e2) * 64) * 16u, w_run + (uint32_t)ln * 16u + (uint32_t)e2 * 1024u,
+                (uint32_t)ks * 2048u);
+    } else {
+      const uint32_t g = (uint32_t)((ks * BK) >> lg);
+      if (lane < 16) {  // one copy per word
+        lds_dma16(srs, slot + (uint32_t)(S_OFF + wave * 16) * 16u, 16u * wc, g * (uint32_t)p.N * 2u);
+        if constexpr (ZP)
+          lds_dma4(zrs, slot + (uint32_t)Z_OFF * 16u + (uint32_t)(wave * 16) * 4u, 4u * wc, g * (uint32_t)NW * 4u);
+      }
+    }
+  };
+  // LDS byte offsets (within a slot) this lane reads
+  auto a_rd = [&](int ln) __attribute__((always_inline)) {
+    const int rr = ln & 15, qq = ln >> 4;
+    return (uint32_t)(A_OFF + kh * BM * CPR + rr * CPR + (qq ^ ((rr >> 1) & 3))) * 16u;
+  };
+  auto w_rd = [&](int ln) __attribute__((always_inline)) { return (uint32_t)ln * 16u + (uint32_t)(W_OFF + wave * 128) * 16u; };
+  auto s_rd = [&](int ln) __attribute__((always_inline)) { return (uint32_t)(ln & 15) * 16u + (uint32_t)(S_OFF + wave * 16) * 16u; };
+  auto z_rd = [&](int ln) __attribute__((always_inline)) {
+    return (uint32_t)(ln & 15) * 4u + (uint32_t)Z_OFF * 16u + (uint32_t)(wave * 16) * 4u;
+  };
+  auto lds16 = [](uint32_t addr) __attribute__((always_inline)) {
+    return *(const __attribute__((address_space(3))) u32x4*)(uintptr_t)addr;
+  };
+  auto lds4 = [](uint32_t addr) __attribute__((always_inline)) {
+    return *(const __attribute__((address_space(3))) uint32_t*)(uintptr_t)addr;
+  };
+  // byte address of k-step s's slot, opaque to the compiler (no per-slot copies of the lane
+  // read addresses are kept)
+  auto slot_of = [&](int s) __attribute__((always_inline)) {
+    uint32_t b = lds0 + (uint32_t)(s % PD) * SLOT_BYTES;
+    asm volatile("" : "+v"(b));
+    return b;
+  };
+
+  const MagicK mk = magic_consts_s();
+  const bool sb = scale_bf16 != 0;
+
+  // the rest specialized on the number of token tiles holding routes (block-uniform)
+  auto body = [&](auto nmt_c) __attribute__((always_inline)) {
+    constexpr int NMT = decltype(nmt_c)::value;
+    f32x4 acc[8][NMT];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int mt = 0; mt < NMT; ++mt) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    int cur_group = -1;
+    // the group's per-nibble constants; with six token tiles (192 accumulator registers) the
+    // fp16 pair (zero, scale) of each nibble is kept packed in one register and unpacked per
+    // k-step (two byte permutes), which keeps the k-loop within the 256 registers of two waves
+    // per SIMD
+    constexpr bool PACK = FAST && NMT >= 6;
+    ColConst cc[8];
+    uint32_t ccp[8];
+    // one k-step from the slot at sb0; between nibble pairs, the pieces of request `req`
+    // the lane index as an opaque value per k-step where registers are short (six tiles): the
+    // lane offsets are then formed anew each k-step (a few VALU operations) instead of held
+    auto lane_now = [&]() __attribute__((always_inline)) {
+      int l = lane;
+      if constexpr (PACK) asm volatile("" : "+v"(l));
+      return l;
+    };
+    auto compute = [&](uint32_t sb0, int s, int req) __attribute__((always_inline)) {
+      const int ln = lane_now();
+      const int g = ((s_first + s) * BK) >> lg;
+      if (g != cur_group) {  // wave-uniform
+        WordSZ sz;
+        sz.s4 = lds16(sb0 + s_rd(ln));
+        sz.zw = ZP ? lds4(sb0 + z_rd(ln)) : 0x88888888u;
+        prep_consts<false, FAST>(sz, sb, cc);
+        if constexpr (PACK) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) ccp[i] = __builtin_amdgcn_perm(cc[i].sc, cc[i].zm, 0x05040100u);  // zm lo | sc lo << 16
+        }
+        cur_group = g;
+      }
+      u32x4 af[NMT];
+#pragma unroll
+      for (int mt = 0; mt < NMT; ++mt) af[mt] = lds16(sb0 + a_rd(ln) + (uint32_t)(mt * 16 * CPR * 16));
+      const u32x4 wv0 = lds16(sb0 + w_rd(ln)), wv1 = lds16(sb0 + w_rd(ln) + 1024u);
+      // nibble I's constants: held, or unpacked right before use (packed form)
+      auto nib_const = [&](int I) __attribute__((always_inline)) {
+        if constexpr (PACK) {
+          uint32_t pk = ccp[I];
+          asm volatile("" : "+v"(pk));
+          ColConst c_;
+          c_.zm = __builtin_amdgcn_perm(pk, pk, 0x01000100u);
+          c_.sc = __builtin_amdgcn_perm(pk, pk, 0x03020302u);
+          c_.scf = 0.0f;
+          return c_;
+        } else {
+          return cc[I];
+        }
+      };
+      // the word at k-rows 8 q + j (j = 0..7); pair rows (2u, 2u + 1) into lo/hi 16-bit halves
+      uint32_t mlo[4], mhi[4];
+      mlo[0] = pair_lo(wv0[0], wv0[1]);
+      mhi[0] = pair_hi(wv0[0], wv0[1]);
+      mlo[1] = pair_lo(wv0[2], wv0[3]);
+      mhi[1] = pair_hi(wv0[2], wv0[3]);
+      mlo[2] = pair_lo(wv1[0], wv1[1]);
+      mhi[2] = pair_hi(wv1[0], wv1[1]);
+      mlo[3] = pair_lo(wv1[2], wv1[3]);
+      mhi[3] = pair_hi(wv1[2], wv1[3]);
+#define AWQ_RB_NIB(I)                                                                       \
+      {                                                                                     \
+        const u32x4 b = rows_operand<I, FAST, T>(mlo, mhi, nib_const(I), mk);               \
+        _Pragma("unroll") for (int mt = 0; mt < NMT; ++mt)                                  \
+          acc[I][mt] = MfmaOp<T>::run(af[mt], b, acc[I][mt]);                               \
+      }
+#define AWQ_RB_REQ(PART)                                                                    \
+      if (req >= 0) {                                                                       \
+        __builtin_amdgcn_sched_barrier(0);                                                  \
+        issue_part(req, PART, ln);                                                          \
+        __builtin_amdgcn_sched_barrier(0);                                                  \
+      }
+      AWQ_RB_NIB(0) AWQ_RB_NIB(1) AWQ_RB_REQ(0)
+      AWQ_RB_NIB(2) AWQ_RB_NIB(3) AWQ_RB_REQ(1)
+      AWQ_RB_NIB(4) AWQ_RB_NIB(5) AWQ_RB_REQ(2)
+      AWQ_RB_NIB(6) AWQ_RB_NIB(7) AWQ_RB_REQ(3)
+#undef AWQ_RB_REQ
+#undef AWQ_RB_NIB
+    };
+
+    // requests for this half's k-steps 0 .. PD - 2
+    for (int s = 0; s < PD - 1; ++s)
+      if (s < n_my)
+#pragma unroll
+        for (int part = 0; part < 4; ++part) issue_part(s, part, lane);
+    for (int s = 0; s < n0; ++s) {
+      // this k-step's DMAs have landed (the PD - 2 after it may stay in flight)
+      if (s < n_my) {
+        const int ahead = min(n_my - 1 - s, PD - 2);  // wave-uniform
+        static_assert(PD - 2 == 3, "the waits below cover three k-steps in flight");
+        if (stl < A_TWO) {
+          constexpr int NB = NB_REST + 2;
+          if (ahead == 3) AWQ_WAIT_VMCNT(3 * NB);
+          else if (ahead == 2) AWQ_WAIT_VMCNT(2 * NB);
+          else if (ahead == 1) AWQ_WAIT_VMCNT(NB);
+          else AWQ_WAIT_VMCNT0();
+        } else {
+          constexpr int NB = NB_REST + 1;
+          if (ahead == 3) AWQ_WAIT_VMCNT(3 * NB);
+          else if (ahead == 2) AWQ_WAIT_VMCNT(2 * NB);
+          else if (ahead == 1) AWQ_WAIT_VMCNT(NB);
+          else AWQ_WAIT_VMCNT0();
+        }
+      }
+      // every wave's share of the k-step has landed, and slot (s + PD - 1) % PD, read in the
+      // previous k-step, is free
+      __syncthreads();
+      if (s < n_my) compute(slot_of(s), s, s + PD - 1 < n_my ? s + PD - 1 : -1);
+    }
+
+    // ---- the K-halves meet: second-half sums through LDS (two rounds of four nibbles),
+    // added to the first half's ----
+    constexpr int NVH = 4 * NMT * 4;  // floats per lane per round
+    float* red = (float*)&lds_all[0];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      __syncthreads();  // LDS free (stage reads done / previous round consumed)
+      if (kh == 1) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) red[((stl * NVH) + (i * NMT + mt) * 4 + v) * 64 + lane] = acc[4 * h + i][mt][v];
+      }
+      __syncthreads();
+      if (kh == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[4 * h + i][mt][v] += red[((stl * NVH) + (i * NMT + mt) * 4 + v) * 64 + lane];
+      }
+    }
+    if (kh == 1) return;
+
+    if (word < 0) return;
+    // ---- epilogue: acc[I][mt][v] = row 16 mt + 4 q + v, column 8 word + nib_col(I) ----
+    auto epilogue = [&](auto kind_c) __attribute__((always_inline)) {
+      constexpr int KIND = decltype(kind_c)::value;
+#pragma unroll
+      for (int mt = 0; mt < NMT; ++mt) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int m = 16 * mt + 4 * q + v;
+          if constexpr (MODE == 0) {
+            // lanes 0..7 hold gate sums, lanes 8..15 the up sums of the same columns: rotate
+            // the 16-lane rows by 8 (every lane of the row active) to bring each up sum to its
+            // gate (each source value is first taken into a register of its own: a DPP move fed
+            // directly from an element of the accumulator tuple was compiled to read element 0)
+            float up[8];
+#pragma unroll
+            for (int I = 0; I < 8; ++I) {
+              float gv = acc[I][mt][v];
+              asm volatile("" : "+v"(gv));
+              up[I] = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, gv), 0x128, 0xF, 0xF, false));
+            }
+            if (r < 8 && m < rows) {
+              const int rt = s_rt[m];
+              const float wgt = s_w[m];
+              float h[8];
+#pragma unroll
+              for (int I = 0; I < 8; ++I) h[nib_col<false>(I)] = gated_act_fast<KIND>(acc[I][mt][v]) * up[I] * wgt;
+              const u32x4 o = {pack2<T>(h[0], h[1]), pack2<T>(h[2], h[3]), pack2<T>(h[4], h[5]), pack2<T>(h[6], h[7])};
+              *(u32x4*)((uint16_t*)p.out + (int64_t)rt * p.ldo + 8 * word) = o;
+            }
+          } else {
+            if (m < rows) {
+              const int rt = s_rt[m];
+              float y[8];
+#pragma unroll
+              for (int I = 0; I < 8; ++I) y[nib_col<false>(I)] = acc[I][mt][v];
+              float* dst = (float*)p.out + (int64_t)rt * p.ldo + 8 * word;
+              *(f32x4*)dst = f32x4{y[0], y[1], y[2], y[3]};
+              *(f32x4*)(dst + 4) = f32x4{y[4], y[5], y[6], y[7]};
+            }
+          }
+        }
+      }
+    };
+    if (MODE == 0 && p.act_kind == 1) epilogue(std::integral_constant<int, 1>{});  // kernel-uniform
+    else epilogue(std::integral_constant<int, 0>{});
+  };
+  switch (n_mt) {
+    case 1: body(std::integral_constant<int, 1>{}); break;
+    case 2: body(std::integral_constant<int, 2>{}); break;
+    case 3: body(std::integral_constant<int, 3>{}); break;
+    case 4: body(std::integral_constant<int, 4>{}); break;
+    case 5: body(std::integral_constant<int, 5>{}); break;
+    default: body(std::integral_constant<int, 6>{}); break;
+  }
+}
+
+}  // namespace awq
+
+namespace awq_host {
+
+template <int MODE, bool ZP, typename T, bool FAST>
+void launch_moe_tile_t(const awq::MoeArgs& a, int E, int sbf, hipStream_t st) {
+  const int col_groups = (int)awq::cdiv(a.tiles, awq::kTST);
+  const int64_t tiles_m = awq::cdiv(a.R, awq::kTBM) + E;  // each expert adds at most one partial tile
+  hipLaunchKernelGGL((awq::moe_tile_kernel<MODE, ZP, T, FAST>), dim3((unsigned)(tiles_m * col_groups)),
+                     dim3(128 * awq::kTST), 0, st, a, sbf, E, col_groups);
+}
+
+template <int MODE>
+void launch_moe_tile_mode(const awq::MoeArgs& a, int E, bool zp, int act, int sbf, hipStream_t st) {
+  using awq::bf16;
+  using awq::f16;
+  if (act == AWQ_DTYPE_BF16) {
+    zp ? launch_moe_tile_t<MODE, true, bf16, false>(a, E, sbf, st) : launch_moe_tile_t<MODE, false, bf16, false>(a, E, sbf, st);
+  } else if (!sbf) {
+    zp ? launch_moe_tile_t<MODE, true, f16, true>(a, E, sbf, st) : launch_moe_tile_t<MODE, false, f16, true>(a, E, sbf, st);
+  } else {
+    zp ? launch_moe_tile_t<MODE, true, f16, false>(a, E, sbf, st) : launch_moe_tile_t<MODE, false, f16, false>(a, E, sbf, st);
+  }
+}
+
+}  // namespace awq_host

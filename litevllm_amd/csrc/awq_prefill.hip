@@ -48,27 +48,6 @@ template <> struct Mfma32<bf16> {
 // differ, which (r ^ r / 8) & 7 gives the dequant stores (rows 8 apart).
 __device__ __forceinline__ int ps_swz(int r) { return (r ^ (r >> 3)) & 7; }
 
-// Buffer loads issued as assembly, like the LDS DMA: the compiler does not track them, so a
-// kernel waits for them itself (s_waitcnt vmcnt) and then passes the destination registers
-// through pin_after_wait() so no use is scheduled before that wait.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ u32x4 asm_load16(const u32x4& rsrc, uint32_t voff, uint32_t soff) {
-  u32x4 v;
-  asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(rsrc), "s"(soff) : "memory");
-  return v;
-}
-__device__ __forceinline__ uint32_t asm_load4(const u32x4& rsrc, uint32_t voff) {
-  uint32_t v;
-  asm volatile("buffer_load_dword %0, %1, %2, 0 offen" : "=v"(v) : "v"(voff), "s"(rsrc) : "memory");
-  return v;
-}
-#pragma clang diagnostic pop
-template <typename V>
-__device__ __forceinline__ void pin_after_wait(V& v) {
-  asm volatile("" : "+v"(v));
-}
-
 constexpr int kPSBM = 256, kPSBK = 64;
 
 template <int NWN, bool ZP, typename T, bool FAST>

@@ -49,13 +49,13 @@ def _dense_experts(d, G):
     return w1.cpu().numpy(), w2.cpu().numpy()
 
 
-def _mfma_path(T, E, H, I, topk):
+def _mfma_path(T, E, H, I, topk, G=128):
     """The grouped MFMA kernels serve at least 16 routes per expert when H and I are multiples
-    of 64; they multiply weights rounded to the activation dtype (dequantized into LDS).  The
-    decode-structured kernels serve the rest and multiply the exact integers q - z, scaling each
-    group's fp32 sum once: unrounded weights, as the reference's int4 kernels
-    (gemma4_moe_int4.py:736-742)."""
-    return T * topk >= 16 * E and H % 64 == 0 and I % 64 == 0
+    of 64 and the group size is a power of two; they multiply weights rounded to the activation
+    dtype (each dequantized operand feeds up to six 16-route MFMA tiles).  The decode-structured
+    kernels serve the rest and multiply the exact integers q - z, scaling each group's fp32 sum
+    once: unrounded weights, as the reference's int4 kernels (gemma4_moe_int4.py:736-742)."""
+    return T * topk >= 16 * E and H % 64 == 0 and I % 64 == 0 and G & (G - 1) == 0
 
 
 def _unrounded_experts(p, G):
