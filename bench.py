@@ -333,13 +333,18 @@ def rot_copies(K, N):
 
 def _time_rotation(torch, ops, X, pool, Y, reps, **kw):
     """us per launch of gemm(X, w) over every weight copy of `pool` (a graph of back-to-back
-    launches, replayed `reps` times)."""
+    launches, replayed `reps` times).  The graph passes over the pool often enough to hold at
+    least 200 launches: a replay costs about 20 us of its own, which over a 21-launch graph
+    would add 1 us to every launch."""
+    inner = max(1, -(-200 // len(pool)))
+
     def run():
-        for qw, qz, sc in pool:
-            ops.gemm(X, qw, sc, qz, G, layout="autoawq", out=Y, **kw)
+        for _ in range(inner):
+            for qw, qz, sc in pool:
+                ops.gemm(X, qw, sc, qz, G, layout="autoawq", out=Y, **kw)
     ms, g = _time_graph(torch, run, reps)
     del g
-    return ms * 1e3 / len(pool)
+    return ms * 1e3 / (inner * len(pool))
 
 
 def _hbm_entry(us, M, K, N):
@@ -375,15 +380,16 @@ def main():
     gen = torch.Generator(device=dev).manual_seed(1)
 
     if args.only == "decode-m1n24576":
+        # the roofline leg's own measurement: the same >= 1 GiB rotation, captured once and
+        # replayed `steps` times, so a kernel trace of this mode sees the launches bench.py times
         W = _weights(torch, K_DEC, 24576, rot_copies(K_DEC, 24576), dev, 7)
         x = torch.randn((1, K_DEC), device=dev, generator=gen).half()
+        y = torch.empty((1, 24576), device=dev, dtype=torch.float16)
         for qw, qz, sc in W:
             ops.prepare_decode_stream(qw)
         torch.cuda.synchronize()
-        for _ in range(args.steps):
-            for qw, qz, sc in W:
-                ops.gemm(x, qw, sc, qz, G, layout="autoawq")
-        torch.cuda.synchronize()
+        us = _time_rotation(torch, ops, x, W, y, args.steps)
+        print(f"decode M=1 K={K_DEC} N=24576: {us:.3f} us per launch over {len(W)} copies", flush=True)
         return
     if args.only in ("moe-t16", "moe-t512"):
         T = 16 if args.only == "moe-t16" else 512
