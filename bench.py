@@ -249,9 +249,11 @@ def _moe_stacks(torch, ops, dev, copies, seed):
     return out
 
 
-def _bench_moe(torch, ops, dev, T, copies=3):
+def _bench_moe(torch, ops, dev, T, copies=3, inner=4):
     """configs[4] step: routing (softmax, top-8, renormalise) + grouped gate_up/act/down +
-    combine, graph-replayed over `copies` expert sets (3 x 201 MB, beyond the MALL)."""
+    combine, graph-replayed over `copies` expert sets (3 x 201 MB, beyond the MALL); one graph
+    passes over the sets `inner` times (12 steps), so a replay's own cost (about 20 us) is
+    spread over many steps as in a model's graph."""
     gen = torch.Generator(device=dev).manual_seed(100 + T)
     stacks = _moe_stacks(torch, ops, dev, copies, 200 + T)
     x = torch.randn((T, MOE_H), device=dev, generator=gen).half()
@@ -261,12 +263,13 @@ def _bench_moe(torch, ops, dev, T, copies=3):
     distinct = int(torch.unique(tid).numel())
 
     def run():
-        for st in stacks:
-            tw, ids = ops.moe_route(logits, MOE_TOPK)
-            ops.moe(x, tw, ids, *st, MOE_G, out=y)
-    ms, g = _time_graph(torch, run, 10)
+        for _ in range(inner):
+            for st in stacks:
+                tw, ids = ops.moe_route(logits, MOE_TOPK)
+                ops.moe(x, tw, ids, *st, MOE_G, out=y)
+    ms, g = _time_graph(torch, run, 5)
     del g, stacks
-    us = ms * 1e3 / copies
+    us = ms * 1e3 / (copies * inner)
     nbytes = distinct * moe_expert_bytes() + 2 * T * MOE_H * 2
     flops = 2.0 * T * MOE_TOPK * (MOE_H * 2 * MOE_I + MOE_I * MOE_H)
     gbs = nbytes / (us * 1e-6) / 1e9

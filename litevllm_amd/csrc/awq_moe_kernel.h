@@ -10,7 +10,7 @@
 //  * gate_up (moe_gemm_kernel<0>): grid (column tile, expert).  An expert's gate_up weight
 //    [H, 2I] is read in the stream layout with its tiles pairing 8 gate words with the 8 up
 //    words of the same columns, so one MFMA operand set yields gate and up together.  The
-//    block's 8 waves split K; the sums meet in LDS in a fixed order; the epilogue computes
+//    block's waves split K; the sums meet in LDS in a fixed order; the epilogue computes
 //    act(gate) * up * route_weight in fp32 and rounds once to the activation dtype -- the
 //    intermediate the reference keeps in x.dtype (gemma4_moe_int4.py:748-760).
 //  * down (moe_gemm_kernel<1>): the same structure over the intermediate rows, writing one fp32
@@ -63,10 +63,9 @@ __device__ __forceinline__ float load_route_weight(const void* rw, int dtype, in
 // kernel, the MFMAs multiply the activations by the exact integers q - z and each group's
 // fp32 sum is scaled once by the group's scale, so the weights enter unrounded -- the
 // reference's int4 kernels do the same, x * (q - 8) * s in fp32 (gemma4_moe_int4.py:736-742).
-template <int MODE, int MT, int D, int SPG, bool ZP, typename T, bool SBF>
-__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(MT == 1 ? 4 : 2, MT == 1 ? 4 : 2)))
+template <int MODE, int MT, int D, int SPG, bool ZP, typename T, bool SBF, int NWV>
+__global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(MT == 1 ? 4 : 2, MT == 1 ? 4 : 2)))
 moe_gemm_kernel(const MoeArgs p) {
-  constexpr int NWV = 8;
   constexpr int NACC = 8 * MT;
   constexpr int CH = NACC < 16 ? NACC : 16;
   static_assert(NACC % CH == 0, "");
@@ -77,8 +76,6 @@ moe_gemm_kernel(const MoeArgs p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int q = lane >> 4, r = lane & 15;
   const int t = blockIdx.x, e = blockIdx.y;
-  const int count = p.counts[e];
-  if (count == 0) return;  // whole block
 
   const int KS = p.K >> 5;
   const int NW = p.N >> 3;
@@ -86,6 +83,34 @@ moe_gemm_kernel(const MoeArgs p) {
   const int* list = p.lists + (int64_t)e * p.R;
   const uint32_t stream_bytes = (uint32_t)p.tiles * (uint32_t)KS * 2048u;
   const char* wbase = (const char*)p.qw + (int64_t)e * stream_bytes;
+  // weight units of a ring slot: 2 x 16 bytes per lane of the unit's 2 KiB run (zeros past the
+  // wave's last unit: an empty descriptor, no memory traffic)
+  uint32_t raw[D][8];
+  auto load_w = [&](int slot, int ks, bool past) {
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(wbase, past ? 0u : stream_bytes);
+    const int kbase = (int)(((uint32_t)t * (uint32_t)KS + (uint32_t)ks) * 2048u);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const u32x4 v = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, (int)((uint32_t)lane * 16u), kbase + 1024 * i, kStreamNT));
+#pragma unroll
+      for (int c = 0; c < 4; ++c) raw[slot][4 * i + c] = v[c];
+    }
+  };
+  // The first round's route rows and weights are requested before the route count arrives,
+  // for the one-group split (every wave on the first 16 * MT routes, K split over the block):
+  // the split of every expert with at most 16 * MT routes.  Rows first, so that waiting for
+  // them does not wait for the weights.
+  int pre_rt[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) pre_rt[mt] = mt * 16 + r < p.R ? list[mt * 16 + r] : -1;
+  {
+    const int ks0 = KS * wave / NWV, n = KS * (wave + 1) / NWV - ks0;
+#pragma unroll
+    for (int u = 0; u < D; ++u) load_w(u, ks0 + u, u >= n);
+  }
+  const int count = p.counts[e];
+  if (count == 0) return;  // whole block
   const uint16_t* sbase = p.sc + (int64_t)e * ngroups * p.N;
   const void* zbase = ZP ? (const void*)(p.qz + (int64_t)e * ngroups * NW) : (const void*)p.sc;
   const uint32_t s_bytes = (uint32_t)ngroups * (uint32_t)p.N * 2u;
@@ -100,7 +125,10 @@ moe_gemm_kernel(const MoeArgs p) {
   // integers q - z: several k-steps per group of one route tile, and bf16
   constexpr bool BIASED = (SPG >= 2 && MT == 1) || (!std::is_same<T, f16>::value && !(MT == 2 && SPG == 1));
 
-  for (int base = 0; base < count; ) {
+  // one round per 16 * MT * (wave groups) routes; the first is its own copy of the code, so
+  // that the waits of its first loads see only what was requested before it
+  auto run_round = [&](const int base, auto first_t) __attribute__((always_inline)) -> int {
+    constexpr bool FIRST = decltype(first_t)::value;
     // wave groups of 16 * MT rows; the waves of a group split K
     const int left = count - base;
     int ng = 1;
@@ -122,17 +150,36 @@ moe_gemm_kernel(const MoeArgs p) {
       for (int i = 0; i < 8; ++i) acc[i][mt] = tot[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
+    // the first round of the one-group split: its weights and rows are in flight already
+    const bool pre = FIRST && ng == 1;  // block-uniform
     if (active && nunits > 0) {
       // the activation operand: route row r of each 16-route tile, 8 k per lane
       uint32_t x_off[MT];
+      // (the divisor is re-read each round, so that its reciprocal is not held across the
+      // k-step loop)
+      int topk = p.topk;
+      asm volatile("" : "+s"(topk));
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      auto row_off = [&](int rt) -> uint32_t {
+        const uint32_t arow = MODE == 0 ? (uint32_t)rt / (uint32_t)topk : (uint32_t)rt;
+        return rt < 0 ? 0x80000000u : arow * (uint32_t)p.lda * 2u + 16u * (uint32_t)(ln >> 4);
+      };
+      // two branches, each using its rows inside: the wait for a list read issued after the
+      // weights (later rounds) must not apply to the first round, whose rows came first
+      if (pre) {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const int m = m0 + mt * 16 + r;
-        const int rt = m < count ? list[m] : -1;
-        const int arow = MODE == 0 ? rt / p.topk : rt;
-        x_off[mt] = rt < 0 ? 0x80000000u : ((uint32_t)arow * (uint32_t)p.lda + 8u * (uint32_t)q) * 2u;
+        for (int mt = 0; mt < MT; ++mt) x_off[mt] = row_off(mt * 16 + r < count ? pre_rt[mt] : -1);
+      } else {
+        const __amdgpu_buffer_rsrc_t lrs = make_rsrc(list, (uint32_t)p.R * 4u);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const int m = m0 + mt * 16 + r;
+          const int rt = m < count ? (int)__builtin_amdgcn_raw_buffer_load_b32(lrs, (int)(4u * (uint32_t)m), 0, 0) : -1;
+          x_off[mt] = row_off(rt);
+          asm volatile("" : "+v"(x_off[mt]));
+        }
       }
-      uint32_t raw[D][8];
       u32x4 xr[D][MT];
       WordSZ sz[D];
       uint32_t zm[8];  // biased zeros of the current group (exact integer operands)
@@ -144,23 +191,15 @@ moe_gemm_kernel(const MoeArgs p) {
       // scales and zeros only where a group starts or in the first turn (prep reads no other
       // slot's); the single-tile kernel keeps per-unit loads (its 128 registers have no room
       // to hold a slot's constants across turns)
-      auto issue = [&](int slot, bool first_turn) {
+      auto issue = [&](int slot, bool first_turn, bool with_w = true) {
         const int ks = iks;
         const bool past = ileft <= 0;
         ++iks;
         --ileft;
-        const __amdgpu_buffer_rsrc_t wrs = make_rsrc(wbase, past ? 0u : stream_bytes);
         const __amdgpu_buffer_rsrc_t xrs = make_rsrc(p.a, past ? 0u : x_bytes);
         const __amdgpu_buffer_rsrc_t srs = make_rsrc(sbase, past ? 0u : s_bytes);
         const __amdgpu_buffer_rsrc_t zrs = make_rsrc(zbase, past ? 0u : z_bytes);
-        const int kbase = (int)(((uint32_t)t * (uint32_t)KS + (uint32_t)ks) * 2048u);
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const u32x4 v = __builtin_bit_cast(
-              u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, (int)((uint32_t)lane * 16u), kbase + 1024 * i, kStreamNT));
-#pragma unroll
-          for (int c = 0; c < 4; ++c) raw[slot][4 * i + c] = v[c];
-        }
+        if (with_w) load_w(slot, ks, past);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
           xr[slot][mt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)x_off[mt], ks * 64, 0));
@@ -226,7 +265,7 @@ moe_gemm_kernel(const MoeArgs p) {
       };
 
 #pragma unroll
-      for (int u = 0; u < D; ++u) issue(u, true);
+      for (int u = 0; u < D; ++u) issue(u, true, !pre);
       __builtin_amdgcn_sched_barrier(0);
       // (one token tile runs without it: the extra loop would cost the registers that let
       // four waves share a SIMD)
@@ -297,6 +336,11 @@ moe_gemm_kernel(const MoeArgs p) {
     // lane (q, r), accumulator [i][mt] element v: route row m0 + 16 mt + 4q + v, tile word r,
     // column nib_col(i) of that word
     if (ki == 0 && active) {
+      // the lane's row and word taken afresh (nothing derived from them is held across the
+      // k-step loop)
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      const int q = ln >> 4, r = ln & 15;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
@@ -335,8 +379,10 @@ moe_gemm_kernel(const MoeArgs p) {
         }
       }
     }
-    base += ng * 16 * MT;
-  }
+    return base + ng * 16 * MT;
+  };
+  int base = run_round(0, std::true_type{});
+  while (base < count) base = run_round(base, std::false_type{});
 }
 
 }  // namespace awq
@@ -344,17 +390,22 @@ moe_gemm_kernel(const MoeArgs p) {
 namespace awq_host {
 using namespace awq;
 
+// waves per block: the 944-1024 blocks of a decode batch's grid (tiles x experts) fit the chip
+// at once with four-wave blocks (four blocks per CU at one 16-route tile), and each wave
+// streams twice the k-steps of an eight-wave block
+constexpr int kMoeStreamWaves = 4;
+
 // grid (column tiles, experts); the group size picks the k-steps per group
 template <int MODE, int MT, bool ZP, typename T, bool SBF>
 inline void launch_moe_gemm_t(const MoeArgs& a, int E, hipStream_t st) {
   const dim3 grid((unsigned)a.tiles, (unsigned)E);
   const int spg = a.G / 32;
   if (spg == 4)
-    hipLaunchKernelGGL((moe_gemm_kernel<MODE, MT, 2, 4, ZP, T, SBF>), grid, dim3(512), 0, st, a);
+    hipLaunchKernelGGL((moe_gemm_kernel<MODE, MT, 2, 4, ZP, T, SBF, kMoeStreamWaves>), grid, dim3(64 * kMoeStreamWaves), 0, st, a);
   else if (spg == 2)
-    hipLaunchKernelGGL((moe_gemm_kernel<MODE, MT, 2, 2, ZP, T, SBF>), grid, dim3(512), 0, st, a);
+    hipLaunchKernelGGL((moe_gemm_kernel<MODE, MT, 2, 2, ZP, T, SBF, kMoeStreamWaves>), grid, dim3(64 * kMoeStreamWaves), 0, st, a);
   else
-    hipLaunchKernelGGL((moe_gemm_kernel<MODE, MT, 2, 1, ZP, T, SBF>), grid, dim3(512), 0, st, a);
+    hipLaunchKernelGGL((moe_gemm_kernel<MODE, MT, 2, 1, ZP, T, SBF, kMoeStreamWaves>), grid, dim3(64 * kMoeStreamWaves), 0, st, a);
 }
 
 // grouped MFMA kernels for many routes per expert (awq_moe_mfma.hip, awq_moe_mfma_down.hip);

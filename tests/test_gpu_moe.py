@@ -143,6 +143,9 @@ CASES = [
     (300, 16, 256, 256, 4, 128, True, "silu"),              # ~75 routes/expert: 2 row tiles
     # Gemma4's symmetric group-32 experts (z = 8, tanh GELU) at a decode batch
     (16, 64, 512, 256, 8, 32, False, "gelu_pytorch_tanh"),
+    # 128 experts, 8 and 12.5 routes each: the stream kernels with one and two route tiles
+    (128, 128, 256, 128, 8, 64, True, "silu"),
+    (200, 128, 256, 128, 8, 128, True, "silu"),
 ]
 
 
@@ -192,6 +195,33 @@ def test_moe_bf16_activations_and_out_of_range_ids():
     # bf16 output: one bf16 ulp is 8 fp16 ulps
     assert np.max(d_ / O.fp16_ulp(exact, floor)) <= 16.0
     assert d_.sum() / np.abs(exact).sum() <= 2e-3
+
+
+def test_moe_tokens_without_routes_get_zero_rows():
+    """Tokens none of whose ids is in [0, E) (expert parallelism: every expert elsewhere) sum
+    nothing: their output rows are zero, with the stream kernels (few routes per expert) and
+    the grouped tile kernels (many)."""
+    for T, E in ((12, 16), (600, 8)):
+        H, I, topk, G = 256, 128, 4 if E == 16 else 2, 64
+        p, d = _problem(T, E, H, I, topk, G, seed=11)
+        tw, tid = _route_cpu(torch.from_numpy(p["logits"]), topk)
+        tid = tid.clone()
+        tid[2] = -1          # all routes masked (negative ids)
+        tid[5] = E + 1       # all routes masked (ids past the experts)
+        tid[7, 1:] = -1      # one route left
+        out = torch.full((T, H), float("nan"), dtype=torch.float16, device=DEV)
+        y = ops.moe(_dev(p["x"]), tw.to(DEV), tid.to(DEV), d["gq"], d["gs"], d["gz"], d["dq"], d["ds"], d["dz"], G,
+                    out=out)
+        torch.cuda.synchronize()
+        yc = y.cpu()
+        assert not torch.isnan(yc).any(), (T, E)
+        assert torch.equal(yc[2], torch.zeros(H, dtype=torch.float16)), (T, E)
+        assert torch.equal(yc[5], torch.zeros(H, dtype=torch.float16)), (T, E)
+        w1, w2 = _experts_used(p, d, G, _mfma_path(T, E, H, I, topk, G))
+        exact = O.moe_grouped_exact(p["x"], tw.numpy(), tid.numpy(), w1, w2)
+        keep = np.ones(T, dtype=bool)
+        keep[[2, 5]] = False
+        _check(yc.numpy()[keep], exact[keep], f"masked tokens T={T} E={E}")
 
 
 def test_gemma4_grouped_surface_ref_layout_with_zeros():
