@@ -329,17 +329,25 @@ int launch_moe(const MoeCall& c, hipStream_t st) {
   float* y = (float*)(ws + w.y);
   const bool zp = c.gu_qz != nullptr;
   const int mt = moe_mt(R, c.E);
+  const int sbf = c.scale_dtype == AWQ_DTYPE_BF16 ? 1 : 0;
+  const bool mfma = R >= (int64_t)kMoeMfmaMinRoutes * c.E && (c.H % 64) == 0 && (c.I % 64) == 0 && (c.G & (c.G - 1)) == 0;
+  // few routes: the stream kernels collect each expert's routes from the ids themselves
+  const bool scan = !mfma && R <= kMoeScanMaxR;
 
-  hipLaunchKernelGGL(moe_align_kernel, dim3((unsigned)c.E), dim3(256), 0, st, c.ids, c.id64, (int)R, lists, counts);
-  if (launch_status() != AWQ_OK) return AWQ_ERR_LAUNCH;
+  if (!scan) {
+    hipLaunchKernelGGL(moe_align_kernel, dim3((unsigned)c.E), dim3(256), 0, st, c.ids, c.id64, (int)R, lists, counts);
+    if (launch_status() != AWQ_OK) return AWQ_ERR_LAUNCH;
+  }
 
   MoeArgs gu{};
   gu.a = (const uint16_t*)c.x;
   gu.qw = (const uint32_t*)c.gu_qw;
   gu.sc = (const uint16_t*)c.gu_sc;
   gu.qz = (const uint32_t*)c.gu_qz;
-  gu.lists = lists;
-  gu.counts = counts;
+  gu.lists = scan ? nullptr : lists;
+  gu.counts = scan ? nullptr : counts;
+  gu.ids = c.ids;
+  gu.id64 = c.id64;
   gu.rw = c.rw;
   gu.out = tmp;
   gu.lda = c.ldx;
@@ -369,8 +377,7 @@ int launch_moe(const MoeCall& c, hipStream_t st) {
   dn.tiles = (int)moe_tiles(c.H, 0);
   dn.rows_a = (int)R;
 
-  const int sbf = c.scale_dtype == AWQ_DTYPE_BF16 ? 1 : 0;
-  if (R >= (int64_t)kMoeMfmaMinRoutes * c.E && (c.H % 64) == 0 && (c.I % 64) == 0 && (c.G & (c.G - 1)) == 0) {
+  if (mfma) {
     // many routes per expert: each dequantized weight operand feeds up to six 16-route tiles
     launch_moe_mfma(gu, dn, c.E, zp, c.act_dtype, sbf, st);
   } else if (c.act_dtype == AWQ_DTYPE_F16 && !sbf) {

@@ -44,14 +44,19 @@ struct MoeArgs {
   const uint32_t* qw;  // stream-packed expert stack [E][tiles][K/32][2048 B]
   const uint16_t* sc;  // scales [E][K/G][N]
   const uint32_t* qz;  // zeros [E][K/G][N/8] (AutoAWQ order) or null (symmetric, z = 8)
-  const int* lists;    // route lists [E][R]
-  const int* counts;   // routes per expert [E]
+  const int* lists;    // route lists [E][R], or null: each block collects its expert's routes
+  const int* counts;   // routes per expert [E]   from ids (R <= kMoeScanMaxR)
+  const void* ids;     // expert ids [R], int32 or int64 (id64)
+  int id64;
   const void* rw;      // route weights [R] (gate_up only)
   void* out;           // gate_up: [R][ldo] act dtype; down: [R][ldo] fp32
   int64_t lda, ldo;
   int R, topk, K, N, G, half, tiles, rows_a;
   int rw_dtype, act_kind;
 };
+
+// Largest route count whose route lists the stream kernels collect themselves.
+constexpr int kMoeScanMaxR = 1024;
 
 __device__ __forceinline__ float load_route_weight(const void* rw, int dtype, int r) {
   if (dtype == AWQ_DTYPE_F16) return h_bits2f(((const uint16_t*)rw)[r]);
@@ -71,6 +76,8 @@ moe_gemm_kernel(const MoeArgs p) {
   static_assert(NACC % CH == 0, "");
   static_assert(D == 2 && (SPG == 1 || SPG % D == 0), "");
   __shared__ f32x4 red[(NWV / 2) * CH * 64];
+  __shared__ int s_list[kMoeScanMaxR];  // the expert's routes, collected from the ids
+  __shared__ int s_wc[NWV];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -97,20 +104,67 @@ moe_gemm_kernel(const MoeArgs p) {
       for (int c = 0; c < 4; ++c) raw[slot][4 * i + c] = v[c];
     }
   };
-  // The first round's route rows and weights are requested before the route count arrives,
-  // for the one-group split (every wave on the first 16 * MT routes, K split over the block):
-  // the split of every expert with at most 16 * MT routes.  Rows first, so that waiting for
-  // them does not wait for the weights.
+  // The first round's weights are requested before the route count is known, for the
+  // one-group split (every wave on the first 16 * MT routes, K split over the block): the split
+  // of every expert with at most 16 * MT routes.  What the route count depends on is requested
+  // first, so that waiting for it does not wait for the weights: the ids (the block collects
+  // its expert's routes) or the first round's route rows (route lists given).
+  const bool scan = p.lists == nullptr;  // kernel-uniform
+  constexpr int SPT = kMoeScanMaxR / (64 * NWV);  // ids per thread
+  int idv[SPT];
   int pre_rt[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) pre_rt[mt] = mt * 16 + r < p.R ? list[mt * 16 + r] : -1;
-  {
+  auto load_first_weights = [&]() __attribute__((always_inline)) {
     const int ks0 = KS * wave / NWV, n = KS * (wave + 1) / NWV - ks0;
 #pragma unroll
     for (int u = 0; u < D; ++u) load_w(u, ks0 + u, u >= n);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  if (scan) {
+    // int64 ids: the low word (the value for every id below 2^31), as the route lists kernel
+    const uint32_t stride = p.id64 ? 8u : 4u;
+    const __amdgpu_buffer_rsrc_t irs = make_rsrc(p.ids, (uint32_t)p.R * stride);
+#pragma unroll
+    for (int u = 0; u < SPT; ++u) {
+      const int i = u * 64 * NWV + tid;
+      const int v = (int)__builtin_amdgcn_raw_buffer_load_b32(irs, (int)((uint32_t)i * stride), 0, 0);
+      idv[u] = i < p.R ? v : -1;
+    }
+    load_first_weights();
+  } else {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) pre_rt[mt] = mt * 16 + r < p.R ? list[mt * 16 + r] : -1;
+    load_first_weights();
   }
-  const int count = p.counts[e];
+  int count;
+  if (scan) {
+    // routes whose id is e, in route order (the order the route lists hold)
+    int c = 0;
+#pragma unroll
+    for (int u = 0; u < SPT; ++u) {
+      if (u * 64 * NWV < p.R) {  // block-uniform
+        const bool hit = idv[u] == e;
+        const uint64_t m = __ballot(hit);
+        if (lane == 0) s_wc[wave] = __popcll(m);
+        __syncthreads();
+        int off = c, tot = c;
+#pragma unroll
+        for (int w = 0; w < NWV; ++w) {
+          off += w < wave ? s_wc[w] : 0;
+          tot += s_wc[w];
+        }
+        if (hit) s_list[off + __popcll(m & ((1ull << lane) - 1ull))] = u * 64 * NWV + tid;
+        __syncthreads();  // the list is complete, and s_wc is read before the next round writes it
+        c = tot;
+      }
+    }
+    count = __builtin_amdgcn_readfirstlane(c);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) pre_rt[mt] = mt * 16 + r < count ? s_list[mt * 16 + r] : -1;
+  } else {
+    count = p.counts[e];
+  }
   if (count == 0) return;  // whole block
+  auto route_at = [&](int m) -> int { return scan ? s_list[m] : list[m]; };
   const uint16_t* sbase = p.sc + (int64_t)e * ngroups * p.N;
   const void* zbase = ZP ? (const void*)(p.qz + (int64_t)e * ngroups * NW) : (const void*)p.sc;
   const uint32_t s_bytes = (uint32_t)ngroups * (uint32_t)p.N * 2u;
@@ -170,6 +224,12 @@ moe_gemm_kernel(const MoeArgs p) {
       if (pre) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) x_off[mt] = row_off(mt * 16 + r < count ? pre_rt[mt] : -1);
+      } else if (scan) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const int m = m0 + mt * 16 + r;
+          x_off[mt] = row_off(m < count ? s_list[m] : -1);
+        }
       } else {
         const __amdgpu_buffer_rsrc_t lrs = make_rsrc(list, (uint32_t)p.R * 4u);
 #pragma unroll
@@ -346,7 +406,7 @@ moe_gemm_kernel(const MoeArgs p) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int m = m0 + mt * 16 + 4 * q + v;
-          const int rt = m < count ? list[m] : -1;
+          const int rt = m < count ? route_at(m) : -1;
           float o[8];
 #pragma unroll
           for (int c = 0; c < 8; ++c) o[c] = tot[col_nib<false>(c)][mt][v];
