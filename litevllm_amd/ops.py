@@ -260,24 +260,20 @@ def _decode_shaped(M, group_size):
     return M <= DECODE_MAX_M and int(group_size) in DECODE_GROUPS
 
 
-def _prefill_tiles_fill_chip(M: int, N: int) -> bool:
-    """Whether 256 x 256 output tiles give every CU a block: the prefill kernel on the AutoAWQ
-    tensor serves those grids best (measured on MI355X, M = 2048, K = 4096, N = 12288 / 24576);
-    smaller grids run faster on the stream copy's prefill kernel (M = 512)."""
-    return -(-M // 256) * -(-N // 256) >= L.num_cus()
-
-
 def _use_decode_stream(M, K, N, group_size, layout, decode_stream):
     """Whether the call reads the stream copy of an AutoAWQ weight: the decode kernel's layout
-    for decode shapes, and the layout the prefill kernel for grids below one block per CU reads
-    (K % 32 == 0, power-of-two group size).  ``decode_stream=False`` keeps the AutoAWQ tensor."""
+    for decode shapes, and the layout of the prefill kernel that reads it (K % 32 == 0,
+    power-of-two group size), which beats the AutoAWQ-layout prefill kernel at configs[3]'s
+    shapes (measured on MI355X: M = 2048, K = 4096, N = 24576 369 against 395 us; N = 12288
+    214 against 216 us; M = 512 136 against 146 us).  ``decode_stream=False`` keeps the
+    AutoAWQ tensor."""
     if decode_stream is False or layout != "autoawq":
         return False
     g = int(group_size)
     if _decode_shaped(M, g):
         eligible = K % 32 == 0
     else:
-        eligible = K % 32 == 0 and g & (g - 1) == 0 and (decode_stream is True or not _prefill_tiles_fill_chip(M, N))
+        eligible = K % 32 == 0 and g & (g - 1) == 0
     if decode_stream is True and not eligible:
         raise ValueError("the stream layout needs K % 32 == 0 (and a power-of-two group size for M > 32)")
     return eligible

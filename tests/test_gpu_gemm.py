@@ -299,20 +299,23 @@ def test_config1_decode_sweep(M, N, stream):
 @pytest.mark.parametrize("M,N", [(512, 12288), (512, 24576), (2048, 12288), (2048, 24576)])
 def test_config3_prefill(M, N):
     """Full-size prefill: every output against a torch fp32 GEMM on the (bit-exact
-    checked) dequantized weight; 128 sampled rows against the exact oracle."""
+    checked) dequantized weight, from both prefill kernels (the stream copy's, which serves
+    these shapes, and the AutoAWQ tensor's); 128 sampled rows against the exact oracle."""
     ops = _lib()
     _note(f"config3 M={M} N={N}")
     K, G = 4096, 128
     p = make_awq_problem(M=M, K=K, N=N, group_size=G, seed=3, outliers=True)
     t = _to_dev(p)
     y = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, layout="autoawq")
+    y_kn = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, layout="autoawq", decode_stream=False)
     wd = ops.dequant(t["qweight"], t["scales"], t["qzeros"], G, layout="autoawq")     # [K, N]
     w = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"], G)
     assert np.array_equal(wd.cpu().numpy().view(np.uint16), w.view(np.uint16))
     y32 = (t["x"].float() @ wd.float())
-    d = (y.float() - y32).abs()
     ulp = torch.exp2(torch.floor(torch.log2(y32.abs().clamp_min(1.0))) - 10)
-    assert bool((d <= 1.0 * ulp + 1e-3 * y32.abs().clamp_min(1.0) * 2 ** -10).all()), float((d / ulp).max())
+    for yy, what in ((y, "stream copy"), (y_kn, "AutoAWQ tensor")):
+        d = (yy.float() - y32).abs()
+        assert bool((d <= 1.0 * ulp + 1e-3 * y32.abs().clamp_min(1.0) * 2 ** -10).all()), (what, float((d / ulp).max()))
     rows = np.random.default_rng(0).choice(M, size=128, replace=False)
     ye = O.linear_exact(p["x"][rows], w.T)
     _check_vs_exact(y.cpu().numpy()[rows], ye, f"config3 M={M} N={N}")
