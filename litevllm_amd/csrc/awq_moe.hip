@@ -22,6 +22,37 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Whole-wave max / sum through DPP (row reductions by quad permutes and mirrors, then the row
+// broadcasts to lane 63), read back as a wave-uniform value: a few cycles per step where the
+// LDS crossbar shuffles above take about a hundred.
+__device__ __forceinline__ int dpp_i(int v, int ctrl, int row_mask) {
+  switch (ctrl) {  // the control word must be a constant
+    case 0xB1: return __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false);
+    case 0x4E: return __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false);
+    case 0x141: return __builtin_amdgcn_update_dpp(v, v, 0x141, 0xF, 0xF, false);
+    case 0x140: return __builtin_amdgcn_update_dpp(v, v, 0x140, 0xF, 0xF, false);
+    case 0x142: return __builtin_amdgcn_update_dpp(v, v, 0x142, 0xA, 0xF, false);
+    default: return __builtin_amdgcn_update_dpp(v, v, 0x143, 0xC, 0xF, false);
+  }
+}
+template <bool MAX>
+__device__ __forceinline__ float dpp_reduce(float v) {
+  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+  // quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror: every lane holds
+  // its row's result
+  v = op(v, __int_as_float(dpp_i(__float_as_int(v), 0xB1, 0xF)));
+  v = op(v, __int_as_float(dpp_i(__float_as_int(v), 0x4E, 0xF)));
+  v = op(v, __int_as_float(dpp_i(__float_as_int(v), 0x141, 0xF)));
+  v = op(v, __int_as_float(dpp_i(__float_as_int(v), 0x140, 0xF)));
+  // row_bcast:15 into rows 1 and 3, row_bcast:31 into rows 2 and 3 (other lanes add their
+  // own value back for the sum: only lane 63 is read)
+  const float b15 = __int_as_float(dpp_i(__float_as_int(v), 0x142, 0xA));
+  v = (MAX || ((__lane_id() >> 4) & 1)) ? op(v, b15) : v;
+  const float b31 = __int_as_float(dpp_i(__float_as_int(v), 0x143, 0xC));
+  v = (MAX || (__lane_id() >> 5)) ? op(v, b31) : v;
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 // x (> 0, finite) rounded once to fp16 (dt F16) or bf16 (dt BF16), returned as fp32: the double
 // is first rounded to fp32 toward zero with the inexact bit kept in the last place (round to
 // odd), which leaves the second rounding to nearest-even the correctly rounded result (fp32
@@ -57,6 +88,37 @@ __global__ void __launch_bounds__(256) moe_route_kernel(const void* logits, int6
   const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;  // whole wave
   const bool in_dt = (flags & AWQ_ROUTE_SOFTMAX_IN_LOGITS_DTYPE) && dtype != AWQ_DTYPE_F32;
+  if (!in_dt && E <= 64) {
+    // fp32 flow, one probability per lane: DPP max and sum, then top_k rounds of (max, lowest
+    // lane holding it) -- the choices and order of the rank pass below
+    const float x = lane < E ? load_logit(logits, dtype, t * ld + lane) : -INFINITY;
+    const float mx = dpp_reduce<true>(x);
+    const float ex = lane < E ? expf(x - mx) : 0.f;
+    const float sum = dpp_reduce<false>(ex);
+    float cur = lane < E ? ex / sum : -1.f;  // -1: not selectable
+    float mine = 0.f, sel_sum = 0.f;
+    int mine_id = 0;
+    for (int k = 0; k < topk; ++k) {
+      const float bv = dpp_reduce<true>(cur);
+      const uint64_t m = __ballot(cur == bv);
+      const int src = __ffsll((unsigned long long)m) - 1;
+      if (lane == k) {
+        mine = bv;
+        mine_id = src;
+      }
+      sel_sum += bv;
+      if (lane == src) cur = -1.f;
+    }
+    if (lane < topk) {
+      float w = mine;
+      if (flags & AWQ_ROUTE_RENORMALIZE) w = mine / ((flags & AWQ_ROUTE_CLAMP_SUM) ? fmaxf(sel_sum, 1e-8f) : sel_sum);
+      const int64_t o = t * topk + lane;
+      if (w_dtype == AWQ_DTYPE_F32) ((float*)out_w)[o] = w;
+      else ((uint16_t*)out_w)[o] = w_dtype == AWQ_DTYPE_F16 ? f2h_bits(w) : f2bf_bits(w);
+      out_ids[o] = mine_id;
+    }
+    return;
+  }
   float v[4];
   float mx = -INFINITY;
 #pragma unroll
