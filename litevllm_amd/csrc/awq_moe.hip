@@ -233,13 +233,14 @@ __global__ void __launch_bounds__(256) moe_pack_stream_kernel(const uint32_t* __
   }
 }
 
-// Route lists: block e collects the routes r (in increasing order) whose id is e.  The ids of
-// the first kAlignPre rounds of 256 are all requested before the first round runs (one memory
-// wait instead of one per round); later rounds load their own.
-constexpr int kAlignPre = 16;
-__global__ void __launch_bounds__(256) moe_align_kernel(const void* ids, int id64, int R, int* lists,
-                                                        int* counts) {
-  __shared__ int s_wcnt[4];
+// Route lists: block e collects the routes r (in increasing order) whose id is e, 1024 ids per
+// round.  The ids of the first kAlignPre rounds are all requested before the first round runs
+// (one memory wait instead of one per round); later rounds load their own.
+constexpr int kAlignPre = 4, kAlignThreads = 1024;
+__global__ void __launch_bounds__(kAlignThreads) moe_align_kernel(const void* ids, int id64, int R, int* lists,
+                                                                  int* counts) {
+  constexpr int NWV = kAlignThreads / 64;
+  __shared__ int s_wcnt[NWV];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int e = blockIdx.x;
   int* list = lists + (int64_t)e * R;
@@ -256,7 +257,7 @@ __global__ void __launch_bounds__(256) moe_align_kernel(const void* ids, int id6
     __syncthreads();
     int off = count, tot = count;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < NWV; ++w) {
       off += w < wave ? s_wcnt[w] : 0;
       tot += s_wcnt[w];
     }
@@ -266,11 +267,11 @@ __global__ void __launch_bounds__(256) moe_align_kernel(const void* ids, int id6
   };
   int pre[kAlignPre];
 #pragma unroll
-  for (int u = 0; u < kAlignPre; ++u) pre[u] = load_id(u * 256 + tid);
+  for (int u = 0; u < kAlignPre; ++u) pre[u] = load_id(u * kAlignThreads + tid);
 #pragma unroll
   for (int u = 0; u < kAlignPre; ++u)
-    if (u * 256 < R) round(u * 256, pre[u]);  // block-uniform
-  for (int base = kAlignPre * 256; base < R; base += 256) round(base, load_id(base + tid));
+    if (u * kAlignThreads < R) round(u * kAlignThreads, pre[u]);  // block-uniform
+  for (int base = kAlignPre * kAlignThreads; base < R; base += kAlignThreads) round(base, load_id(base + tid));
   if (tid == 0) counts[e] = count;
 }
 
@@ -280,10 +281,11 @@ template <typename T>
 __global__ void __launch_bounds__(256) moe_combine_kernel(const float* __restrict__ y, const void* ids, int id64,
                                                           int E, int64_t T_tok, int64_t H, int topk,
                                                           uint16_t* __restrict__ out, int64_t ldo) {
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t hq = H >> 2;
-  if (idx >= T_tok * hq) return;
-  const int64_t t = idx / hq, c = idx - t * hq;
+  // T_tok * H / 4 < 2^31 (the caller's 32-bit offset limits): 32-bit index arithmetic
+  const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t hq = (uint32_t)(H >> 2);
+  if ((int64_t)idx >= T_tok * (int64_t)hq) return;
+  const int64_t t = idx / hq, c = idx - (uint32_t)t * hq;
   f32x4 s = {0.f, 0.f, 0.f, 0.f};
   int j = 0;
   // eight routes at a time: their ids and rows are all requested before any is added (the
@@ -397,7 +399,8 @@ int launch_moe(const MoeCall& c, hipStream_t st) {
   const bool scan = !mfma && R <= kMoeScanMaxR;
 
   if (!scan) {
-    hipLaunchKernelGGL(moe_align_kernel, dim3((unsigned)c.E), dim3(256), 0, st, c.ids, c.id64, (int)R, lists, counts);
+    hipLaunchKernelGGL(moe_align_kernel, dim3((unsigned)c.E), dim3(kAlignThreads), 0, st, c.ids, c.id64, (int)R, lists,
+                       counts);
     if (launch_status() != AWQ_OK) return AWQ_ERR_LAUNCH;
   }
 
