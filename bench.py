@@ -56,6 +56,11 @@ def _weights(torch, K, N, copies, dev, seed):
     return out
 
 
+def _progress(what):
+    """One line per bench leg on stderr (stdout carries only the JSON result)."""
+    print(f"[bench] {what}", file=sys.stderr, flush=True)
+
+
 def _time_graph(torch, fn, reps, warmup=3):
     """Capture fn() in a HIP graph, replay `reps` times between events; returns ms/replay."""
     s = torch.cuda.Stream()
@@ -413,15 +418,16 @@ def main():
         torch.cuda.synchronize()
         return
     if args.only == "prefill":
-        W = _weights(torch, K_DEC, 24576, 2, dev, 9)
+        # the prefill leg's own measurement (three weight copies, graph of >= 200 launches)
+        W = _weights(torch, K_DEC, 24576, 3, dev, 9)
         x = torch.randn((2048, K_DEC), device=dev, generator=gen).half()
-        for _ in range(args.steps):
-            for qw, qz, sc in W:
-                ops.gemm(x, qw, sc, qz, G, layout="autoawq")
-        torch.cuda.synchronize()
+        y = torch.empty((2048, 24576), device=dev, dtype=torch.float16)
+        us = _time_rotation(torch, ops, x, W, y, args.steps)
+        print(f"prefill M=2048 K={K_DEC} N=24576: {us:.1f} us per launch over {len(W)} copies", flush=True)
         return
 
     # ---- configs[1] decode sweep (the metric) ----
+    _progress("decode sweep")
     # one weight pool per N whose rotation alone reads >= 1 GiB; step c gives shape (m, n) its
     # own copy 3 c + (index of m), so a step reads nine distinct weights and the steps rotate
     # through >= 1 GiB before any copy comes back
@@ -456,6 +462,7 @@ def main():
     del graph
 
     # ---- per-shape launch durations: back-to-back launches over each pool (>= 1 GiB) ----
+    _progress("per-shape launches")
     per_shape = {}
     for m, n in SWEEP:
         us = _time_rotation(torch, ops, X[m], pools[n], Y[(m, n)], 20)
@@ -470,6 +477,7 @@ def main():
     del pools, X, Y
 
     # ---- configs[0], configs[2] (split-K 1/4/8), configs[3] (all four shapes) ----
+    _progress("configs 0, 2, 3")
     configs = None
     if not args.no_configs:
         configs = {}
@@ -503,6 +511,7 @@ def main():
         configs["config3"] = c3
 
     # ---- prefill headline (configs[3], M=2048, N=24576) ----
+    _progress("prefill")
     prefill = None
     if not args.no_prefill:
         M, N = 2048, 24576
@@ -516,11 +525,13 @@ def main():
         del Wp
 
     # ---- grouped MoE (configs[4]: E=64, top-8, H=2048, I=1024, g=128, zero points) ----
+    _progress("grouped MoE")
     moe = None
     if not args.no_moe:
         moe = {T: _bench_moe(torch, ops, dev, T) for T in (16, 512)}
 
     # ---- fused RMSNorm + GEMM (the QKV projection after the input norm, K=4096, N=6144) ----
+    _progress("RMSNorm + GEMM")
     rms = None
     if not args.no_rmsnorm:
         rms = _bench_rmsnorm(torch, ops, dev)
