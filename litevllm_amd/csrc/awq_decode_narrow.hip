@@ -3,18 +3,23 @@
 // BLOCK_M = 1 .. 32 (vllm/kernels/triton/awq_fused_gemm.py:1883-1990) for shapes whose 128-
 // column tiles are too few to fill 256 CUs.
 //
-//  * Narrow stream layout (awq_w4a16_pack_decode_narrow): tile t = columns 16 t .. 16 t + 15;
-//    the (tile t, k-step s) run of 256 bytes starts at byte (t * K/32 + s) * 256 and lane
-//    l = 16 q + r owns its u32 at byte 4 l: the eight nibbles of column 16 t + r at rows
-//    32 s + 8 q + j, rows 2u and 2u + 1 at nibble u of the low and the high 16-bit half.  One
-//    u32 is then the lane's whole MFMA operand: pair u (rows 2u, 2u + 1) is magic_bits<u>.
+//  * Narrow stream layout (awq_w4a16_pack_decode_narrow): tile t = columns 16 t .. 16 t + 15,
+//    K cut into quads of four 32-row k-steps (KQ = ceil(K / 128) per tile, k-steps past K
+//    zero).  The (tile t, quad c) run of 1 KiB starts at byte (t * KQ + c) * 1024; lane
+//    l = 16 q + r owns the 16 bytes at 16 l, its u32 number i being k-step s = 4 c + i: the
+//    eight nibbles of column 16 t + r at rows 32 s + 8 q + j, rows 2u and 2u + 1 at nibble u of
+//    the low and the high 16-bit half.  One u32 is then the lane's whole MFMA operand for one
+//    k-step (pair u is magic_bits<u>), and one 16-byte load per lane brings four k-steps.
 //  * Lane (q, r) multiplies the activations (16 tokens x 32 k) by column 16 t + r's 32 rows
 //    with one v_mfma_f32_16x16x32 per k-step; the operand holds the exact integers q - z
 //    (magic-exponent unpack, one packed subtraction per pair of rows), each group's sum is
 //    scaled once by the column's fp32 scale -- unrounded weights, as in the wide decode
 //    kernel and the reference's M = 1 formulation (awq_fused_gemm.py:1966-1971).
-//  * The block's waves take contiguous shares of K with an 8-deep register ring (one u32 of
-//    weights per k-step and lane), meet in LDS, and sum in wave order (bitwise reproducible).
+//  * Short launches are bounded by the instructions a wave runs before its first weight load
+//    and after its last one lands, so each wave issues its weight loads (contiguous quads, a
+//    ring of D quads) as its first memory operations; the block's DMA of scales, zero words
+//    and activation rows into LDS follows, then one wait and one barrier.  The waves meet in
+//    LDS at the end and sum in wave order (bitwise reproducible).
 //  * Gated epilogue (GemmArgs::gate_act): the gate/up pair interleaved per 8 columns, so a
 //    tile's columns c < 8 and 8 + c are the gate and up sums of output 8 t + c.
 #include "awq_decode_kernel.h"
@@ -112,26 +117,63 @@ struct NormRow {
 
 // XL (one token tile): the M activation rows are staged in LDS once ([M][K]) and every lane
 // reads its k-slice of row min(r, M - 1) from there (the MFMA's rows past M repeat a real row
-// and are never read back); otherwise each k-step loads the token rows per lane.
+// and are never read back); otherwise each quad's activations come with its weights, per lane.
 // NORM (one fp16 row staged by XL, K / 8 <= kNormCols * NWV * 64): the row comes through
 // registers and is staged normalised (RMSNorm prologue) before the first k-step.
 template <int MT, int NWV, int SPG, bool ZP, typename T, bool SBF, bool ONE, bool XL, bool NORM = false>
-__global__ void __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(4, 4)))
-decode_narrow_kernel(const GemmArgs p, int tiles) {
+__global__ void __launch_bounds__(NWV * 64) decode_narrow_kernel(const GemmArgs p, int tiles) {
   static_assert(!ONE || MT == 1, "");
   static_assert(!XL || MT == 1, "");
   static_assert(!NORM || (XL && ONE && std::is_same<T, f16>::value), "");
-  constexpr int D = 8;
+  static_assert(SPG == 1 || SPG == 2 || SPG == 4, "a quad holds whole groups or lies in one");
+  constexpr int D = XL ? 4 : 2;  // quads in flight per wave
   constexpr int MROWS = ONE ? 1 : 16 * MT;
   extern __shared__ __align__(16) unsigned char smem[];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int q = lane >> 4, r = lane & 15;
   const int t = blockIdx.x;
-  const int KS = p.K >> 5;
-  const int ks0 = KS * wave / NWV, nunits = KS * (wave + 1) / NWV - ks0;
-  const int col = t * 16 + r;
+  const int KS = p.K >> 5, KQ = (KS + 3) >> 2;
+  const int qa = KQ * wave / NWV, nq = KQ * (wave + 1) / NWV - qa;
+
+  // ---- the wave's weight quads first: nothing but their addresses comes before them ----
+  const uint32_t w_bytes = (uint32_t)tiles * (uint32_t)KQ * 1024u;
+  const uint32_t w_lane_off = (uint32_t)lane * 16u;
+  const uint32_t x_bytes = (uint32_t)((uint64_t)p.M * (uint64_t)p.lda * 2u);
+  uint32_t x_lane_off[MT];
+  if constexpr (!XL) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+      x_lane_off[mt] = ((uint32_t)(mt * 16 + (lane & 15)) * (uint32_t)p.lda + 8u * (uint32_t)(lane >> 4)) * 2u;
+  }
+  u32x4 wr[D];
+  u32x4 xr[XL ? 1 : D][XL ? 1 : 4][MT];
+  int ic = qa, ileft = nq;
+  auto issue = [&](int slot) {
+    const int c = ic;  // wave-uniform
+    const bool past = ileft <= 0;
+    ++ic;
+    --ileft;
+    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(p.qw, past ? 0u : w_bytes);
+    wr[slot] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             wrs, (int)w_lane_off, (int)(((uint32_t)t * (uint32_t)KQ + (uint32_t)c) * 1024u), 0));
+    if constexpr (!XL) {
+      // the k-step's byte offset rides in the SGPR offset, which the range check does not
+      // cover: k-steps past K (the tile's last quad) get an empty range instead
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const __amdgpu_buffer_rsrc_t xrs = make_rsrc(p.a, (past || c * 4 + i >= KS) ? 0u : x_bytes);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          xr[slot][i][mt] = __builtin_bit_cast(
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)x_lane_off[mt], (c * 4 + i) * 64, 0));
+      }
+    }
+  };
+#pragma unroll
+  for (int u = 0; u < D; ++u) issue(u);
+
+  const int q = lane >> 4, r = lane & 15;
   const int NW = p.N >> 3;
   const int ngroups = p.K / p.G;
   const NarrowLds L = narrow_lds(NWV, MROWS, ngroups, p.K, ZP, XL ? p.M : 0);
@@ -141,13 +183,13 @@ decode_narrow_kernel(const GemmArgs p, int tiles) {
   const uint16_t* x_lds = (const uint16_t*)(smem + L.x);
   const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)smem;
 
-  // ---- the tile's scales and zero words (and with XL the activation row) go to LDS by DMA;
-  // wave w issues instructions w, w + NWV, ... of 64 lanes each ----
+  // ---- then the tile's scales and zero words (and with XL the activation rows) by DMA into
+  // LDS; wave w issues instructions w, w + NWV, ... of 64 lanes each ----
   {
     const u32x4 srs = rsrc_words(p.sc, (uint32_t)((uint64_t)ngroups * p.N * 2u));
     const u32x4 zrs = rsrc_words(p.qz, ZP ? (uint32_t)((uint64_t)ngroups * NW * 4u) : 0u);
-    const u32x4 xrs = rsrc_words(p.a, (uint32_t)((uint64_t)p.M * (uint64_t)p.lda * 2u));
-    const int n_s = (ngroups * 2 + 63) / 64;      // 16-byte pieces: group i / 2, half i % 2
+    const u32x4 xrs = rsrc_words(p.a, x_bytes);
+    const int n_s = (ngroups * 2 + 63) / 64;           // 16-byte pieces: group i / 2, half i % 2
     const int n_z = ZP ? (ngroups * 2 + 63) / 64 : 0;  // words: group i / 2, word 2t + i % 2
     const int kp = p.K / 8;                            // 16-byte pieces per activation row
     const int n_x = (XL && !NORM) ? (p.M * kp + 63) / 64 : 0;
@@ -172,50 +214,22 @@ decode_narrow_kernel(const GemmArgs p, int tiles) {
   }
   NormRow<NWV * 64> npc;
   if constexpr (NORM) npc.load(p, tid);
+  // every load of this wave has landed (the ring's first quads with it: they were issued
+  // together); the barrier then covers every wave's DMA (with NORM the prologue's first)
+  AWQ_WAIT_VMCNT0();
+  if constexpr (NORM) npc.normalise(p, (uint16_t*)(smem + L.x), red, wave, lane, tid);
+  else __syncthreads();
 
   f32x4 acc[MT], tot[MT];
   float tot1 = 0.f;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = tot[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const uint32_t w_bytes = (uint32_t)tiles * (uint32_t)KS * 256u;
-  const uint32_t x_bytes = (uint32_t)((uint64_t)p.M * (uint64_t)p.lda * 2u);
-  uint32_t x_lane_off[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) x_lane_off[mt] = ((uint32_t)(mt * 16 + r) * (uint32_t)p.lda + 8u * (uint32_t)q) * 2u;
-  const uint32_t w_lane_off = (uint32_t)lane * 4u;
   const int zsh = 4 * col_nib<false>(r & 7);
   const int x_row_off = ONE ? 0 : min(r, p.M - 1) * p.K;  // XL: the lane's activation row in LDS
   const MagicK mk = magic_consts();
 
-  uint32_t wr[D];
-  u32x4 xr[XL ? 1 : D][MT];
-  int iks = ks0, ileft = nunits;
-  auto issue = [&](int slot) {
-    const int ks = iks;  // wave-uniform
-    const bool past = ileft <= 0;
-    ++iks;
-    --ileft;
-    const __amdgpu_buffer_rsrc_t wrs = make_rsrc(p.qw, past ? 0u : w_bytes);
-    wr[slot] = __builtin_amdgcn_raw_buffer_load_b32(wrs, (int)w_lane_off,
-                                                    (int)(((uint32_t)t * (uint32_t)KS + (uint32_t)ks) * 256u), 0);
-    if constexpr (!XL) {
-      const __amdgpu_buffer_rsrc_t xrs = make_rsrc(p.a, past ? 0u : x_bytes);
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-        xr[slot][mt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)x_lane_off[mt], ks * 64, 0));
-    }
-  };
-#pragma unroll
-  for (int u = 0; u < D; ++u) issue(u);
-  // this wave's DMA (issued before the ring) has landed once at most the ring is in flight;
-  // the barrier then covers every wave's (with NORM the first barrier of the prologue)
-  AWQ_WAIT_VMCNT(XL ? D : D * (1 + MT));
-  if constexpr (NORM) npc.normalise(p, (uint16_t*)(smem + L.x), red, wave, lane, tid);
-  else __syncthreads();
-
   uint32_t zm0 = 0, zm1 = 0;  // biased zero of the current group (even / odd nibble forms)
-  float sf = 0.f;             // scale of the current group
+  float sf = 0.f;             // scale of the current group (0 before the first: flushes nothing)
   auto flush = [&]() {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
@@ -231,8 +245,7 @@ decode_narrow_kernel(const GemmArgs p, int tiles) {
     const uint16_t sb = s_lds[16 * g + r];
     sf = SBF ? bf_bits2f(sb) : h_bits2f(sb);
   };
-  auto compute = [&](int slot, int ks) {
-    const uint32_t w = wr[slot];
+  auto compute = [&](uint32_t w, int slot, int i, int ks) {
     u32x4 op;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -252,32 +265,35 @@ decode_narrow_kernel(const GemmArgs p, int tiles) {
       acc[0] = MfmaOp<T>::run(xv, op, acc[0]);
     } else {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) acc[mt] = MfmaOp<T>::run(xr[slot][mt], op, acc[mt]);
+      for (int mt = 0; mt < MT; ++mt) acc[mt] = MfmaOp<T>::run(xr[slot][i][mt], op, acc[mt]);
     }
   };
 
-  if (nunits > 0) {
-    int g_cur = -1, cks = ks0;
-    for (int done = 0; done < nunits; done += D) {
+  // quads in order; a quad starts on a group boundary (SPG divides 4), so group changes fall
+  // on fixed k-steps of it.  k-steps past K (the tile's last quad) are skipped.
+  for (int done = 0; done < nq; done += D) {
 #pragma unroll
-      for (int u = 0; u < D; ++u) {
-        if (done + u < nunits) {  // wave-uniform
-          const int ks = cks++;
-          const int g = ks / SPG;
-          if (g != g_cur) {
-            if (g_cur >= 0) flush();
-            g_cur = g;
-            prep(g);
+    for (int u = 0; u < D; ++u) {
+      if (done + u < nq) {  // wave-uniform
+        const int c = qa + done + u;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int ks = 4 * c + i;
+          if (ks < KS) {  // wave-uniform
+            if (i % SPG == 0) {
+              flush();
+              prep(ks / SPG);
+            }
+            compute(wr[u][i], u, i, ks);
           }
-          compute(u, ks);
         }
-        __builtin_amdgcn_sched_barrier(0);
-        issue(u);
-        __builtin_amdgcn_sched_barrier(0);
       }
+      __builtin_amdgcn_sched_barrier(0);
+      if (done + D < nq) issue(u);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    flush();
   }
+  flush();
 
   // ---- the waves' sums meet in LDS: lane (q, r), element v = token mt*16 + 4q + v, column r
 #pragma unroll
@@ -316,19 +332,21 @@ decode_narrow_kernel(const GemmArgs p, int tiles) {
   }
 }
 
-// Narrow stream pack: thread = one lane's u32 of one (tile, k-step) run.
+// Narrow stream pack: thread = one lane's u32 of one (tile, quad) run, number i = k-step
+// 4 c + i (zero past K and past N).
 __global__ void __launch_bounds__(256) pack_narrow_kernel(const uint32_t* __restrict__ in, uint32_t* __restrict__ out,
                                                           int64_t K, int64_t N, int64_t tiles) {
-  const int64_t KS = K / 32;
+  const int64_t KS = K / 32, KQ = (KS + 3) / 4;
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= tiles * KS * 64) return;
-  const int l = (int)(idx & 63);
-  const int64_t ts = idx >> 6;
-  const int64_t t = ts / KS, s = ts - t * KS;
+  if (idx >= tiles * KQ * 256) return;
+  const int i = (int)(idx & 3);
+  const int l = (int)((idx >> 2) & 63);
+  const int64_t tc = idx >> 8;
+  const int64_t t = tc / KQ, s = (tc - t * KQ) * 4 + i;
   const int q = l >> 4, r = l & 15;
   const int64_t col = t * 16 + r;
   uint32_t v = 0;
-  if (col < N) {
+  if (col < N && s < KS) {
     const int64_t NW = N / 8;
     const int sh = 4 * col_nib<false>((int)(col & 7));
     for (int j = 0; j < 8; ++j) {
@@ -349,11 +367,11 @@ static int narrow_status() {
   return e == hipSuccess ? AWQ_OK : AWQ_ERR_LAUNCH;
 }
 
-int64_t decode_narrow_bytes(int64_t K, int64_t N) { return cdiv(N, 16) * 16 * K / 2; }
+int64_t decode_narrow_bytes(int64_t K, int64_t N) { return cdiv(N, 16) * cdiv(K / 32, 4) * 1024; }
 
 int launch_pack_decode_narrow(const int32_t* qweight_kn, int32_t* out, int64_t K, int64_t N, hipStream_t st) {
   const int64_t tiles = cdiv(N, 16);
-  const int64_t n = tiles * (K / 32) * 64;
+  const int64_t n = tiles * cdiv(K / 32, 4) * 256;
   if (n > 0)
     hipLaunchKernelGGL(pack_narrow_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st, (const uint32_t*)qweight_kn,
                        (uint32_t*)out, K, N, tiles);

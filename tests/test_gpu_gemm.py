@@ -347,21 +347,22 @@ def _stream_layout_numpy(qw_kn):
 
 
 def _narrow_layout_numpy(qw):
-    """Narrow decode layout: (tile t, k-step s, lane 16 q + r) -> u32 holding column 16 t + r at
-    rows 32 s + 8 q + j, row j at bit 16 (j % 2) + 4 (j // 2)."""
+    """Narrow decode layout: (tile t, quad c, lane 16 q + r, i) -> u32 holding column 16 t + r
+    at rows 32 s + 8 q + j of k-step s = 4 c + i (zero past K), row j at bit 16 (j % 2) + 4 (j // 2)."""
     K, NW = qw.shape
     N = NW * 8
     tiles, KS = -(-N // 16), K // 32
-    pad = np.zeros((K, tiles * 16), dtype=np.uint32)
-    pad[:, :N] = O.unpack_awq(qw)
-    v = pad.reshape(KS, 4, 8, tiles, 16)                     # [s, q, j, t, r]
-    out = np.zeros((tiles, KS, 4, 16), dtype=np.uint32)
+    KQ = -(-KS // 4)
+    pad = np.zeros((KQ * 128, tiles * 16), dtype=np.uint32)
+    pad[:K, :N] = O.unpack_awq(qw)
+    v = pad.reshape(KQ, 4, 4, 8, tiles, 16)                  # [c, i, q, j, t, r]
+    out = np.zeros((tiles, KQ, 4, 16, 4), dtype=np.uint32)   # [t, c, q, r, i]
     for j in range(8):
-        out |= v[:, :, j].transpose(2, 0, 1, 3) << np.uint32((j & 1) * 16 + (j >> 1) * 4)
+        out |= v[:, :, :, j].transpose(3, 0, 2, 4, 1) << np.uint32((j & 1) * 16 + (j >> 1) * 4)
     return out.reshape(-1).view(np.int32)
 
 
-@pytest.mark.parametrize("K,N", [(256, 4096), (128, 1000), (64, 520), (32, 8)])
+@pytest.mark.parametrize("K,N", [(256, 4096), (128, 1000), (64, 520), (32, 8), (96, 24), (2816, 48)])
 def test_pack_decode_narrow_layout(K, N):
     ops = _lib()
     rng = np.random.default_rng(K * 3 + N)
