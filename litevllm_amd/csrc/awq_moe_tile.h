@@ -241,13 +241,15 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
       for (int mt = 0; mt < NMT; ++mt) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     int cur_group = -1;
-    // the group's per-nibble constants; with six token tiles (192 accumulator registers) the
-    // fp16 pair (zero, scale) of each nibble is kept packed in one register and unpacked per
-    // k-step (two byte permutes), which keeps the k-loop within the 256 registers of two waves
-    // per SIMD
+    // the group's per-nibble constants; with six token tiles (192 accumulator registers) only
+    // the raw scale words and zero word are held (five registers) and each nibble's biased zero
+    // is formed where it is used (two instructions; the scale half and both zero halves reach
+    // the packed operations through their operand selects), which keeps the k-loop within the
+    // 256 registers of two waves per SIMD
     constexpr bool PACK = FAST && NMT >= 6;
     ColConst cc[8];
-    uint32_t ccp[8];
+    u32x4 s4p = {0u, 0u, 0u, 0u};
+    uint32_t zwp = 0u;
     // one k-step from the slot at sb0; between nibble pairs, the pieces of request `req`
     // the lane index as an opaque value per k-step where registers are short (six tiles): the
     // lane offsets are then formed anew each k-step (a few VALU operations) instead of held
@@ -263,10 +265,11 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
         WordSZ sz;
         sz.s4 = lds16(sb0 + s_rd(ln));
         sz.zw = ZP ? lds4(sb0 + z_rd(ln)) : 0x88888888u;
-        prep_consts<false, FAST>(sz, sb, cc);
         if constexpr (PACK) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) ccp[i] = __builtin_amdgcn_perm(cc[i].sc, cc[i].zm, 0x05040100u);  // zm lo | sc lo << 16
+          s4p = sz.s4;
+          zwp = sz.zw;
+        } else {
+          prep_consts<false, FAST>(sz, sb, cc);
         }
         cur_group = g;
       }
@@ -274,20 +277,6 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
 #pragma unroll
       for (int mt = 0; mt < NMT; ++mt) af[mt] = lds16(sb0 + a_rd(ln) + (uint32_t)(mt * 16 * CPR * 16));
       const u32x4 wv0 = lds16(sb0 + w_rd(ln)), wv1 = lds16(sb0 + w_rd(ln) + 1024u);
-      // nibble I's constants: held, or unpacked right before use (packed form)
-      auto nib_const = [&](int I) __attribute__((always_inline)) {
-        if constexpr (PACK) {
-          uint32_t pk = ccp[I];
-          asm volatile("" : "+v"(pk));
-          ColConst c_;
-          c_.zm = __builtin_amdgcn_perm(pk, pk, 0x01000100u);
-          c_.sc = __builtin_amdgcn_perm(pk, pk, 0x03020302u);
-          c_.scf = 0.0f;
-          return c_;
-        } else {
-          return cc[I];
-        }
-      };
       // the word at k-rows 8 q + j (j = 0..7); pair rows (2u, 2u + 1) into lo/hi 16-bit halves
       uint32_t mlo[4], mhi[4];
       mlo[0] = pair_lo(wv0[0], wv0[1]);
@@ -298,9 +287,30 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
       mhi[2] = pair_hi(wv1[0], wv1[1]);
       mlo[3] = pair_lo(wv1[2], wv1[3]);
       mhi[3] = pair_hi(wv1[2], wv1[3]);
+      // nibble I's operand: from the held constants, or (six tiles) from the raw words, which
+      // pass through an opaque copy so that nothing derived from them is held across k-steps
+      auto operand = [&](auto i_c) __attribute__((always_inline)) {
+        constexpr int I = decltype(i_c)::value;
+        if constexpr (PACK) {
+          constexpr int c = nib_col<false>(I);
+          uint32_t zw = zwp, sw = s4p[c >> 1];
+          asm volatile("" : "+v"(zw), "+v"(sw));
+          const uint32_t z = (zw >> (4 * I)) & 0xFu;
+          const f16x2 zh = as_h2((I & 1) ? (0x5400u | (z << 4)) : (0x6400u | z));
+          const f16x2 zb = __builtin_shufflevector(zh, zh, 0, 0);
+          const f16x2 sh = as_h2(sw);
+          const f16x2 sc = (c & 1) ? __builtin_shufflevector(sh, sh, 1, 1) : __builtin_shufflevector(sh, sh, 0, 0);
+          u32x4 b;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) b[u] = as_u((as_h2(magic_bits<I & 3>(I < 4 ? mlo[u] : mhi[u], mk)) - zb) * sc);
+          return b;
+        } else {
+          return rows_operand<I, FAST, T>(mlo, mhi, cc[I], mk);
+        }
+      };
 #define AWQ_RB_NIB(I)                                                                       \
       {                                                                                     \
-        const u32x4 b = rows_operand<I, FAST, T>(mlo, mhi, nib_const(I), mk);               \
+        const u32x4 b = operand(std::integral_constant<int, I>{});                          \
         _Pragma("unroll") for (int mt = 0; mt < NMT; ++mt)                                  \
           acc[I][mt] = MfmaOp<T>::run(af[mt], b, acc[I][mt]);                               \
       }
@@ -348,39 +358,71 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
       if (s < n_my) compute(slot_of(s), s, s + PD - 1 < n_my ? s + PD - 1 : -1);
     }
 
-    // ---- the K-halves meet: second-half sums through LDS (two rounds of four nibbles),
-    // added to the first half's ----
-    constexpr int NVH = 4 * NMT * 4;  // floats per lane per round
-    float* red = (float*)&lds_all[0];
+    // ---- the K-halves meet.  down (and bf16 gate_up, short of registers for the exchange
+    // below): the second half's sums go through LDS to the first-half wave, which stores every
+    // row.  fp16 gate_up (whose epilogue also evaluates the activation): both finish the tile, the first-half wave of a stream tile taking token tiles 0 .. H0 - 1
+    // and the second-half wave the rest; each sends its partial sums of the other's tiles
+    // (16 bytes per lane and value) and adds the partner's to its own (a two-term fp32 sum is
+    // the same in either order).  Two rounds of four nibbles each ----
+    constexpr bool SPLIT = MODE == 0 && FAST;
+    constexpr int H0 = SPLIT ? (NMT + 1) / 2 : NMT;  // token tiles the first half finishes
+    if constexpr (SPLIT) {
+      f32x4* red4 = (f32x4*)&lds_all[0];  // [wave][4 nibbles][H0 tiles][64 lanes]
+      static_assert(NWV * 4 * H0 * 64 * 16 <= PD * SLOT * 16, "the exchange fits the stage slots");
+      const int partner = wave ^ kTST;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      __syncthreads();  // LDS free (stage reads done / previous round consumed)
-      if (kh == 1) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int mt = 0; mt < NMT; ++mt)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) red[((stl * NVH) + (i * NMT + mt) * 4 + v) * 64 + lane] = acc[4 * h + i][mt][v];
-      }
-      __syncthreads();
-      if (kh == 0) {
+      for (int h = 0; h < 2; ++h) {
+        __syncthreads();  // LDS free (stage reads done / previous round consumed)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-          for (int mt = 0; mt < NMT; ++mt)
+          for (int mt = 0; mt < NMT; ++mt) {
+            if (kh == 0 ? mt >= H0 : mt < H0)  // the partner's tile (wave-uniform)
+              red4[((wave * 4 + i) * H0 + (kh == 0 ? mt - H0 : mt)) * 64 + lane] = acc[4 * h + i][mt];
+          }
+        __syncthreads();
 #pragma unroll
-            for (int v = 0; v < 4; ++v) acc[4 * h + i][mt][v] += red[((stl * NVH) + (i * NMT + mt) * 4 + v) * 64 + lane];
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int mt = 0; mt < NMT; ++mt) {
+            if (kh == 0 ? mt < H0 : mt >= H0)  // this wave's tile
+              acc[4 * h + i][mt] += red4[((partner * 4 + i) * H0 + (kh == 0 ? mt : mt - H0)) * 64 + lane];
+          }
       }
+    } else {
+      constexpr int NVH = 4 * NMT * 4;  // floats per lane per round
+      float* red = (float*)&lds_all[0];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        __syncthreads();  // LDS free (stage reads done / previous round consumed)
+        if (kh == 1) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+              for (int v = 0; v < 4; ++v) red[((stl * NVH) + (i * NMT + mt) * 4 + v) * 64 + lane] = acc[4 * h + i][mt][v];
+        }
+        __syncthreads();
+        if (kh == 0) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+              for (int v = 0; v < 4; ++v) acc[4 * h + i][mt][v] += red[((stl * NVH) + (i * NMT + mt) * 4 + v) * 64 + lane];
+        }
+      }
+      if (kh == 1) return;
     }
-    if (kh == 1) return;
 
-    if (word < 0) return;
-    // ---- epilogue: acc[I][mt][v] = row 16 mt + 4 q + v, column 8 word + nib_col(I) ----
+    // ---- epilogue of this wave's token tiles: acc[I][mt][v] = row 16 mt + 4 q + v, column
+    // 8 word + nib_col(I) ----
     auto epilogue = [&](auto kind_c) __attribute__((always_inline)) {
       constexpr int KIND = decltype(kind_c)::value;
 #pragma unroll
       for (int mt = 0; mt < NMT; ++mt) {
+        if (kh == 0 ? mt >= H0 : mt < H0) continue;  // the partner's tile (wave-uniform)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int m = 16 * mt + 4 * q + v;
@@ -396,7 +438,7 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
               asm volatile("" : "+v"(gv));
               up[I] = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, gv), 0x128, 0xF, 0xF, false));
             }
-            if (r < 8 && m < rows) {
+            if (r < 8 && m < rows && word >= 0) {
               const int rt = s_rt[m];
               const float wgt = s_w[m];
               float h[8];
@@ -406,7 +448,7 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
               *(u32x4*)((uint16_t*)p.out + (int64_t)rt * p.ldo + 8 * word) = o;
             }
           } else {
-            if (m < rows) {
+            if (m < rows && word >= 0) {
               const int rt = s_rt[m];
               float y[8];
 #pragma unroll
