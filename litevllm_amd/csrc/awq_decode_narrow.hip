@@ -126,7 +126,8 @@ __global__ void __launch_bounds__(NWV * 64) decode_narrow_kernel(const GemmArgs 
   static_assert(!XL || MT == 1, "");
   static_assert(!NORM || (XL && ONE && std::is_same<T, f16>::value), "");
   static_assert(SPG == 1 || SPG == 2 || SPG == 4, "a quad holds whole groups or lies in one");
-  constexpr int D = XL ? 4 : 2;  // quads in flight per wave
+  // quads in flight per wave (measured at K = 4096: two, except four for one row in 8-wave blocks)
+  constexpr int D = (XL && ONE && NWV == 8) ? 4 : 2;
   constexpr int MROWS = ONE ? 1 : 16 * MT;
   extern __shared__ __align__(16) unsigned char smem[];
 
