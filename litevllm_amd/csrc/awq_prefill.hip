@@ -52,7 +52,7 @@ constexpr int kPSBM = 256, kPSBK = 64;
 
 template <int NWN, bool ZP, typename T, bool FAST>
 __global__ void __launch_bounds__(128 * NWN, 2) prefill_stream_kernel(const GemmArgs p, int scale_bf16, int tiles_m,
-                                                                      int tiles_n, int log2g) {
+                                                                      int tiles_n, int log2g, int n_off) {
   constexpr int NT = 128 * NWN;                // threads
   constexpr int BM = kPSBM, BN = 64 * NWN, BK = kPSBK;
   constexpr int CPR = BK / 8;                  // 16-byte chunks per LDS row
@@ -75,7 +75,7 @@ __global__ void __launch_bounds__(128 * NWN, 2) prefill_stream_kernel(const Gemm
   int bid = blockIdx.x;
   if ((ntiles & 7) == 0) bid = (bid & 7) * (ntiles >> 3) + (bid >> 3);
   const int tm = bid / tiles_n, tn = bid - tm * tiles_n;
-  const int m0 = tm * BM, n0 = tn * BN;
+  const int m0 = tm * BM, n0 = n_off + tn * BN;  // the launch covers columns n_off ..
 
   const int KS = p.K >> 5;                     // 32-row k-steps of the stream layout
   const int nst = (p.K + BK - 1) / BK;
@@ -334,16 +334,38 @@ template <bool ZP, typename T, bool FAST>
 static void launch_ps(const GemmArgs& a, int sbf, int log2g, hipStream_t st) {
   const int tm = (int)cdiv(a.M, kPSBM);
   const int tn4 = (int)cdiv(a.N, 256);
+  const int cus = num_cus();
+  auto wide = [&](int tiles_n, int n_off) {
+    hipLaunchKernelGGL((prefill_stream_kernel<4, ZP, T, FAST>), dim3(tm * tiles_n), dim3(512), 0, st, a, sbf, tm, tiles_n,
+                       log2g, n_off);
+  };
+  auto narrow = [&](int tiles_n, int n_off) {
+    hipLaunchKernelGGL((prefill_stream_kernel<2, ZP, T, FAST>), dim3(tm * tiles_n), dim3(256), 0, st, a, sbf, tm, tiles_n,
+                       log2g, n_off);
+  };
   // 256-column blocks (two waves per SIMD) once they cover three quarters of the CUs; below
   // that, twice as many 128-column blocks.  Measured on MI355X (K = 4096): M = 512, N = 24576
   // (192 blocks of 256 columns) 101 us against 134 us in 384 blocks of 128; M = 512, N = 12288
   // (96 blocks of 256 columns) 92 us against 74 us in 192 blocks of 128.
-  if ((int64_t)tm * tn4 * 4 >= (int64_t)num_cus() * 3) {
-    hipLaunchKernelGGL((prefill_stream_kernel<4, ZP, T, FAST>), dim3(tm * tn4), dim3(512), 0, st, a, sbf, tm, tn4, log2g);
-  } else {
-    const int tn2 = (int)cdiv(a.N, 128);
-    hipLaunchKernelGGL((prefill_stream_kernel<2, ZP, T, FAST>), dim3(tm * tn2), dim3(256), 0, st, a, sbf, tm, tn2, log2g);
+  if ((int64_t)tm * tn4 * 4 < (int64_t)cus * 3) {
+    narrow((int)cdiv(a.N, 128), 0);
+    return;
   }
+  // Whole rounds of 256-column blocks, then a part round of them as 128-column blocks in a
+  // second launch, where those fill the chip once: the part round runs at twice the blocks
+  // for half the work each instead of leaving CUs idle (M = 2048, N = 12288: 384 blocks, 1.5
+  // rounds).
+  if (cus % tm == 0) {
+    const int per_round = cus / tm;  // 256-column tiles per round of blocks
+    const int full = tn4 / per_round * per_round;
+    const int rest = (int)cdiv(a.N - full * 256, 128);
+    if (full > 0 && rest > 0 && (int64_t)tm * rest <= cus) {
+      wide(full, 0);
+      narrow(rest, full * 256);
+      return;
+    }
+  }
+  wide(tn4, 0);
 }
 
 bool launch_prefill_stream(const GemmArgs& a, bool zp, int act, int sdt, hipStream_t st) {
