@@ -407,28 +407,33 @@ moe_gemm_kernel(const MoeArgs p) {
         for (int v = 0; v < 4; ++v) {
           const int m = m0 + mt * 16 + 4 * q + v;
           const int rt = m < count ? route_at(m) : -1;
-          float o[8];
-#pragma unroll
-          for (int c = 0; c < 8; ++c) o[c] = tot[col_nib<false>(c)][mt][v];
           if constexpr (MODE == 0) {
-            // the up values of the same columns sit 8 lanes higher (tile words 8 .. 15)
-            float u[8];
+            // the up sums of the gate columns sit 8 lanes higher (tile words 8 .. 15).  Lane
+            // r < 8 finishes columns 0..3 of gate word 8 t + r and lane r + 8 columns 4..7 of
+            // the same word: per column pair, two row rotations by 8 that each write one half
+            // of the row (DPP bank mask; the other half keeps its own value) give every lane
+            // the gate and the up sum of its column
+            float gt[4], ut[4];
 #pragma unroll
-            for (int c = 0; c < 8; ++c) u[c] = __shfl_xor(o[c], 8);
-            const int gw = 8 * t + r;  // gate word
-            if (r < 8 && rt >= 0 && gw < p.half) {
+            for (int j = 0; j < 4; ++j) {
+              float a = tot[col_nib<false>(j)][mt][v], b = tot[col_nib<false>(4 + j)][mt][v];
+              asm volatile("" : "+v"(a), "+v"(b));
+              gt[j] = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, a), __builtin_bit_cast(int, b), 0x128, 0xF, 0xC, false));
+              ut[j] = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, b), __builtin_bit_cast(int, a), 0x128, 0xF, 0x3, false));
+            }
+            const int gw = 8 * t + (r & 7);  // gate word
+            if (rt >= 0 && gw < p.half) {
               const float wgt = load_route_weight(p.rw, p.rw_dtype, rt);
-              float h[8];
+              float h[4];
 #pragma unroll
-              for (int c = 0; c < 8; ++c) h[c] = gated_act(o[c], p.act_kind) * u[c] * wgt;
-              u32x4 st;
-              st[0] = pack2<T>(h[0], h[1]);
-              st[1] = pack2<T>(h[2], h[3]);
-              st[2] = pack2<T>(h[4], h[5]);
-              st[3] = pack2<T>(h[6], h[7]);
-              *(u32x4*)((uint16_t*)p.out + (int64_t)rt * p.ldo + 8 * gw) = st;
+              for (int j = 0; j < 4; ++j) h[j] = gated_act(gt[j], p.act_kind) * ut[j] * wgt;
+              *(u32x2*)((uint16_t*)p.out + (int64_t)rt * p.ldo + 8 * gw + (r & 8) / 2) =
+                  u32x2{pack2<T>(h[0], h[1]), pack2<T>(h[2], h[3])};
             }
           } else {
+            float o[8];
+#pragma unroll
+            for (int c = 0; c < 8; ++c) o[c] = tot[col_nib<false>(c)][mt][v];
             const int w = 16 * t + r;
             if (rt >= 0 && w < NW) {
               float* dst = (float*)p.out + (int64_t)rt * p.ldo + 8 * w;

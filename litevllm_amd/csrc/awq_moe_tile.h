@@ -427,25 +427,28 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
         for (int v = 0; v < 4; ++v) {
           const int m = 16 * mt + 4 * q + v;
           if constexpr (MODE == 0) {
-            // lanes 0..7 hold gate sums, lanes 8..15 the up sums of the same columns: rotate
-            // the 16-lane rows by 8 (every lane of the row active) to bring each up sum to its
-            // gate (each source value is first taken into a register of its own: a DPP move fed
-            // directly from an element of the accumulator tuple was compiled to read element 0)
-            float up[8];
+            // lanes 0..7 hold gate sums, lanes 8..15 the up sums of the same columns.  Lane r < 8
+            // finishes columns 0..3 of its word and lane r + 8 columns 4..7: per column pair, two
+            // row rotations by 8 that each write one half of the row (DPP bank mask; the other
+            // half keeps its own value) give every lane the gate and the up sum of its column.
+            // Each source value is first taken into a register of its own (a DPP move fed
+            // directly from an element of the accumulator tuple was compiled to read element 0).
+            float gt[4], ut[4];
 #pragma unroll
-            for (int I = 0; I < 8; ++I) {
-              float gv = acc[I][mt][v];
-              asm volatile("" : "+v"(gv));
-              up[I] = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, gv), 0x128, 0xF, 0xF, false));
+            for (int j = 0; j < 4; ++j) {
+              float a = acc[col_nib<false>(j)][mt][v], b = acc[col_nib<false>(4 + j)][mt][v];
+              asm volatile("" : "+v"(a), "+v"(b));
+              gt[j] = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, a), __builtin_bit_cast(int, b), 0x128, 0xF, 0xC, false));
+              ut[j] = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, b), __builtin_bit_cast(int, a), 0x128, 0xF, 0x3, false));
             }
-            if (r < 8 && m < rows && word >= 0) {
+            if (m < rows && word >= 0) {
               const int rt = s_rt[m];
               const float wgt = s_w[m];
-              float h[8];
+              float h[4];
 #pragma unroll
-              for (int I = 0; I < 8; ++I) h[nib_col<false>(I)] = gated_act_fast<KIND>(acc[I][mt][v]) * up[I] * wgt;
-              const u32x4 o = {pack2<T>(h[0], h[1]), pack2<T>(h[2], h[3]), pack2<T>(h[4], h[5]), pack2<T>(h[6], h[7])};
-              *(u32x4*)((uint16_t*)p.out + (int64_t)rt * p.ldo + 8 * word) = o;
+              for (int j = 0; j < 4; ++j) h[j] = gated_act_fast<KIND>(gt[j]) * ut[j] * wgt;
+              const int col = r < 8 ? 8 * word : 8 * (word - p.half) + 4;
+              *(u32x2*)((uint16_t*)p.out + (int64_t)rt * p.ldo + col) = u32x2{pack2<T>(h[0], h[1]), pack2<T>(h[2], h[3])};
             }
           } else {
             if (m < rows && word >= 0) {
