@@ -81,9 +81,10 @@ __device__ inline void moe_row_tile_wave(const int* counts, int E, int t, int& e
 //    the activation dtype right after.
 //  * The K-halves meet in LDS (fixed order: first half + second half), then lane (q, r) of the
 //    first-half wave holds the 8 columns 8 w .. 8 w + 7 of its word w for rows 4 q .. 4 q + 3 of
-//    each token tile, so the epilogue stores 8 contiguous values per row: for gate_up the up
-//    sums come from lane r + 8 (a row rotation by 8 lanes) and act(gate) * up * route_weight is
-//    rounded once into the intermediate; down writes fp32 rows per route.
+//    each token tile, so the epilogue stores contiguous values per row: for gate_up lane r
+//    (gate sums) and lane r + 8 (up sums of the same columns) trade halves through row
+//    rotations by 8 lanes, each finishes 4 of the word's columns, and act(gate) * up *
+//    route_weight is rounded once into the intermediate; down writes fp32 rows per route.
 // fp32 sums; the intermediate is rounded once to the activation dtype and down writes fp32
 // route rows, as in moe_gemm_kernel.  Every row is computed independently of its tile mates, so
 // results are bitwise reproducible.
