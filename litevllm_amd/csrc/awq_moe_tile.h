@@ -127,16 +127,6 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
   const int rows = __builtin_amdgcn_readfirstlane(s_tile[2]);
   if (e < 0) return;  // past the last row tile (whole block)
   const int n_mt = (rows + 15) >> 4;  // token tiles holding routes (block-uniform)
-  {
-    const int* list = p.lists + (int64_t)e * p.R;
-    if (tid < rows) {
-      const int rt = list[m0 + tid];
-      s_rt[tid] = rt;
-      s_w[tid] = MODE == 0 ? load_route_weight(p.rw, p.rw_dtype, rt) : 0.f;
-    }
-  }
-  __syncthreads();
-
   const int KS = p.K >> 5;
   const int NW = p.N >> 3;
   const int ngroups = p.K / p.G;
@@ -165,8 +155,7 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
     }
     return off;
   };
-  const uint32_t a_voff0 = a_off(stl);
-  const uint32_t a_voff4 = stl < A_TWO ? a_off(kTST + stl) : 0x80000000u;
+  uint32_t a_voff0 = 0x80000000u, a_voff4 = 0x80000000u;  // set once the route list is in LDS
 
   // ---- weights: the lane's piece of run (st, k-step): rows 8 q .. 8 q + 3 of word r at byte
   // 16 lane of the run, rows 8 q + 4 .. 8 q + 7 at 1024 + 16 lane; the DMA puts them at the
@@ -205,6 +194,33 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
       }
     }
   };
+  // the first requests' weights, scales and zeros depend on the expert only: requested before
+  // the route list is read, so their latency overlaps the list's
+  for (int s = 0; s < PD - 1; ++s)
+    if (s < n_my)
+#pragma unroll
+      for (int part = 1; part < 4; ++part) issue_part(s, part, lane);
+  {
+    const int* list = p.lists + (int64_t)e * p.R;
+    int rt = 0;
+    if (tid < rows) {
+      rt = list[m0 + tid];
+      s_rt[tid] = rt;
+      if (MODE == 0 && p.rw_dtype != AWQ_DTYPE_F32) s_w[tid] = load_route_weight(p.rw, p.rw_dtype, rt);
+    }
+    __syncthreads();
+    // fp32 route weights (read by the epilogue only) go to LDS by DMA, waited for with the
+    // first k-step's data
+    if (MODE == 0 && p.rw_dtype == AWQ_DTYPE_F32 && tid < rows) {
+      const uint32_t sw_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)&s_w[0];
+      lds_dma4(rsrc_words(p.rw, (uint32_t)p.R * 4u), sw_lds + (uint32_t)wave * 256u, (uint32_t)rt * 4u, 0u);
+    }
+  }
+  a_voff0 = a_off(stl);
+  if (stl < A_TWO) a_voff4 = a_off(kTST + stl);
+  for (int s = 0; s < PD - 1; ++s)
+    if (s < n_my) issue_part(s, 0, lane);
+
   // LDS byte offsets (within a slot) this lane reads
   auto a_rd = [&](int ln) __attribute__((always_inline)) {
     const int rr = ln & 15, qq = ln >> 4;
@@ -329,11 +345,10 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
 #undef AWQ_RB_NIB
     };
 
-    // requests for this half's k-steps 0 .. PD - 2
-    for (int s = 0; s < PD - 1; ++s)
-      if (s < n_my)
-#pragma unroll
-        for (int part = 0; part < 4; ++part) issue_part(s, part, lane);
+    // the requests for this half's k-steps 0 .. PD - 2 went out before the route list (weights,
+    // scales, zeros) and after it (activations), so their order differs from one request per
+    // k-step: all of them (and the route weights' DMA) are waited for here
+    AWQ_WAIT_VMCNT0();
     for (int s = 0; s < n0; ++s) {
       // this k-step's DMAs have landed (the PD - 2 after it may stay in flight)
       if (s < n_my) {

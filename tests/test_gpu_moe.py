@@ -417,3 +417,19 @@ def test_moe_mfma_path_bf16():
     assert np.max(d_ / O.fp16_ulp(exact, floor)) <= 16.0
     assert d_.sum() / np.abs(exact).sum() <= 2e-3
 
+
+
+@pytest.mark.parametrize("wdtype", [torch.float16, torch.bfloat16])
+def test_moe_mfma_path_16bit_routing_weights(wdtype):
+    # the tile kernels read fp32 routing weights by LDS DMA and 16-bit ones by plain loads:
+    # the same weight values in either dtype give the same bits
+    T, E, H, I, topk, G = 96, 4, 256, 128, 2, 64   # 48 routes per expert: tile kernels
+    p, d = _problem(T, E, H, I, topk, G, seed=11)
+    tw, tid = _route_cpu(torch.from_numpy(p["logits"]), topk)
+    tw16 = tw.to(wdtype)
+    x = _dev(p["x"])
+    args = (d["gq"], d["gs"], d["gz"], d["dq"], d["ds"], d["dz"], G)
+    y16 = ops.moe(x, tw16.to(DEV), tid.to(DEV), *args)
+    y32 = ops.moe(x, tw16.float().to(DEV), tid.to(DEV), *args)
+    torch.cuda.synchronize()
+    assert torch.equal(y16.view(torch.int16), y32.view(torch.int16))
