@@ -381,8 +381,9 @@ int launch_pack_decode_narrow(const int32_t* qweight_kn, int32_t* out, int64_t K
 
 // 16 waves per block (one block per CU) when the tiles fit the CUs once and the activations
 // come from LDS, else 8 (two per CU; with per-k-step activation loads 8 waves also measured
-// faster at one tile per CU); one token tile stages its activation rows in LDS when they fit
-constexpr uint32_t kNarrowLdsMax = 65536;
+// faster at one tile per CU); one token tile stages its activation rows in LDS when they fit:
+// in 64 KiB, or in the CU's 160 KiB when the tiles fit the CUs once (one block per CU anyway)
+constexpr uint32_t kNarrowLdsMax = 65536, kNarrowLdsMaxOne = 163840;
 
 template <int MT, bool ZP, typename T, bool SBF, bool ONE, bool XL, bool NORM = false>
 static bool launch_narrow_t(const GemmArgs& a, hipStream_t st) {
@@ -391,7 +392,7 @@ static bool launch_narrow_t(const GemmArgs& a, hipStream_t st) {
   const dim3 grid((unsigned)tiles);
   const int nwv = (tiles <= num_cus() && XL) ? 16 : 8;
   const NarrowLds L = narrow_lds(nwv, ONE ? 1 : 16 * MT, a.K / a.G, a.K, ZP, XL ? a.M : 0);
-  if (L.total > kNarrowLdsMax) return false;
+  if (L.total > (tiles <= num_cus() ? kNarrowLdsMaxOne : kNarrowLdsMax)) return false;
   if (NORM && a.K / 8 > (int64_t)kNormCols * nwv * 64) return false;
 #define AWQ_NARROW_L(NWV, SPG_) \
   hipLaunchKernelGGL((decode_narrow_kernel<MT, NWV, SPG_, ZP, T, SBF, ONE, XL, NORM>), grid, dim3((NWV) * 64), L.total, st, a, tiles)
