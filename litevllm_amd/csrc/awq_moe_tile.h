@@ -112,21 +112,7 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
   const int q = lane >> 4, r = lane & 15;
 
   const int cg = blockIdx.x % col_groups;
-  if (wave == 0) {
-    int te, tm0, trows;
-    moe_row_tile_wave(p.counts, E, blockIdx.x / col_groups, te, tm0, trows);
-    if (lane == 0) {
-      s_tile[0] = te;
-      s_tile[1] = tm0;
-      s_tile[2] = trows;
-    }
-  }
-  __syncthreads();
-  const int e = __builtin_amdgcn_readfirstlane(s_tile[0]);
-  const int m0 = __builtin_amdgcn_readfirstlane(s_tile[1]);
-  const int rows = __builtin_amdgcn_readfirstlane(s_tile[2]);
-  if (e < 0) return;  // past the last row tile (whole block)
-  const int n_mt = (rows + 15) >> 4;  // token tiles holding routes (block-uniform)
+  const int t_tile = blockIdx.x / col_groups;  // this block's row tile
   const int KS = p.K >> 5;
   const int NW = p.N >> 3;
   const int ngroups = p.K / p.G;
@@ -144,6 +130,7 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
   // 16 i + lane / 4, slot lane % 4, holding k-chunk slot ^ ((row / 2) & 3); wave (stl, kh)
   // issues DMA stl of its half, and waves stl < 2 also DMA 4 + stl ----
   const u32x4 ars = rsrc_words(p.a, (uint32_t)((uint64_t)p.rows_a * (uint64_t)p.lda * 2u));
+  int rows = 0;
   auto a_off = [&](int i) {
     const int row = 16 * i + (lane >> 2);
     const int kc = (lane & 3) ^ ((row >> 1) & 3);
@@ -162,11 +149,14 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
   // same lane's place in LDS.  Scales (16 bytes: the word's 8 columns) and zeros (the word)
   // of the k-step's group likewise, by lanes 0..15 ----
   const uint32_t stream_bytes = (uint32_t)p.tiles * (uint32_t)KS * 2048u;
-  const u32x4 wrs = rsrc_words((const char*)p.qw + (int64_t)e * stream_bytes, wave_on ? stream_bytes : 0u);
   const uint32_t w_run = (uint32_t)(wave_on ? st : 0) * (uint32_t)KS * 2048u;  // + 16 lane
-  const u32x4 srs = rsrc_words(p.sc + (int64_t)e * ngroups * p.N, (uint32_t)ngroups * (uint32_t)p.N * 2u);
-  const u32x4 zrs = rsrc_words(ZP ? (const void*)(p.qz + (int64_t)e * ngroups * NW) : (const void*)p.sc,
-                               ZP ? (uint32_t)ngroups * (uint32_t)NW * 4u : 0u);
+  u32x4 wrs, srs, zrs;  // expert ex's stream copy, scales and zeros
+  auto set_expert = [&](int ex) {
+    wrs = rsrc_words((const char*)p.qw + (int64_t)ex * stream_bytes, wave_on ? stream_bytes : 0u);
+    srs = rsrc_words(p.sc + (int64_t)ex * ngroups * p.N, (uint32_t)ngroups * (uint32_t)p.N * 2u);
+    zrs = rsrc_words(ZP ? (const void*)(p.qz + (int64_t)ex * ngroups * NW) : (const void*)p.sc,
+                     ZP ? (uint32_t)ngroups * (uint32_t)NW * 4u : 0u);
+  };
   // DMA instructions per k-step: activation (1, or 2 for waves stl < A_TWO), weight (2),
   // scales (1), zeros (1)
   constexpr int NB_REST = 2 + 1 + (ZP ? 1 : 0);
@@ -194,17 +184,55 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
       }
     }
   };
-  // the first requests' weights, scales and zeros depend on the expert only: requested before
-  // the route list is read, so their latency overlaps the list's
-  for (int s = 0; s < PD - 1; ++s)
-    if (s < n_my)
+  // the first requests' weights, scales and zeros (they depend on the expert only)
+  auto issue_wsz = [&]() {
+    for (int s = 0; s < PD - 1; ++s)
+      if (s < n_my)
 #pragma unroll
-      for (int part = 1; part < 4; ++part) issue_part(s, part, lane);
+        for (int part = 1; part < 4; ++part) issue_part(s, part, lane);
+  };
+
+  // ---- the row tile is found from the route counts (one round of loads).  Before that, the
+  // block bets on the usual prefill case, every expert with 1 .. BM - 1 routes: row tile t is
+  // then expert t's only tile, its routes from 0.  The bet's weights, scales and zeros and
+  // its first BM list entries are requested at once; a lost bet waits for them and asks
+  // again, so the bet changes only when the data arrive ----
+  const bool bet = t_tile < E;  // block-uniform
+  int e_cur = bet ? t_tile : 0;
+  set_expert(e_cur);
+  if (bet) issue_wsz();
+  int rt_bet = 0;
+  if (bet && tid < BM && tid < p.R) rt_bet = p.lists[(int64_t)e_cur * p.R + tid];
+  if (wave == 0) {
+    int te, tm0, trows;
+    moe_row_tile_wave(p.counts, E, t_tile, te, tm0, trows);
+    if (lane == 0) {
+      s_tile[0] = te;
+      s_tile[1] = tm0;
+      s_tile[2] = trows;
+    }
+  }
+  __syncthreads();
+  const int e = __builtin_amdgcn_readfirstlane(s_tile[0]);
+  const int m0 = __builtin_amdgcn_readfirstlane(s_tile[1]);
+  rows = __builtin_amdgcn_readfirstlane(s_tile[2]);
+  if (e < 0) {  // past the last row tile (whole block); no LDS DMA may land after the exit
+    AWQ_WAIT_VMCNT0();
+    return;
+  }
+  const int n_mt = (rows + 15) >> 4;  // token tiles holding routes (block-uniform)
+  const bool won = bet && e == e_cur && m0 == 0;  // block-uniform
+  if (!won) {
+    AWQ_WAIT_VMCNT0();  // the bet's DMAs have landed before their slots are requested again
+    e_cur = e;
+    set_expert(e);
+    issue_wsz();
+  }
   {
     const int* list = p.lists + (int64_t)e * p.R;
     int rt = 0;
     if (tid < rows) {
-      rt = list[m0 + tid];
+      rt = won ? rt_bet : list[m0 + tid];
       s_rt[tid] = rt;
       if (MODE == 0 && p.rw_dtype != AWQ_DTYPE_F32) s_w[tid] = load_route_weight(p.rw, p.rw_dtype, rt);
     }
