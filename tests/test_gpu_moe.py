@@ -433,3 +433,18 @@ def test_moe_mfma_path_16bit_routing_weights(wdtype):
     y32 = ops.moe(x, tw16.float().to(DEV), tid.to(DEV), *args)
     torch.cuda.synchronize()
     assert torch.equal(y16.view(torch.int16), y32.view(torch.int16))
+
+
+def test_moe_tile_path_fewer_row_tiles_than_experts():
+    # every route on experts 5 and 2 (256 each: two full 96-route tiles and a 64-route
+    # partial per expert, six row tiles for eight experts): row tile t is not expert t's, and
+    # the blocks of row tiles 6 and 7 find no tile at all
+    T, E, H, I, topk, G = 256, 8, 256, 128, 2, 128
+    assert _mfma_path(T, E, H, I, topk, G)
+    p, d = _problem(T, E, H, I, topk, G, seed=13)
+    tid = torch.tensor([[5, 2]] * T, dtype=torch.int64)
+    tw = torch.rand(T, topk, generator=torch.Generator().manual_seed(1))
+    y = ops.moe(_dev(p["x"]), tw.to(DEV), tid.to(DEV), d["gq"], d["gs"], d["gz"], d["dq"], d["ds"], d["dz"], G)
+    w1, w2 = _experts_used(p, d, G, True)
+    exact = O.moe_grouped_exact(p["x"], tw.numpy(), tid.numpy(), w1, w2)
+    _check(y.cpu().numpy(), exact, "fewer row tiles than experts")
