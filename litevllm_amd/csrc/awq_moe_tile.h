@@ -16,7 +16,9 @@ constexpr int kTBM = 96, kTBK = 32, kTST = 4, kTPD = 5;
 // every expert's last partial tile, so the heavy tiles are dispatched first.  Computed by one
 // wave from the per-expert route counts, 64 experts per pass (one count per lane, prefix sums
 // across the wave), so a block spends one round of count loads on it.  e = -1 past the end.
-__device__ inline void moe_row_tile_wave(const int* counts, int E, int t, int& e, int& m0, int& rows) {
+// have0: the lane's count of expert `lane` is already in cnt0 (the first 64 experts).
+__device__ inline void moe_row_tile_wave(const int* counts, int E, int t, int& e, int& m0, int& rows, bool have0 = false,
+                                         int cnt0 = 0) {
   const int lane = threadIdx.x & 63;
   auto prefix = [&](int v) {  // inclusive prefix sum over the wave
 #pragma unroll
@@ -34,7 +36,7 @@ __device__ inline void moe_row_tile_wave(const int* counts, int E, int t, int& e
     int base = 0;
     for (int c0 = 0; c0 < E; c0 += 64) {
       const int ex = c0 + lane;
-      const int cnt = ex < E ? counts[ex] : 0;
+      const int cnt = (have0 && c0 == 0) ? cnt0 : (ex < E ? counts[ex] : 0);
       const int n = phase == 0 ? cnt / kTBM : (cnt % kTBM != 0 ? 1 : 0);
       const int incl = prefix(n);
       const int tot = __shfl(incl, 63);
@@ -198,14 +200,26 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
   // its first BM list entries are requested at once; a lost bet waits for them and asks
   // again, so the bet changes only when the data arrive ----
   const bool bet = t_tile < E;  // block-uniform
+  // wave 0 requests the counts of experts 0..63 ahead of its bet (an assembly load, waited for
+  // below by count: the bet's DMAs after it stay in flight)
+  uint32_t cnt0 = 0;
+  if (wave == 0) {
+    const u32x4 crs = rsrc_words(p.counts, (uint32_t)E * 4u);  // lanes past E read zero
+    asm volatile("buffer_load_dword %0, %1, %2, %3 offen" : "=v"(cnt0) : "v"((uint32_t)lane * 4u), "s"(crs), "s"(0u) : "memory");
+  }
   int e_cur = bet ? t_tile : 0;
   set_expert(e_cur);
   if (bet) issue_wsz();
   int rt_bet = 0;
   if (bet && tid < BM && tid < p.R) rt_bet = p.lists[(int64_t)e_cur * p.R + tid];
   if (wave == 0) {
+    // issued after the counts: the bet's NB_REST DMAs for each of its first PD - 1 k-steps (and
+    // the list load, not counted: a smaller count only waits longer)
+    if (bet && n_my >= PD - 1) AWQ_WAIT_VMCNT((PD - 1) * NB_REST);
+    else AWQ_WAIT_VMCNT0();
+    pin_after_wait(cnt0);
     int te, tm0, trows;
-    moe_row_tile_wave(p.counts, E, t_tile, te, tm0, trows);
+    moe_row_tile_wave(p.counts, E, t_tile, te, tm0, trows, true, (int)cnt0);
     if (lane == 0) {
       s_tile[0] = te;
       s_tile[1] = tm0;
