@@ -353,17 +353,18 @@ def rot_copies(K, N):
     return max(2, -(-ROT_BYTES // weight_bytes(K, N)))
 
 
-def _time_rotation(torch, ops, X, pool, Y, reps, **kw):
-    """us per launch of gemm(X, w) over every weight copy of `pool` (a graph of back-to-back
-    launches, replayed `reps` times).  The graph passes over the pool often enough to hold at
-    least 200 launches: a replay costs about 20 us of its own, which over a 21-launch graph
-    would add 1 us to every launch."""
+def _time_rotation(torch, ops, X, pool, Y, reps, fn=None, **kw):
+    """us per launch of gemm(X, w) (or ``fn``, same arguments) over every weight copy of `pool`
+    (a graph of back-to-back launches, replayed `reps` times).  The graph passes over the pool
+    often enough to hold at least 200 launches: a replay costs about 20 us of its own, which
+    over a 21-launch graph would add 1 us to every launch."""
     inner = max(1, -(-200 // len(pool)))
+    call = fn or ops.gemm
 
     def run():
         for _ in range(inner):
             for qw, qz, sc in pool:
-                ops.gemm(X, qw, sc, qz, G, layout="autoawq", out=Y, **kw)
+                call(X, qw, sc, qz, G, layout="autoawq", out=Y, **kw)
     ms, g = _time_graph(torch, run, reps)
     del g
     return ms * 1e3 / (inner * len(pool))
@@ -511,6 +512,19 @@ def main():
         c2["copies"] = len(W2)
         configs["config2"] = c2
         del W2
+        # row-exact mode (one launch, a grid row per input row, each row the M = 1 plan) against
+        # a plain GEMM of the same rows, at configs[1]'s K and two of its widths
+        rx = {}
+        for n in (4096, 24576):
+            Wr = _weights(torch, K_DEC, n, rot_copies(K_DEC, n), dev, 53 + n)
+            for m in (2, 4):
+                xr = torch.randn((m, K_DEC), device=dev, generator=gen).half()
+                yr = torch.empty((m, n), device=dev, dtype=torch.float16)
+                e = _hbm_entry(_time_rotation(torch, ops, xr, Wr, yr, 20, fn=ops.gemm_rows_exact), m, K_DEC, n)
+                e["us_plain_gemm"] = round(_time_rotation(torch, ops, xr, Wr, yr, 20), 3)
+                rx[f"M{m}_N{n}"] = e
+            del Wr
+        configs["rows_exact"] = rx
         c3 = {}
         for n in (12288, 24576):
             W3 = _weights(torch, K_DEC, n, 3, dev, 52 + n)

@@ -65,10 +65,15 @@ extern "C" {
  *                      M (K % 32 == 0): the decode kernel serves M <= 32 with group sizes
  *                      32/64/128, the prefill kernel the rest, so one copy serves both.
  * AWQ_LAYOUT_DECODE_NARROW : an AUTOAWQ qweight re-ordered by awq_w4a16_pack_decode_narrow
- *                      into 16-column tiles (one 32-bit word per column and 8 rows), read by
- *                      the narrow decode kernel: one block per 16 columns over the whole K,
- *                      no split-K.  For decode shapes whose N is small against the chip
- *                      (N <= 16 x 2 x CUs); same conditions as DECODE_STREAM.
+ *                      into 16-column tiles cut along K into quads of four 32-row k-steps
+ *                      (KQ = ceil(K / 128) quads per tile; k-steps past K are zero): the run of
+ *                      (tile t, quad c) is 1 KiB at byte (t * KQ + c) * 1024, lane l = 16 q + r
+ *                      owns its 16 bytes at 16 l, and u32 number i of them holds k-step
+ *                      s = 4 c + i of column 16 t + r, rows 32 s + 8 q + j (j < 8).  Read by the
+ *                      narrow decode kernel: one block per 16 columns over the whole K, no
+ *                      split-K.  Accepted by awq_w4a16_gemm only for M <= 32, group sizes
+ *                      32 / 64 / 128 and K % 32 == 0 (prefill-sized calls need DECODE_STREAM
+ *                      or AUTOAWQ).
  */
 #define AWQ_LAYOUT_AUTOAWQ 0
 #define AWQ_LAYOUT_KN_SEQ 1
@@ -169,8 +174,18 @@ int awq_w4a16_gemm_noalloc(const void* a, int64_t lda, const int32_t* qweight, c
  * packed_int4_symmetric_group32_rows_exact_msmall_safe, vllm/kernels/triton/awq_fused_gemm.py:
  * 1066-1143, 2925-2998), whose contract is that M = 2 / 4 rows equal independent M = 1 calls
  * (tests/test_awq_fused_gemm_numerics.py:128-161); here for any M, group size and layout the
- * M = 1 call takes.  Arguments and requirements as awq_w4a16_gemm; the workspace is the M = 1
- * call's (awq_w4a16_gemm_workspace_bytes(1, ...)).  One launch per row, in row order. */
+ * M = 1 call takes.  Arguments and requirements as awq_w4a16_gemm.  With group size 32, 64 or
+ * 128 (the decode kernels) it is one launch over a grid of (the M = 1 call's blocks) x M, as the
+ * reference's grid (cdiv(N, BN), M) (awq_fused_gemm.py:2980-2981): grid row m runs row m's
+ * M = 1 problem, with split-K counters and partials of its own, so the workspace holds M sets
+ * of them (awq_w4a16_gemm_rows_exact_workspace_bytes).  Other group sizes take one launch per
+ * row, in row order. */
+/* Workspace bytes of awq_w4a16_gemm_rows_exact for M rows (0 if none): the 64 KiB counter
+ * region, then M times the fp32 partials of the M = 1 call (awq_w4a16_gemm_workspace_bytes(1,
+ * ...)).  Same zero-on-entry, zero-on-exit counter rule as awq_w4a16_gemm's workspace. */
+size_t awq_w4a16_gemm_rows_exact_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_size,
+                                                 int32_t split_k, int32_t layout);
+
 int awq_w4a16_gemm_rows_exact(const void* a, int64_t lda, const int32_t* qweight, const void* scales,
                               const int32_t* qzeros, const void* bias, void* c, int64_t ldc, int64_t M,
                               int64_t N, int64_t K, int32_t group_size, int32_t split_k, int32_t layout,

@@ -48,14 +48,12 @@ def _kernel_policy(config: Any | None = None, policy: dict | None = None) -> dic
     return kp if isinstance(kp, dict) else {}
 
 
-def _parse_split(raw) -> int | None:
-    if raw is None:
-        return None
-    s = str(raw).strip().lower()
-    if s in ("", "auto"):
-        return None
+def _parse_forced(raw) -> int:
+    """A forced split-K value: an integer clamped to >= 1, anything unparsable (the empty
+    string included) 1 -- ``int(raw)`` with the reference's ``ValueError`` fallback
+    (``awq_fused_gemm.py:436-441``)."""
     try:
-        return max(1, int(s))
+        return max(1, int(str(raw).strip().lower()))
     except ValueError:
         return 1
 
@@ -63,13 +61,22 @@ def _parse_split(raw) -> int | None:
 def _select_split_k(m: int, n: int, k: int, *, config: Any | None = None,
                     policy: dict | None = None) -> int:
     """Split-K knob with the reference's precedence (``awq_fused_gemm.py:420-469``):
-    tool override, then ``kernel_policy["awq_fused_gemm_split_k"]``, then the tuning
-    snapshot.  Returns 0 for "auto" (the library plans the partition)."""
-    for raw in (_AWQ_FUSED_TUNING.get("FASTINFERENCE_AWQ_FUSED_GEMM_SPLIT_K"),
-                _kernel_policy(config, policy).get("awq_fused_gemm_split_k")):
-        v = _parse_split(raw)
-        if v is not None:
-            return v
+      * the tool override ``FASTINFERENCE_AWQ_FUSED_GEMM_SPLIT_K`` of the tuning snapshot, when
+        the key is present at all (an empty or unparsable value forces 1, as ``int()``'s
+        ``ValueError`` does there);
+      * ``kernel_policy["awq_fused_gemm_split_k"]`` unless it is ``""`` or ``"auto"``;
+      * otherwise "auto".  (The reference's later snapshot lookup, ``456-462``, can only see a
+        key the tool override has already taken, so it never decides.)
+    Returns 0 for "auto": the library plans the partition for the MI355X (the reference's
+    auto rule, ``470-501``, sizes a 16-24-program gfx1151 grid and is not reproduced)."""
+    if "FASTINFERENCE_AWQ_FUSED_GEMM_SPLIT_K" in _AWQ_FUSED_TUNING:
+        return _parse_forced(_AWQ_FUSED_TUNING["FASTINFERENCE_AWQ_FUSED_GEMM_SPLIT_K"])
+    kp = _kernel_policy(config, policy)
+    if "awq_fused_gemm_split_k" in kp:
+        # a present None reaches the reference's last lookup as the string "none": forced 1
+        raw = str(kp["awq_fused_gemm_split_k"]).strip().lower()
+        if raw not in ("", "auto"):
+            return _parse_forced(raw)
     return 0
 
 

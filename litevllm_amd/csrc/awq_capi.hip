@@ -134,11 +134,15 @@ size_t awq_w4a16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t g
   return ws;
 }
 
-int awq_w4a16_gemm(const void* a, int64_t lda, const int32_t* qweight, const void* scales,
-                   const int32_t* qzeros, const void* bias, void* c, int64_t ldc, int64_t M,
-                   int64_t N, int64_t K, int32_t group_size, int32_t split_k, int32_t layout,
-                   int32_t act_dtype, int32_t scale_dtype, int32_t bias_dtype, void* workspace,
-                   size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+// The body of awq_w4a16_gemm.  rows > 1 (M == 1): a row-exact launch of the decode kernels, grid
+// row y computing row y (activation row a + y lda, output row c + y ldc) exactly as a lone M = 1
+// call does, with split-K counters and partials of its own.
+static int gemm_impl(const void* a, int64_t lda, const int32_t* qweight, const void* scales, const int32_t* qzeros,
+                     const void* bias, void* c, int64_t ldc, int64_t M, int64_t N, int64_t K, int32_t group_size,
+                     int32_t split_k, int32_t layout, int32_t act_dtype, int32_t scale_dtype, int32_t bias_dtype,
+                     void* workspace, size_t workspace_bytes, void* stream, int64_t rows) {
   if (!a || !qweight || !scales || !c) return AWQ_ERR_NULL;
   if (bias && bias_dtype == AWQ_DTYPE_NONE) return AWQ_ERR_UNSUPPORTED;
   if (!dtype_16(act_dtype) || !dtype_16(scale_dtype)) return AWQ_ERR_UNSUPPORTED;
@@ -149,6 +153,7 @@ int awq_w4a16_gemm(const void* a, int64_t lda, const int32_t* qweight, const voi
   if (split_k < 0) return AWQ_ERR_SHAPE;
   if (M == 0 || N == 0) return AWQ_OK;
   if (lda < K || ldc < N || (lda % 8) != 0 || (ldc % 8) != 0) return AWQ_ERR_STRIDE;
+  if (rows > 1 && (M != 1 || !decode_covers(1, group_size))) return AWQ_ERR_UNSUPPORTED;
   if ((((uintptr_t)a) & 15) || (((uintptr_t)c) & 15) || (((uintptr_t)scales) & 15) ||
       (((uintptr_t)qweight) & 15))
     return AWQ_ERR_STRIDE;
@@ -160,6 +165,7 @@ int awq_w4a16_gemm(const void* a, int64_t lda, const int32_t* qweight, const voi
     return AWQ_ERR_UNSUPPORTED;
   // 32-bit buffer offsets: weights, activations and the output must stay below 2 GiB
   if (decode_stream_bytes(K, N) > 0x7FFFFFFFLL || M * lda * 2 > 0x7FFFFFFFLL) return AWQ_ERR_UNSUPPORTED;
+  if (rows > 0x7FFF) return AWQ_ERR_UNSUPPORTED;  // grid rows
   hipStream_t st = (hipStream_t)stream;
 
   GemmArgs ga{};
@@ -176,6 +182,7 @@ int awq_w4a16_gemm(const void* a, int64_t lda, const int32_t* qweight, const voi
   ga.K = (int)K;
   ga.G = group_size;
   ga.bias_dtype = bias ? bias_dtype : AWQ_DTYPE_NONE;
+  ga.rows = rows > 1 ? (int)rows : 0;
   const bool seq = layout == AWQ_LAYOUT_KN_SEQ;
   const bool zp = qzeros != nullptr;
 
@@ -187,8 +194,10 @@ int awq_w4a16_gemm(const void* a, int64_t lda, const int32_t* qweight, const voi
     const DecodeMode mode = decode_mode(layout, act_dtype, scale_dtype);
     const DecodePlan sp = plan_decode(M, N, K, group_size, split_k, mode);
     if (sp.ws_bytes) {
-      if (!workspace || workspace_bytes < sp.ws_bytes) return AWQ_ERR_WORKSPACE;
-      if ((size_t)sp.tiles * sizeof(int) > kCounterBytes) return AWQ_ERR_UNSUPPORTED;
+      // a row-exact launch holds `rows` sets of counters and partials, one per grid row
+      const size_t nrow = rows > 1 ? (size_t)rows : 1;
+      if (!workspace || workspace_bytes < kCounterBytes + nrow * (sp.ws_bytes - kCounterBytes)) return AWQ_ERR_WORKSPACE;
+      if (nrow * (size_t)sp.tiles * sizeof(int) > kCounterBytes) return AWQ_ERR_UNSUPPORTED;
       if (sp.ws_bytes - kCounterBytes > 0x7FFFFFFFu) return AWQ_ERR_UNSUPPORTED;  // 32-bit offsets
       ga.counters = (int*)workspace;
       ga.partial = (float*)((char*)workspace + kCounterBytes);
@@ -203,6 +212,17 @@ int awq_w4a16_gemm(const void* a, int64_t lda, const int32_t* qweight, const voi
     return AWQ_ERR_UNSUPPORTED;
   }
   return launch_status();
+}
+
+extern "C" {
+
+int awq_w4a16_gemm(const void* a, int64_t lda, const int32_t* qweight, const void* scales,
+                   const int32_t* qzeros, const void* bias, void* c, int64_t ldc, int64_t M,
+                   int64_t N, int64_t K, int32_t group_size, int32_t split_k, int32_t layout,
+                   int32_t act_dtype, int32_t scale_dtype, int32_t bias_dtype, void* workspace,
+                   size_t workspace_bytes, void* stream) {
+  return gemm_impl(a, lda, qweight, scales, qzeros, bias, c, ldc, M, N, K, group_size, split_k, layout, act_dtype,
+                   scale_dtype, bias_dtype, workspace, workspace_bytes, stream, 1);
 }
 
 size_t awq_w4a16_gemm_noalloc_max_workspace(void) { return kNoallocScratchBytes; }
@@ -224,6 +244,13 @@ int awq_w4a16_gemm_noalloc(const void* a, int64_t lda, const int32_t* qweight, c
                         act_dtype, scale_dtype, bias_dtype, ws, need > 0 ? kNoallocScratchBytes : 0, stream);
 }
 
+size_t awq_w4a16_gemm_rows_exact_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_size,
+                                                 int32_t split_k, int32_t layout) {
+  const size_t one = awq_w4a16_gemm_workspace_bytes(1, N, K, group_size, split_k, layout);
+  if (M <= 0 || one == 0) return 0;
+  return kCounterBytes + (size_t)M * (one - kCounterBytes);
+}
+
 int awq_w4a16_gemm_rows_exact(const void* a, int64_t lda, const int32_t* qweight, const void* scales,
                               const int32_t* qzeros, const void* bias, void* c, int64_t ldc, int64_t M,
                               int64_t N, int64_t K, int32_t group_size, int32_t split_k, int32_t layout,
@@ -233,12 +260,16 @@ int awq_w4a16_gemm_rows_exact(const void* a, int64_t lda, const int32_t* qweight
   if (M < 0) return AWQ_ERR_SHAPE;
   if (M == 0 || N == 0) return AWQ_OK;
   if (M > 1 && (lda < K || ldc < N)) return AWQ_ERR_STRIDE;
+  // the decode kernels' group sizes: one launch of M grid rows, each row the M = 1 problem
+  if (M == 1 || (group_size > 0 && decode_covers(1, group_size)))
+    return gemm_impl(a, lda, qweight, scales, qzeros, bias, c, ldc, 1, N, K, group_size, split_k, layout, act_dtype,
+                     scale_dtype, bias_dtype, workspace, workspace_bytes, stream, M);
+  // other group sizes take the prefill kernel at M = 1: one launch per row, in row order
   const int64_t ebytes = 2;  // both activation dtypes are 16-bit
   for (int64_t m = 0; m < M; ++m) {
-    // row m as an M = 1 call: the same plan, kernel and reduction order as a lone row
-    const int rc = awq_w4a16_gemm((const char*)a + m * lda * ebytes, lda, qweight, scales, qzeros, bias,
-                                  (char*)c + m * ldc * ebytes, ldc, 1, N, K, group_size, split_k, layout,
-                                  act_dtype, scale_dtype, bias_dtype, workspace, workspace_bytes, stream);
+    const int rc = gemm_impl((const char*)a + m * lda * ebytes, lda, qweight, scales, qzeros, bias,
+                             (char*)c + m * ldc * ebytes, ldc, 1, N, K, group_size, split_k, layout, act_dtype,
+                             scale_dtype, bias_dtype, workspace, workspace_bytes, stream, 1);
     if (rc != AWQ_OK) return rc;
   }
   return AWQ_OK;

@@ -227,7 +227,26 @@ struct GemmArgs {
   const uint16_t* norm_w;
   float eps;
   int norm_bf16;
+  // decode kernels only: > 1 = a row-exact launch (awq_w4a16_gemm_rows_exact) of that many grid
+  // rows, M = 1: grid row y computes row y of the call as a lone M = 1 call would (row_slice)
+  int rows;
 };
+
+// The M = 1 problem of grid row y = blockIdx.y of a row-exact launch: activation row y, output
+// row y and, with split-K, the y-th set of `tiles` arrival counters and `parts` fp32 partial
+// floats.  Row 0 (every other launch) is the call itself.  Every other argument and the whole
+// computation are those of the M = 1 call, so each row's bits equal a lone call's.
+__device__ __forceinline__ GemmArgs row_slice(const GemmArgs& p, int tiles, int parts) {
+  GemmArgs q = p;
+  const int y = (int)blockIdx.y;
+  q.a += (int64_t)y * p.lda;
+  q.c += (int64_t)y * p.ldc;
+  if (p.counters) {  // split-K workspace present
+    q.counters += y * tiles;
+    q.partial += (int64_t)y * parts;
+  }
+  return q;
+}
 
 // Work decomposition of the decode kernel: tiles x ksteps units; each tile's k-steps are cut
 // into `splits` ranges of `per` k-steps (the last ones shorter or empty), one block each

@@ -47,7 +47,7 @@ namespace awq {
 template <int MT, int NWV, int D, int SPG, bool SEQ, bool ZP, typename T, bool SBF, bool STREAM, bool ONE,
           int OCC, bool XL>
 __global__ void __launch_bounds__(NWV * 64) __attribute__((amdgpu_waves_per_eu(OCC, OCC)))
-decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
+decode_kn_kernel(const GemmArgs p_in, const DecodeWork wk) {
   static_assert((SPG & (SPG - 1)) == 0, "");
   static_assert(!XL || (ONE && STREAM), "");
   static_assert(NWV >= 2 && (NWV & (NWV - 1)) == 0, "power-of-two waves per block");
@@ -58,6 +58,8 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
   // subtraction per pair of rows, a single multiply-add per group) are cheaper.
   constexpr bool BIASED = (SPG >= 2 && MT == 1) || (!std::is_same<T, f16>::value && !(MT == 2 && SPG == 1));
   constexpr int MROWS = ONE ? 1 : 16 * MT;  // token rows a wave can hold
+  // grid row y of a row-exact launch: row y's M = 1 problem (the call itself otherwise)
+  const GemmArgs p = row_slice(p_in, wk.tiles, wk.tiles * wk.splits * p_in.M * 128);
   __shared__ float red[NWV * MROWS * 128];  // every wave's sums: [wave][token][tile column]
   __shared__ int s_last;
   extern __shared__ __align__(16) unsigned char xsm[];  // XL: activations k0 * 32 .. k1 * 32 of row 0
@@ -332,7 +334,7 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
   }
 
   const int M = p.M;
-  const int tile_floats = M * 128;  // one partial: [M, 128] fp32
+  const int tile_floats = M * 128;  // one partial: [M, 128] fp32 (M = 1 in a row-exact launch)
   // partial (t, part): [M][128] floats, columns relative to the tile
   const __amdgpu_buffer_rsrc_t prs = make_rsrc(p.partial, (uint32_t)wk.tiles * (uint32_t)S * (uint32_t)tile_floats * 4u);
   const uint32_t tbase = (uint32_t)t * (uint32_t)S * (uint32_t)tile_floats * 4u;
@@ -389,8 +391,13 @@ decode_kn_kernel(const GemmArgs p, const DecodeWork wk) {
   if (S == 1) return;
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed (device scope)
   __syncthreads();                // ... and every thread's
+  // The arrival count is an agent-scope acquire-release: its release orders the block's
+  // partials (every wave's, complete at the barrier above) before the count, and the acquire
+  // of the block that arrives last orders every other block's partials before its reads, by
+  // the memory model rather than by the cache-policy bits alone (which the partial stores and
+  // loads keep, so no line of the partials is served stale from another XCD's L2).
   if (tid == 0)
-    s_last = __hip_atomic_fetch_add(&p.counters[t], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+    s_last = __hip_atomic_fetch_add(&p.counters[t], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
   __syncthreads();
   if (!s_last) return;
   // the last of the S blocks of tile t sums the partials in split (k) order, adds the bias
@@ -467,7 +474,7 @@ template <int MT, bool SEQ, bool ZP, typename T, bool SBF, bool STREAM, bool ONE
 inline void launch_x(const GemmArgs& a, const DecodePlan& s, uint32_t shmem, hipStream_t st) {
   const DecodeWork wk{s.tiles, s.ksteps, s.splits, s.per};
   constexpr int NWV = ONE ? 16 : 8, OCC = ONE ? 4 : 2;
-  const dim3 grid((unsigned)s.blocks), block(NWV * 64);
+  const dim3 grid((unsigned)s.blocks, (unsigned)(a.rows > 1 ? a.rows : 1)), block(NWV * 64);
   const int spg = a.G / 32;
   if (spg == 4)
     hipLaunchKernelGGL((decode_kn_kernel<MT, NWV, 2, 4, SEQ, ZP, T, SBF, STREAM, ONE, OCC, XL>), grid, block, shmem, st, a, wk);

@@ -121,7 +121,7 @@ struct NormRow {
 // NORM (one fp16 row staged by XL, K / 8 <= kNormCols * NWV * 64): the row comes through
 // registers and is staged normalised (RMSNorm prologue) before the first k-step.
 template <int MT, int NWV, int SPG, bool ZP, typename T, bool SBF, bool ONE, bool XL, bool NORM = false>
-__global__ void __launch_bounds__(NWV * 64) decode_narrow_kernel(const GemmArgs p, int tiles) {
+__global__ void __launch_bounds__(NWV * 64) decode_narrow_kernel(const GemmArgs p_in, int tiles) {
   static_assert(!ONE || MT == 1, "");
   static_assert(!XL || MT == 1, "");
   static_assert(!NORM || (XL && ONE && std::is_same<T, f16>::value), "");
@@ -129,6 +129,9 @@ __global__ void __launch_bounds__(NWV * 64) decode_narrow_kernel(const GemmArgs 
   // quads in flight per wave (measured at K = 4096: two, except four for one row in 8-wave blocks)
   constexpr int D = (XL && ONE && NWV == 8) ? 4 : 2;
   constexpr int MROWS = ONE ? 1 : 16 * MT;
+  // grid row y of a row-exact launch: row y's M = 1 problem (the call itself otherwise); the
+  // narrow kernel takes no workspace
+  const GemmArgs p = row_slice(p_in, 0, 0);
   extern __shared__ __align__(16) unsigned char smem[];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -389,7 +392,7 @@ template <int MT, bool ZP, typename T, bool SBF, bool ONE, bool XL, bool NORM = 
 static bool launch_narrow_t(const GemmArgs& a, hipStream_t st) {
   const int tiles = (int)cdiv(a.N, 16);
   const int spg = a.G / 32;
-  const dim3 grid((unsigned)tiles);
+  const dim3 grid((unsigned)tiles, (unsigned)(a.rows > 1 ? a.rows : 1));
   const int nwv = (tiles <= num_cus() && XL) ? 16 : 8;
   const NarrowLds L = narrow_lds(nwv, ONE ? 1 : 16 * MT, a.K / a.G, a.K, ZP, XL ? a.M : 0);
   if (L.total > (tiles <= num_cus() ? kNarrowLdsMaxOne : kNarrowLdsMax)) return false;

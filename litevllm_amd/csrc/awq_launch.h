@@ -48,8 +48,9 @@ bool launch_decode_misc_stream(const awq::GemmArgs& a, const DecodePlan& s, bool
 inline int64_t decode_stream_bytes(int64_t K, int64_t N) { return awq::cdiv(N / 8, 16) * 16 * K * 4; }
 int launch_pack_decode_stream(const int32_t* qweight_kn, int32_t* out, int64_t K, int64_t N, hipStream_t st);
 
-// Narrow decode stream layout (16-column tiles, one u32 per lane and k-step; layout documented
-// in awq_decode_narrow.hip) and its kernel: M <= 32, group sizes 32/64/128, K % 32 == 0.
+// Narrow decode layout (16-column tiles in 1 KiB runs of four 32-row k-steps, 16 bytes per
+// lane; documented in awq_decode_narrow.hip) and its kernel: M <= 32, group sizes 32/64/128,
+// K % 32 == 0.
 int64_t decode_narrow_bytes(int64_t K, int64_t N);
 int launch_pack_decode_narrow(const int32_t* qweight_kn, int32_t* out, int64_t K, int64_t N, hipStream_t st);
 bool launch_decode_narrow(const awq::GemmArgs& a, bool zp, int act, int sdt, hipStream_t st);

@@ -166,10 +166,13 @@ __global__ void __launch_bounds__(128 * NWN, 2) prefill_stream_kernel(const Gemm
       for (int i = 0; i < ACH; ++i) lds_dma16(ars, dst + (uint32_t)(i * 1024), a_voff[i], (uint32_t)(s * BK * 2));
     }
   };
-  // stage s's weight piece, scales and zero word into slot s & 1 (NB loads; stages past the last
-  // one read through an empty descriptor: zeros, no traffic)
+  // stage s's weight piece, scales and zero word into slot s & 1 (NB loads).  The stage's run
+  // offset s * 4096 rides in soffset, which the buffer range check does not cover, so a piece
+  // whose k-step 2 s + pks lies past K (stages past the last one, and the upper half of a last
+  // half stage when K % 64 == 32) reads through an empty descriptor instead: zeros, no traffic.
+  // Its activations are zero, so the zero piece adds nothing.
   auto load_b = [&](int s, int slot) {
-    bq[slot] = asm_load16(s < nst ? wrs : wrs0, w_voff, (uint32_t)s * 4096u);
+    bq[slot] = asm_load16(2 * s + pks < KS ? wrs : wrs0, w_voff, (uint32_t)s * 4096u);
     const int gi = min((s * BK + 8 * kchunk) >> log2g, ngroups - 1);
     bs[slot].s4 = asm_load16(srs, (uint32_t)((gi * p.N + 8 * wld) * 2), 0u);
     if constexpr (ZP) bs[slot].zw = asm_load4(zrs, (uint32_t)((gi * NW + wld) * 4));

@@ -205,8 +205,9 @@ class _Workspace:
 
     A buffer that has been handed out is never freed: when a larger one is needed, the old
     one stays alive (``_retired``), because HIP graphs captured earlier hold its address and
-    write their counters and partials into it on every replay.  ``reserve`` the largest size
-    up front to avoid regrowth altogether."""
+    write their counters and partials into it on every replay.  Sizes are powers of two (at
+    least 16 MiB), so the retired buffers never add up to more than the live one.  ``reserve``
+    the largest size up front to avoid regrowth altogether."""
 
     def __init__(self):
         self._bufs: dict = {}
@@ -220,7 +221,9 @@ class _Workspace:
             if buf is None or buf.numel() < nbytes:
                 if buf is not None:
                     self._retired.append(buf)
-                size = max(nbytes, 16 << 20)
+                # powers of two: the retired buffers of a growing size sum to less than the
+                # live one, however small the steps of growth
+                size = 1 << max(int(nbytes) - 1, (16 << 20) - 1).bit_length()
                 buf = torch.zeros(size, dtype=torch.uint8, device=device)
                 self._bufs[k] = buf
             return buf
@@ -279,17 +282,38 @@ def _use_decode_stream(M, K, N, group_size, layout, decode_stream):
     return eligible
 
 
+def _auto_splits(M: int, N: int, K: int) -> int:
+    """The K partition count the library's planner picks for the 128-column stream kernel when
+    split_k is 0 (``plan_decode``: about 32 k-steps per range, at most one round of blocks on
+    the chip, at most one range per 64-row block)."""
+    tiles = -(-N // 128)
+    fit = max(1, L.num_cus() // tiles)
+    by_k = max(1, (K // 32 + 16) // 32)
+    return max(1, min(-(-K // 64), by_k, fit))
+
+
 def _narrow_fits(M: int, N: int, K: int, split_k: int) -> bool:
-    """Whether the narrow layout (one block per 16 columns over the whole K, no split-K hand-
-    off) serves a decode-shaped call faster than the 128-column stream (measured on MI355X:
-    up to two 16-column tiles per CU while the activation rows fit the kernel's LDS staging,
-    M = 1 .. 4; otherwise, up to M = 16, one tile per CU and K <= 4096)."""
-    if split_k != 0:
+    """Whether a decode-shaped call reads the narrow layout (one block per 16 columns over the
+    whole K, no split-K hand-off) instead of the 128-column stream.
+
+    ``split_k = 0`` ("auto"): where the narrow kernel is faster (measured on MI355X: up to two
+    16-column tiles per CU while the activation rows fit the kernel's LDS staging, M = 1 .. 4;
+    otherwise, up to M = 16, one tile per CU and K <= 4096).
+    ``split_k = 1`` (the whole K per block, the reference's non-split kernel): the same kernel
+    as auto wherever auto does not split K, so a forced 1 and auto give the same bits there;
+    where auto would split, the narrow kernel, whose N / 16 blocks cover the chip that the
+    N / 128 whole-K stream blocks leave mostly idle.
+    ``split_k > 1`` fixes a partition of K, which only the stream kernel takes."""
+    if split_k > 1:
         return False
     tiles = -(-N // 16)
     if M <= 4 and M * K * 2 <= 49152:
-        return tiles <= 2 * L.num_cus()
-    return M <= 16 and tiles <= L.num_cus() and K <= 4096
+        auto = tiles <= 2 * L.num_cus()
+    else:
+        auto = M <= 16 and tiles <= L.num_cus() and K <= 4096
+    if split_k == 0 or auto:
+        return auto
+    return _auto_splits(M, N, K) > 1
 
 
 def _kernel_weight(qweight, scales, qzeros, group_size, layout, M, N, K, split_k, decode_stream, decode_layout):
@@ -362,7 +386,9 @@ def gemm_rows_exact(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor
     """``gemm`` with every row computed exactly as a lone ``M = 1`` call computes it (the same
     weight copy, plan, kernel and reduction order), so ``out[m]`` equals ``gemm(a[m:m+1], ...)``
     bit for bit whatever the batch -- the contract of the reference's row-exact small-batch
-    kernel (``awq_fused_gemm.py:1066-1143``)."""
+    kernel (``awq_fused_gemm.py:1066-1143``).  One launch whose grid has a row of the M = 1
+    call's blocks per input row (group sizes 32 / 64 / 128), as the reference's grid
+    ``(cdiv(N, BN), M)``."""
     lib = L.load()
     if a.dim() != 2:
         raise ValueError("a must be 2-D")
@@ -382,7 +408,7 @@ def gemm_rows_exact(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor
     if bias is not None:
         bias = bias.contiguous()
     dev = a.device
-    ws_bytes = int(lib.awq_w4a16_gemm_workspace_bytes(1, N, K, int(group_size), int(split_k), lc))
+    ws_bytes = int(lib.awq_w4a16_gemm_rows_exact_workspace_bytes(M, N, K, int(group_size), int(split_k), lc))
     ws = WORKSPACE.get(dev, ws_bytes) if ws_bytes else None
     rc = lib.awq_w4a16_gemm_rows_exact(
         _ptr(a), int(a.stride(0)), _ptr(qweight), _ptr(scales), _ptr(qzeros), _ptr(bias), _ptr(out),

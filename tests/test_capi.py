@@ -166,6 +166,29 @@ def test_decode_layout_choice():
     assert not ops._narrow_fits(16, 16 * cus + 16, 4096, 0) and not ops._narrow_fits(17, 4096, 4096, 0)
 
 
+def test_forced_split1_kernel_choice():
+    """split_k = 1 keeps auto's kernel wherever auto does not split K (narrow where auto takes
+    narrow, the whole-K stream plan where auto's plan has one range), and takes the narrow kernel
+    where auto would split: among configs 1 and 2 that is M = 16, N = 6144 and config 2 at
+    M = 8 and 32."""
+    from litevllm_amd import ops
+    if L.num_cus() != 256:
+        pytest.skip("planner figures are for a 256-CU part")
+    shapes = [(m, 4096, n) for m in (1, 4, 16) for n in (4096, 6144, 24576)] + [(m, 12288, 4096) for m in (1, 8, 32)]
+    for M, K, N in shapes:
+        auto_narrow = ops._narrow_fits(M, N, K, 0)
+        auto_whole_k = auto_narrow or ops._auto_splits(M, N, K) == 1
+        forced_narrow = ops._narrow_fits(M, N, K, 1)
+        if auto_whole_k:
+            assert forced_narrow == auto_narrow, (M, K, N)
+        else:
+            assert forced_narrow, (M, K, N)
+    splitting = [(M, K, N) for M, K, N in shapes if not (ops._narrow_fits(M, N, K, 0) or ops._auto_splits(M, N, K) == 1)]
+    assert splitting == [(16, 4096, 6144), (8, 12288, 4096), (32, 12288, 4096)]
+    assert ops._auto_splits(1, 24576, 4096) == 1 and ops._auto_splits(16, 6144, 4096) == 4
+    assert ops._auto_splits(8, 4096, 12288) == 8
+
+
 def _rn_gemm(lib, **kw):
     p = _fake(4096)
     return lib.awq_w4a16_rmsnorm_gemm(

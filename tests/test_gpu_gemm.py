@@ -277,6 +277,30 @@ def test_split_k_uneven_ranges(M, K, sk, stream):
     _check_vs_exact(y1.cpu().numpy(), O.linear_exact(p["x"], _w_used(p, M, G).T), f"split {sk}")
 
 
+CONFIG12 = [(m, 4096, n) for m in (1, 4, 16) for n in (4096, 6144, 24576)] + [(m, 12288, 4096) for m in (1, 8, 32)]
+
+
+@pytest.mark.parametrize("M,K,N", CONFIG12)
+def test_forced_split1_matches_auto(M, K, N):
+    """A forced ``split_k = 1`` (the whole K per block) runs the kernel "auto" runs wherever
+    auto does not split K, so the two are bitwise equal there: every config-1 shape but
+    M = 16, N = 6144, and config 2 at M = 1.  Where auto splits, split 1 takes the narrow
+    kernel (N / 16 whole-K blocks): bit-stable and within 1 ulp of the exact oracle."""
+    ops = _lib()
+    G = 128
+    auto_whole_k = ops._narrow_fits(M, N, K, 0) or ops._auto_splits(M, N, K) == 1
+    _note(f"split 1 vs auto M={M} K={K} N={N} auto_whole_k={auto_whole_k}")
+    p = make_awq_problem(M=M, K=K, N=N, group_size=G, seed=M * 7 + N)
+    t = _to_dev(p)
+    ya = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, split_k=0, layout="autoawq")
+    y1 = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, split_k=1, layout="autoawq")
+    y1b = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, split_k=1, layout="autoawq")
+    assert torch.equal(y1.view(torch.int16), y1b.view(torch.int16)), "split 1 not bit-stable"
+    if auto_whole_k:
+        assert torch.equal(y1.view(torch.int16), ya.view(torch.int16)), "split 1 differs from auto"
+    _check_vs_exact(y1.cpu().numpy(), O.linear_exact(p["x"], _w_used(p, M, G).T), f"split 1 M={M} N={N}")
+
+
 # ------------------------------------------------------------------ benchmark configs
 @pytest.mark.parametrize("M,N", [(m, n) for m in (1, 4, 16) for n in (4096, 6144, 24576)])
 @pytest.mark.parametrize("stream", [None, False])

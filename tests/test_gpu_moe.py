@@ -146,6 +146,9 @@ CASES = [
     # 128 experts, 8 and 12.5 routes each: the stream kernels with one and two route tiles
     (128, 128, 256, 128, 8, 64, True, "silu"),
     (200, 128, 256, 128, 8, 128, True, "silu"),
+    # 128 experts at 32 routes each: the grouped tile kernels, whose tile search passes over
+    # the experts 64 at a time
+    (512, 128, 256, 128, 8, 128, True, "silu"),
 ]
 
 
@@ -374,7 +377,7 @@ def test_config4_full_size_vs_fused_moe_port(T):
     serialized per-token branch at T = 512, fused_moe.py:21, 57-75) on the same routes.
 
     Bar, absolute and in ulps: |y - port| <= 12 fp16 ulps at max(|port|, RMS) and mean relative
-    error <= 1.5e-3.  The port itself sits up to 0.58 absolute (6.3 ulps at the RMS scale, RMS
+    error <= 1e-3, the north star's mean-relative bar.  The port itself sits up to 0.58 absolute (6.3 ulps at the RMS scale, RMS
     42-50) and 7e-4 mean relative from the exact result (float64, measured on the CPU for these
     seeds); the kernel sits within 4 ulps of it (test_config4_full_size).  The north star's 2e-2
     absolute bar is below one fp16 ulp (0.03-0.06) at this output magnitude, so it cannot hold
@@ -396,7 +399,7 @@ def test_config4_full_size_vs_fused_moe_port(T):
     mrel = float(d_.sum() / np.abs(port).sum())
     print(f"config4 T={T} vs port: max abs {d_.max():.4f}, max ulp@max(|y|,rms) {ulps.max():.2f}, "
           f"mean rel {mrel:.2e}, rms {rms:.1f}", flush=True)
-    assert ulps.max() <= 12.0 and mrel <= 1.5e-3
+    assert ulps.max() <= 12.0 and mrel <= 1e-3
 
 
 def test_moe_mfma_path_bf16():
@@ -433,6 +436,38 @@ def test_moe_mfma_path_16bit_routing_weights(wdtype):
     y32 = ops.moe(x, tw16.float().to(DEV), tid.to(DEV), *args)
     torch.cuda.synchronize()
     assert torch.equal(y16.view(torch.int16), y32.view(torch.int16))
+
+
+def test_moe_tile_path_experts_past_64_skewed():
+    """E = 128 on the tile path with the routes skewed onto experts 64 and above: experts 70 and
+    100 take 200 routes each (two full 96-route tiles and a partial one), experts 64 .. 127 the
+    rest, experts 0 .. 63 none, so every row tile belongs to the tile search's second pass of
+    64 experts (full tiles first, then the partial ones)."""
+    T, E, H, I, topk, G = 512, 128, 256, 128, 4, 64
+    assert _mfma_path(T, E, H, I, topk, G)
+    p, d = _problem(T, E, H, I, topk, G, seed=17)
+    g = torch.Generator().manual_seed(17)
+    tid = torch.empty((T, topk), dtype=torch.int64)
+    tid[:, 0] = torch.where(torch.arange(T) < 200, 70, 64 + torch.randint(0, 64, (T,), generator=g))
+    tid[:, 1] = torch.where(torch.arange(T) >= T - 200, 100, 64 + torch.randint(0, 64, (T,), generator=g))
+    tid[:, 2:] = 64 + torch.randint(0, 64, (T, topk - 2), generator=g)
+    # distinct experts per token (a token's routes to one expert would be summed twice anyway,
+    # but keep the reference's top-k shape)
+    for t in range(T):
+        seen = set()
+        for j in range(topk):
+            e = int(tid[t, j])
+            while e in seen:
+                e = 64 + (e - 64 + 1) % 64
+            tid[t, j] = e
+            seen.add(e)
+    tw = torch.rand(T, topk, generator=g)
+    counts = torch.bincount(tid.flatten(), minlength=E)
+    assert int(counts[:64].sum()) == 0 and int(counts[70]) >= 192 and int(counts[100]) >= 192
+    y = ops.moe(_dev(p["x"]), tw.to(DEV), tid.to(DEV), d["gq"], d["gs"], d["gz"], d["dq"], d["ds"], d["dz"], G)
+    w1, w2 = _experts_used(p, d, G, True)
+    exact = O.moe_grouped_exact(p["x"], tw.numpy(), tid.numpy(), w1, w2)
+    _check(y.cpu().numpy(), exact, "E=128 skewed onto experts 64..127")
 
 
 def test_moe_tile_path_fewer_row_tiles_than_experts():

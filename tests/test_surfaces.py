@@ -424,6 +424,34 @@ def test_rows_exact_msmall_matches_independent_m1_bitwise(n, k, dtype):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("M,K,N,G,split_k", [(3, 4096, 4096, 128, 0), (7, 4096, 24576, 128, 0), (4, 12288, 4096, 128, 4),
+                                             (32, 2048, 1536, 64, 0), (5, 1024, 520, 32, 3), (2, 4096, 24576, 128, 2)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_rows_exact_single_launch_zero_point(M, K, N, G, split_k, dtype):
+    """``ops.gemm_rows_exact`` (one launch, grid rows = M) on AutoAWQ tensors with zero points and
+    a bias: row m equals ``ops.gemm`` of row m alone, bit for bit -- on the narrow copy (N = 4096,
+    1536, 520), the stream copy without split (N = 24576) and with forced splits (each grid row
+    has counters and partials of its own), for fp16 and bf16, into a row-strided output."""
+    print(f"rows_exact single launch M={M} K={K} N={N} G={G} split={split_k} {dtype}", flush=True)
+    p = make_awq_problem(M=M, K=K, N=N, group_size=G, seed=M + K + N)
+    t = {k: torch.from_numpy(v).to(DEV) for k, v in p.items() if isinstance(v, np.ndarray)}
+    x = t["x"].to(dtype)
+    sc = t["scales"].to(dtype)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(M)).to(dtype).to(DEV)
+    big = torch.zeros((M, N + 64), dtype=dtype, device=DEV)
+    out = big[:, :N]
+    y = ops.gemm_rows_exact(x, t["qweight"], sc, t["qzeros"], G, bias=bias, split_k=split_k, layout="autoawq", out=out)
+    assert y.data_ptr() == out.data_ptr()
+    rows = torch.cat([ops.gemm(x[m:m + 1], t["qweight"], sc, t["qzeros"], G, bias=bias, split_k=split_k,
+                               layout="autoawq") for m in range(M)])
+    assert torch.equal(out.view(torch.int16), rows.view(torch.int16))
+    assert bool((big[:, N:] == 0).all())
+    # a second call reuses the workspace whose counters the first left at zero
+    y2 = ops.gemm_rows_exact(x, t["qweight"], sc, t["qzeros"], G, bias=bias, split_k=split_k, layout="autoawq")
+    assert torch.equal(y2.view(torch.int16), rows.view(torch.int16))
+
+
+@pytest.mark.gpu
 def test_rows_exact_policy_in_packed_int4_weight():
     """``awq_rows_exact_msmall`` on: PackedInt4Weight.matmul at M = 2 / 4 takes the row-exact
     path (tensor.py:1200-1234) and equals per-row M = 1 calls; off: the generic path."""
