@@ -9,9 +9,16 @@ import torch
 from . import ops
 
 
+def _k_of(qweight: torch.Tensor, layout: str) -> int:
+    """K of a 2-D packed weight: ``[N, K/8]`` in the reference layout, ``[K, N/8]`` otherwise."""
+    return int(qweight.shape[1] * 8) if layout == "ref" else int(qweight.shape[0])
+
+
 def awq_fused_capability_check(input: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
-                               qzeros: torch.Tensor | None, group_size: int) -> tuple[bool, str]:
-    """Same checks and reason strings as ``awq_triton.py:7-35`` (reference layout)."""
+                               qzeros: torch.Tensor | None, group_size: int, *,
+                               layout: str = "ref") -> tuple[bool, str]:
+    """Same checks and reason strings as ``awq_triton.py:7-35`` (``layout="ref"``, the reference
+    layout; ``"autoawq"`` / ``"kn_seq"`` read K from ``qweight``'s first dimension)."""
     if input.device.type == "cpu":
         return False, "cpu_input"
     if qweight.device != input.device:
@@ -26,7 +33,7 @@ def awq_fused_capability_check(input: torch.Tensor, qweight: torch.Tensor, scale
         return False, "qzeros_missing"
     if qzeros.dim() != 2:
         return False, "qzeros_not_2d"
-    k = int(qweight.shape[1] * 8)
+    k = _k_of(qweight, layout)
     if int(input.shape[-1]) != k:
         return False, "k_dim_mismatch"
     if group_size <= 0:
@@ -37,8 +44,9 @@ def awq_fused_capability_check(input: torch.Tensor, qweight: torch.Tensor, scale
 
 
 def packed_int4_fused_capability_check(input: torch.Tensor, qweight: torch.Tensor,
-                                       scales: torch.Tensor, group_size: int) -> tuple[bool, str]:
-    """``awq_triton.py:38-61`` (symmetric mode, no zero tensor)."""
+                                       scales: torch.Tensor, group_size: int, *,
+                                       layout: str = "ref") -> tuple[bool, str]:
+    """``awq_triton.py:38-61`` (symmetric mode, no zero tensor); ``layout`` as above."""
     if input.device.type == "cpu":
         return False, "cpu_input"
     if qweight.device != input.device or scales.device != input.device:
@@ -49,7 +57,7 @@ def packed_int4_fused_capability_check(input: torch.Tensor, qweight: torch.Tenso
         return False, "qweight_not_2d"
     if scales.dim() != 2:
         return False, "scales_not_2d"
-    k = int(qweight.shape[1] * 8)
+    k = _k_of(qweight, layout)
     if int(input.shape[-1]) != k:
         return False, "k_dim_mismatch"
     if group_size <= 0:

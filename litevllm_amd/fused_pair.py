@@ -75,11 +75,15 @@ def try_fused_awq_pair_matmul(x: torch.Tensor, lin_a, lin_b, owner: nn.Module, c
         q_cat = torch.cat([qa, qb], dim=dim).contiguous()
         s_cat = torch.cat([lin_a.scales, lin_b.scales], dim=dim).contiguous()
         prefix = getattr(lin_a, "prefix", "") or f"fused_pair:{cache_key}"
+        hint = str(getattr(lin_a, "awq_profile_hint", "") or "")  # the pair's execution policy
         if zero_point:
             z_cat = torch.cat([za, zb], dim=dim).contiguous()
-            fused = AWQWeight(q_cat, s_cat, z_cat, group_size=gs, prefix=prefix, layout=layout)
+            fused = AWQWeight(q_cat, s_cat, z_cat, group_size=gs, prefix=prefix, profile_hint=hint, layout=layout)
         else:
-            fused = PackedInt4Weight(q_cat, s_cat, group_size=gs, prefix=prefix, layout=layout)
+            shape = getattr(lin_a, "weight_shape", None)
+            shape = (2 * int(shape[0]), int(shape[1])) if shape is not None else None
+            fused = PackedInt4Weight(q_cat, s_cat, group_size=gs, original_shape=shape, prefix=prefix,
+                                     profile_hint=hint, layout=layout)
         setattr(owner, cache_attr, fused)
 
     lead = x.shape[:-1]

@@ -223,3 +223,20 @@ def test_rmsnorm_gemm_workspace_is_host_only(lib):
     assert w16 >= g + 12288 * 2 and wbf >= w16 + 4096 * 2
     # no GEMM workspace (prefill): the counter region is still kept clear
     assert lib.awq_w4a16_rmsnorm_gemm_workspace_bytes(64, 4096, 4096, 128, 0, 0, L.DTYPE_F16) == 65536 + 64 * 4096 * 2
+
+
+def test_workspace_grows_geometrically():
+    """Split-K / MoE workspaces are kept alive once handed out (graphs captured earlier hold their
+    addresses), so they grow in powers of two: requests rising in small steps leave retired
+    buffers that add up to less than the live one."""
+    import torch
+    from litevllm_amd import ops
+    ws = ops._Workspace()
+    dev = torch.device("cpu")
+    for i in range(48):
+        n = (16 << 20) + 1 + i * (3 << 20)
+        buf = ws.get(dev, n)
+        assert buf.numel() >= n and buf.numel() & (buf.numel() - 1) == 0
+    live = ws.get(dev, 1).numel()
+    assert live == 256 << 20 and len(ws._retired) == 4
+    assert sum(int(r.numel()) for r in ws._retired) < live

@@ -16,9 +16,11 @@ def _lin(p, layout="autoawq", dev="cpu", bias=None, zeros=True, **kw):
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
     K = p["qweight"].shape[0]
     N = p["qweight"].shape[1] * 8
+    # a profiled model's MLP pair: the execution policy's fused scope is "all" (tensor.py:437-443)
     return SimpleNamespace(input_size=K, output_size=N, qweight=t(p["qweight"]), scales=t(p["scales"]),
                            qzeros=t(p["qzeros"]) if zeros else None, group_size=p["group_size"],
-                           bias=bias, layout=layout, prefix="", **kw)
+                           bias=bias, layout=layout, prefix="model.layers.0.mlp.gate_proj",
+                           awq_profile_hint="qwen35_9b_awq", **kw)
 
 
 def test_lora_activity_rules():

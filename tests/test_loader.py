@@ -70,7 +70,9 @@ def test_adapted_weight_matmul(fmt, M):
         comps = {"qweight": t(qr), "scales": t(sr)}
     w = loader.make_awq_weight(comps, device=DEV, prepare_decode=True)
     assert w.layout == "autoawq"
-    y = w.matmul(t(p["x"]).to(DEV)).float().cpu().numpy()
+    # no prefix and no profile hint: the reference's default scope (attention_only) would take the
+    # dense path, so ask for the fused one
+    y = w.matmul(t(p["x"]).to(DEV), config={"kernel_policy": {"awq_fused_scope": "all"}}).float().cpu().numpy()
     zp = fmt != "symmetric"
     wd = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"] if zp else None, G,
                        out_dtype="float32" if M <= 32 else "float16", zero_point=zp)

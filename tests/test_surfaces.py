@@ -268,6 +268,7 @@ def test_awqconfig_apply_reference_layout(M, K, N, G, zp):
     layer = torch.nn.Module()
     cfg.init_layer(layer)
     layer.prefix = "model.layers.0.mlp.down_proj"
+    layer.awq_profile_hint = "qwen35_9b_awq"  # a profiled model: fused scope "all" (tensor.py:437-443)
     items = [("model.layers.0.mlp.down_proj.qweight", torch.from_numpy(qr).to(DEV)),
              ("model.layers.0.mlp.down_proj.scales", torch.from_numpy(sr).to(DEV))]
     if zp:
@@ -319,7 +320,7 @@ def test_dense_fallback(mode, monkeypatch):
     p = make_awq_problem(M=M, K=K, N=N, group_size=G, seed=77)
     qr, zr, sr = _ref_layout(p)
     w = TT.AWQWeight(torch.from_numpy(qr).to(DEV), torch.from_numpy(sr).to(DEV), torch.from_numpy(zr).to(DEV), G,
-                     prefix="fb", high_fidelity=(mode == "high_fidelity"))
+                     prefix="fb.self_attn.q_proj", high_fidelity=(mode == "high_fidelity"))
     cfg = None
     if mode == "forced_refusal":
         monkeypatch.setattr(w, "_fused", lambda x2, bias, config: (x2, False, "forced"))
@@ -331,12 +332,15 @@ def test_dense_fallback(mode, monkeypatch):
     y = w.matmul(x, config=cfg)
     y2 = w.matmul(x, config=cfg)
     assert torch.equal(y, y2)
-    ps = TT.get_awq_runtime_prefix_stats()["fb"]
-    assert ps["awq_dense_builds"] == 1 and ps["awq_cache_hits"] == 1
+    ps = TT.get_awq_runtime_prefix_stats()["fb.self_attn.q_proj"]
+    assert ps["dense_build"] == 1 and ps["cache_hit"] == 1 and ps["matmul_calls"] == 2
     if mode == "forced_refusal":
-        assert ps["reason:forced"] == 2 and ps["fused_runtime_fallback"] == 2
+        # the decision stays fused (tensor.py:1034-1086): each call tries and falls back
+        assert ps["decision_fused"] == 1 and ps["reason:forced"] == 2 and ps["fused_runtime_fallback"] == 2
+    elif mode == "policy_off":
+        assert ps["decision_dense"] == 1 and ps["reason:fused_disabled"] == 1 and "fused_attempt" not in ps
     else:
-        assert "awq_fused_attempt" not in ps
+        assert ps["high_fidelity_forced"] == 1 and "fused_attempt" not in ps
     wd = w.dense_weight()
     w16 = O.dequant_ref(qr, sr, zr, G)                              # [N, K] fp16, the oracle's dequant
     assert np.array_equal(wd.cpu().numpy().view(np.uint16), w16.view(np.uint16))
@@ -461,7 +465,7 @@ def test_rows_exact_policy_in_packed_int4_weight():
     qweight = torch.randint(-(2**31), 2**31 - 1, (n, k // 8), dtype=torch.int32, generator=g).to(DEV)
     scales = (torch.rand((n, k // 32), generator=g) * 0.02 + 1e-4).half().to(DEV)
     w = TT.PackedInt4Weight(qweight, scales, 32, prefix="rx")
-    cfg = {"kernel_policy": {"awq_rows_exact_msmall": True}}
+    cfg = {"kernel_policy": {"awq_rows_exact_msmall": True, "awq_fused_scope": "all"}}
     TT.reset_awq_runtime_stats()
     x = torch.randn((4, k), generator=g).half().to(DEV)
     y = w.matmul(x, config=cfg)
