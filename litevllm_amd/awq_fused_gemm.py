@@ -376,7 +376,7 @@ def _concat_qkv(q_qweight, k_qweight, v_qweight, q_scales, k_scales, v_scales):
     return qw.contiguous(), sc.contiguous()
 
 
-_QKV_CACHE = ops._DerivedCache(_concat_qkv)
+_QKV_CACHE = ops._DerivedCache("qkv_concat", _concat_qkv)
 
 
 def _qkv(a, q_qweight, k_qweight, v_qweight, q_scales, k_scales, v_scales, group_size, out):

@@ -6,13 +6,14 @@
   (``gemma4_moe_int4.py:1640-1708``).  Added: optional zero tensors (zero-point AWQ experts),
   group sizes 32 / 64 / 128 (the reference kernels take symmetric g = 32 only) and the
   AutoAWQ expert layout.
-* :func:`fused_moe` mirrors ``vllm/model_executor/layers/fused_moe/fused_moe.py:4-77`` for
-  int4 AWQ experts (:class:`AWQExperts`): routing, the gated expert MLP, the weighted sum.
+* :func:`fused_moe` mirrors ``vllm/model_executor/layers/fused_moe/fused_moe.py:4-77``: int4 AWQ
+  experts (:class:`AWQExperts`) run the grouped kernels (routing, the gated expert MLP, the
+  weighted sum); the ungated form and dense expert tensors take the reference's own expert loop.
 * :func:`moe_route` is the routing alone: ``flow="logits"`` is ``fused_moe.py:12-15``'s dtype flow,
   ``flow="fp32"`` the Gemma4 router's (``gemma4/moe.py:106-123``, weights cast to the hidden
   dtype with ``weights_dtype``).
 
-Every byte of arithmetic runs in ``libawq_w4a16.so``; there is no CPU or eager fallback.
+Every byte of the int4 arithmetic runs in ``libawq_w4a16.so``; there is no CPU fallback.
 """
 from __future__ import annotations
 
@@ -59,7 +60,7 @@ def _ref_builder(qweight, scales, qzeros, n_rows, group_size):
     return ops.repack_experts_ref_to_autoawq(qweight[:, :n_rows], scales[:, :n_rows], qz, group_size)
 
 
-_REF_CACHE = ops._DerivedCache(_ref_builder)
+_REF_CACHE = ops._DerivedCache("moe_ref_autoawq", _ref_builder)
 
 
 def _as_autoawq(ex: AWQExperts, n_rows: int):
@@ -190,24 +191,101 @@ def gemma4_moe_int4_prefill_grouped_fused(x, topk_weights, topk_ids, gate_up_qwe
                                            down_qzeros=down_qzeros, layout=layout)
 
 
-def fused_moe(hidden_states: torch.Tensor, w1: AWQExperts, w2: AWQExperts, gating_output: torch.Tensor,
-              topk: int, renormalize: bool = True) -> torch.Tensor:
-    """``fused_moe`` (``fused_moe.py:4-77``) for int4 AWQ experts: ``w1`` the gate_up stack
-    ``[E, 2I, H]`` (unpacked orientation), ``w2`` the down stack ``[E, H, I]``.
+def _dense_stack(ex: AWQExperts, n_rows: int, dtype: torch.dtype) -> torch.Tensor:
+    """``[E, n_rows, K]`` dense experts in ``dtype``, dequantized by the HIP kernel (one rounding
+    of ``(q - z) * s`` to fp16, bit-exact against the reference's dequant), held on the stack."""
+    return _DENSE_CACHE.get(ex.qweight, ex.scales, ex.qzeros, args=(int(n_rows), ex.group(), ex.layout, dtype))
+
+
+def _dense_build(qweight, scales, qzeros, n, g, layout, dt):
+    outs = []
+    for e in range(int(qweight.shape[0])):
+        w = ops.dequant(qweight[e], scales[e], qzeros[e] if qzeros is not None else None, g, layout=layout)
+        outs.append((w if layout == "ref" else w.t())[:n])
+    return torch.stack(outs).to(dt).contiguous()
+
+
+_DENSE_CACHE = ops._DerivedCache("moe_dense_experts", _dense_build)
+
+
+def _expert_mlp(tokens: torch.Tensor, w1e: torch.Tensor, w2e: torch.Tensor, inter: int) -> torch.Tensor:
+    """One expert on dense weights, the reference's dtype flow (``fused_moe.py:48-54``): the
+    gated form when w1 holds gate and up (``2 * inter`` rows), otherwise SiLU alone."""
+    res = torch.nn.functional.linear(tokens, w1e)
+    if res.shape[-1] == 2 * inter:
+        res = torch.nn.functional.silu(res[:, :inter]) * res[:, inter:]
+    else:
+        res = torch.nn.functional.silu(res)
+    return torch.nn.functional.linear(res, w2e)
+
+
+def _fused_moe_dense(hidden_states, w1, w2, topk_weights, topk_ids):
+    """The reference's expert loop over dense expert tensors (``fused_moe.py:17-75``), both of its
+    branches with their summation orders: routes grouped by expert and ``index_add_`` into the
+    output (E < 256, K <= 4096, M <= 128), else token by token in slot order.  These are dense
+    fp16 / bf16 GEMMs (hipBLASLt through ``F.linear``), outside the int4 W4A16 kernels: the form
+    for callers that hand over materialised experts, kept call-compatible."""
+    M, K = hidden_states.shape
+    E, topk = int(w1.shape[0]), int(topk_ids.shape[1])
+    inter = int(w2.shape[-1])
+    out = torch.zeros_like(hidden_states)
+    if not (E >= 256 or K > 4096 or M > 128):
+        flat_ids = topk_ids.reshape(-1).long()
+        flat_w = topk_weights.reshape(-1)
+        tok = torch.arange(M, device=hidden_states.device).repeat_interleave(topk)
+        sorted_ids, order = torch.sort(flat_ids)
+        tok, flat_w = tok[order], flat_w[order]
+        uniq, counts = torch.unique_consecutive(sorted_ids, return_counts=True)
+        off = 0
+        for e, c in zip(uniq.tolist(), counts.tolist()):
+            idx = tok[off:off + c]
+            res = _expert_mlp(hidden_states.index_select(0, idx), w1[e], w2[e], inter)
+            out.index_add_(0, idx, res * flat_w[off:off + c].unsqueeze(-1))
+            off += c
+        return out
+    for m in range(M):
+        h = hidden_states[m:m + 1]
+        acc = torch.zeros_like(h)
+        for k in range(topk):
+            e = int(topk_ids[m, k].item())
+            acc += _expert_mlp(h, w1[e], w2[e], inter) * topk_weights[m, k].item()
+        out[m] = acc
+    return out
+
+
+def fused_moe(hidden_states: torch.Tensor, w1, w2, gating_output: torch.Tensor, topk: int,
+              renormalize: bool = True) -> torch.Tensor:
+    """``fused_moe`` (``fused_moe.py:4-77``).
 
     Routing follows the reference's dtype flow (``fused_moe.py:12-15``): the softmax rounded to
     the logits dtype, top-k on those values, renormalisation in that dtype, weights in that
-    dtype (:func:`moe_route` with ``flow="logits"``).  Dense fp16 expert tensors are outside the
-    W4A16 path and raise ``TypeError``."""
-    if not isinstance(w1, AWQExperts) or not isinstance(w2, AWQExperts):
-        raise TypeError("fused_moe here takes int4 AWQ expert stacks (AWQExperts) for w1 and w2")
-    _, _, n1 = w1.dims()
-    _, _, n2 = w2.dims()
-    inter = w2.dims()[1]
-    if n1 != 2 * inter:
-        raise ValueError("w1 must hold gate and up (2 * intermediate rows); the ungated form "
-                         "of fused_moe.py:52-53 is not provided")
-    if n2 != int(hidden_states.shape[1]):
-        raise ValueError("w2 rows must equal the hidden size")
+    dtype (:func:`moe_route` with ``flow="logits"``, a HIP kernel).
+      * ``w1``, ``w2`` int4 AWQ expert stacks (:class:`AWQExperts`), ``w1`` the gate_up stack
+        ``[E, 2I, H]`` (unpacked orientation), ``w2`` the down stack ``[E, H, I]``: the grouped
+        W4A16 kernels (gate, up, SiLU, down and the weighted sum, fp32 sums).
+      * ``w1`` an AWQ stack of ``I`` rows (the ungated form, ``fused_moe.py:52-53``): the experts
+        are dequantized once by the HIP kernel (held on the stack) and run in the dense form.
+      * dense ``w1 [E, 2I or I, H]`` / ``w2 [E, H, I]`` tensors (the materialised experts the
+        reference's zero-point Gemma4 path passes, ``gemma4/moe.py:722-750, 788``): the
+        reference's own expert loop on the device (dense GEMMs, not the int4 kernels)."""
+    awq1, awq2 = isinstance(w1, AWQExperts), isinstance(w2, AWQExperts)
+    if awq1 != awq2:
+        raise TypeError("w1 and w2 must both be AWQExperts or both be dense expert tensors")
+    H = int(hidden_states.shape[1])
     tw, tid = moe_route(gating_output, topk, renormalize, flow="logits")
-    return awq_moe(hidden_states, tw, tid, w1, w2, intermediate_dim=inter, activation="silu")
+    if awq1:
+        _, _, n1 = w1.dims()
+        _, inter, n2 = w2.dims()
+        if n2 != H:
+            raise ValueError("w2 rows must equal the hidden size")
+        if n1 == 2 * inter:
+            return awq_moe(hidden_states, tw, tid, w1, w2, intermediate_dim=inter, activation="silu")
+        if n1 != inter:
+            raise ValueError("w1 must hold 2 * intermediate (gated) or intermediate (ungated) rows")
+        w1 = _dense_stack(w1, n1, hidden_states.dtype)
+        w2 = _dense_stack(w2, n2, hidden_states.dtype)
+    if w1.dim() != 3 or w2.dim() != 3 or int(w1.shape[2]) != H or int(w2.shape[1]) != H:
+        raise ValueError("dense experts must be w1 [E, 2I or I, H] and w2 [E, H, I]")
+    if int(w1.shape[1]) not in (int(w2.shape[2]), 2 * int(w2.shape[2])):
+        raise ValueError("w1 rows must be I or 2 * I for w2 [E, H, I]")
+    return _fused_moe_dense(hidden_states, w1, w2, tw.to(hidden_states.dtype), tid)

@@ -8,16 +8,15 @@ Layouts (``layout=`` keyword everywhere):
                    scales [K/G, N], qzeros int32 [K/G, N/8]
   * ``"kn_seq"``   [K, N/8] with sequential nibbles (the reference dequant's row-grouped geometry)
 
-Decode-shaped calls (M <= 32, fp16 activations and scales, group 32/64/128) read a one-time,
-lossless re-ordering of the AutoAWQ qweight (the library's decode stream layout) that the
-decode kernel streams as contiguous 8 KiB runs.  It is built on first use and cached per
-weight tensor, the way the reference caches derived packs on its weight objects
-(``tensor.py:1251-1256``); ``prepare_decode_stream`` builds it ahead of time.
+Calls read a one-time, lossless re-ordering of the packed qweight that their kernel streams
+contiguously (the narrow or the stream decode layout; prefill reads the stream layout).  It is
+built on first use and held by the weight tensor itself, the way the reference holds derived
+packs on its weight objects (``tensor.py:1251-1256``); ``prepare_decode_stream`` builds it ahead
+of time and ``derived_copies`` lists what a weight holds.
 """
 from __future__ import annotations
 
 import threading
-import weakref
 
 import torch
 
@@ -142,16 +141,21 @@ def pack_decode_narrow(qweight: torch.Tensor) -> torch.Tensor:
     return out
 
 
-class _DerivedCache:
-    """Caches tensors derived from a packed weight, keyed by the source tensors' storage
-    pointers, shapes and version counters and checked against a weak reference to the
-    source (the role the reference's derived-pack cache plays at tensor.py:1251-1256)."""
+_DERIVED_ATTR = "_awq_derived"
+_DERIVED_LOCK = threading.Lock()
 
-    def __init__(self, build, capacity: int = 1024):
+
+class _DerivedCache:
+    """Tensors derived from a packed weight (a repack, a kernel-layout copy, a concatenation),
+    held by the source tensor object itself, as the reference holds its derived packs on the
+    weight object (``tensor.py:1251-1256``): they live exactly as long as the weight, and no
+    module-global table grows, evicts or rebuilds them.  An entry is reused while the source
+    and the other inputs are the same storage, shape and version (an in-place update of any of
+    them rebuilds it); one entry per cache and source tensor."""
+
+    def __init__(self, name: str, build):
+        self.name = name
         self.build = build
-        self.capacity = capacity
-        self._d: dict = {}
-        self._lock = threading.Lock()
 
     @staticmethod
     def _key(*tensors):
@@ -160,38 +164,60 @@ class _DerivedCache:
 
     def get(self, src: torch.Tensor, *others, args=()):
         key = (self._key(src, *others), args)
-        with self._lock:
-            hit = self._d.get(key)
-            if hit is not None:
-                ref, val = hit
-                if ref() is src:
-                    return val
+        store = src.__dict__.get(_DERIVED_ATTR)
+        hit = store.get(self.name) if store is not None else None
+        if hit is not None and hit[0] == key:
+            return hit[1]
         val = self.build(src, *others, *args)
-        with self._lock:
-            # drop entries whose source tensor is gone, then the oldest beyond capacity
-            for k in [k for k, (r, _) in self._d.items() if r() is None]:
-                del self._d[k]
-            while len(self._d) >= self.capacity:
-                self._d.pop(next(iter(self._d)))
-            self._d[key] = (weakref.ref(src), val)
+        with _DERIVED_LOCK:
+            store = src.__dict__.setdefault(_DERIVED_ATTR, {})
+            store[self.name] = (key, val)
         return val
 
-    def clear(self):
-        with self._lock:
-            self._d.clear()
+    def held(self, src: torch.Tensor):
+        """The value this cache holds on ``src`` (whatever its key), or None."""
+        hit = (src.__dict__.get(_DERIVED_ATTR) or {}).get(self.name)
+        return None if hit is None else hit[1]
 
 
-def _repack_builder(qweight, scales, qzeros, group_size):
-    return repack_ref_to_autoawq(qweight, scales, qzeros, group_size)
+def derived_copies(src: torch.Tensor) -> dict:
+    """Name -> value of every derived pack a weight tensor holds (for inspection and tests)."""
+    return {k: v[1] for k, v in (src.__dict__.get(_DERIVED_ATTR) or {}).items()}
 
 
-REPACK_CACHE = _DerivedCache(_repack_builder)
-STREAM_CACHE = _DerivedCache(pack_decode_stream)
-NARROW_CACHE = _DerivedCache(pack_decode_narrow)
+def _repack_sz_builder(qweight, scales, qzeros, group_size):
+    """Scales and zeros of a reference-layout weight in the AutoAWQ layout the kernels read
+    (about 4 % of the weight's bytes); the repacked qweight is not kept."""
+    _, sc, qz = repack_ref_to_autoawq(qweight, scales, qzeros, group_size)
+    return sc, qz
+
+
+def _repack_qw_builder(qweight, scales, qzeros, group_size):
+    return repack_ref_to_autoawq(qweight, scales, qzeros, group_size)[0]
+
+
+def _ref_stream_builder(qweight, scales, qzeros, group_size):
+    return pack_decode_stream(repack_ref_to_autoawq(qweight, scales, qzeros, group_size)[0])
+
+
+def _ref_narrow_builder(qweight, scales, qzeros, group_size):
+    return pack_decode_narrow(repack_ref_to_autoawq(qweight, scales, qzeros, group_size)[0])
+
+
+# AutoAWQ-layout weights: the kernel copies are built from the tensor itself
+STREAM_CACHE = _DerivedCache("decode_stream", pack_decode_stream)
+NARROW_CACHE = _DerivedCache("decode_narrow", pack_decode_narrow)
+# reference-layout weights: repacked scales and zeros, and kernel copies built through a
+# transient AutoAWQ repack; the AutoAWQ qweight is kept only for the kernels that read it
+REF_SZ_CACHE = _DerivedCache("ref_scales_zeros", _repack_sz_builder)
+REF_QW_CACHE = _DerivedCache("ref_autoawq_qweight", _repack_qw_builder)
+REF_STREAM_CACHE = _DerivedCache("ref_decode_stream", _ref_stream_builder)
+REF_NARROW_CACHE = _DerivedCache("ref_decode_narrow", _ref_narrow_builder)
 
 
 def prepare_decode_stream(qweight: torch.Tensor) -> torch.Tensor:
-    """Build (and cache) the decode stream copy of an AutoAWQ qweight ahead of the first call."""
+    """Build (and hold on the tensor) the decode stream copy of an AutoAWQ qweight ahead of the
+    first call."""
     return STREAM_CACHE.get(qweight)
 
 
@@ -317,25 +343,36 @@ def _narrow_fits(M: int, N: int, K: int, split_k: int) -> bool:
 
 
 def _kernel_weight(qweight, scales, qzeros, group_size, layout, M, N, K, split_k, decode_stream, decode_layout):
-    """The weight copy and layout code the kernels read for this call: a reference-layout
-    weight is repacked to AutoAWQ once (cached); decode-shaped calls take the cached narrow or
-    stream copy (see ``gemm``)."""
-    if layout == "ref":
-        qweight, scales, qzeros = REPACK_CACHE.get(qweight, scales, qzeros, args=(int(group_size),))
-        layout = "autoawq"
-    qweight, scales = qweight.contiguous(), scales.contiguous()
-    qzeros = qzeros.contiguous() if qzeros is not None else None
-    lc = layout_code(layout)
+    """The weight copy and layout code the kernels read for this call.  Decode-shaped calls
+    take the narrow or stream copy and prefill-sized ones the stream copy (see ``gemm``); both
+    are held by the caller's weight tensor.  A reference-layout weight holds its scales and
+    zeros in the AutoAWQ layout and the kernel copies built through a transient AutoAWQ repack;
+    the repacked qweight itself is kept only when a kernel reads that layout directly
+    (``decode_stream=False``, or a shape the stream layout does not cover)."""
     if decode_layout not in (None, "narrow", "stream"):
         raise ValueError(f"unknown decode_layout {decode_layout!r}")
-    if _use_decode_stream(M, K, N, group_size, layout, decode_stream):
-        if decode_layout == "narrow" and not _decode_shaped(M, group_size):
+    g = int(group_size)
+    ref = layout == "ref"
+    src_qw, src_sc, src_qz = qweight, scales, qzeros
+    if ref:
+        scales, qzeros = REF_SZ_CACHE.get(src_qw, src_sc, src_qz, args=(g,))
+    else:
+        scales = scales.contiguous()
+        qzeros = qzeros.contiguous() if qzeros is not None else None
+    if _use_decode_stream(M, K, N, g, "autoawq" if ref else layout, decode_stream):
+        if decode_layout == "narrow" and not _decode_shaped(M, g):
             raise ValueError("the narrow layout needs M <= 32 and group 32/64/128")
-        narrow = _decode_shaped(M, group_size) and (
+        narrow = _decode_shaped(M, g) and (
             decode_layout == "narrow" or (decode_layout is None and _narrow_fits(M, N, K, int(split_k))))
-        qweight = (NARROW_CACHE if narrow else STREAM_CACHE).get(qweight)
-        lc = L.LAYOUT_DECODE_NARROW if narrow else L.LAYOUT_DECODE_STREAM
-    return qweight, scales, qzeros, lc
+        if ref:
+            cache = REF_NARROW_CACHE if narrow else REF_STREAM_CACHE
+            qweight = cache.get(src_qw, src_sc, src_qz, args=(g,))
+        else:
+            qweight = (NARROW_CACHE if narrow else STREAM_CACHE).get(qweight.contiguous())
+        return qweight, scales, qzeros, (L.LAYOUT_DECODE_NARROW if narrow else L.LAYOUT_DECODE_STREAM)
+    if ref:
+        return REF_QW_CACHE.get(src_qw, src_sc, src_qz, args=(g,)), scales, qzeros, L.LAYOUT_AUTOAWQ
+    return qweight.contiguous(), scales, qzeros, layout_code(layout)
 
 
 def gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, qzeros: torch.Tensor | None,
@@ -525,7 +562,7 @@ def pack_gate_up(gate_qweight, up_qweight, gate_scales, up_scales, gate_qzeros, 
     return qw, sc, qz, (derived(qw) if derived else None)
 
 
-GATE_UP_CACHE = _DerivedCache(pack_gate_up)
+GATE_UP_CACHE = _DerivedCache("gate_up_pair", pack_gate_up)
 
 GATE_UP_ACTIVATIONS = {"silu": L.MOE_ACT_SILU, "gelu": L.MOE_ACT_GELU_TANH,
                        "gelu_pytorch_tanh": L.MOE_ACT_GELU_TANH}
@@ -639,11 +676,11 @@ def pack_moe_stream(qweight: torch.Tensor, gate_up: bool) -> torch.Tensor:
     return out
 
 
-MOE_STREAM_CACHE = _DerivedCache(pack_moe_stream)
+MOE_STREAM_CACHE = _DerivedCache("moe_stream", pack_moe_stream)
 
 
 def prepare_moe_stream(qweight: torch.Tensor, gate_up: bool) -> torch.Tensor:
-    """Build (and cache) the MoE stream copy of an AutoAWQ expert stack."""
+    """Build (and hold on the stack tensor) the MoE stream copy of an AutoAWQ expert stack."""
     return MOE_STREAM_CACHE.get(qweight, args=(bool(gate_up),))
 
 

@@ -483,3 +483,54 @@ def test_moe_tile_path_fewer_row_tiles_than_experts():
     w1, w2 = _experts_used(p, d, G, True)
     exact = O.moe_grouped_exact(p["x"], tw.numpy(), tid.numpy(), w1, w2)
     _check(y.cpu().numpy(), exact, "fewer row tiles than experts")
+
+
+@pytest.mark.parametrize("T", [12, 200])
+@pytest.mark.parametrize("form", ["dense_gated", "dense_ungated", "awq_ungated"])
+def test_fused_moe_dense_and_ungated_forms(T, form):
+    """``fused_moe`` with dense expert tensors (the materialised experts the reference's zero-point
+    Gemma4 path hands over, gemma4/moe.py:722-750, 788) and with an ungated ``w1`` of I rows
+    (fused_moe.py:52-53; an AWQ stack is dequantized by the HIP kernel first): the reference's own
+    expert loop, grouped by expert at T = 12 and token by token at T = 200 (M > 128,
+    fused_moe.py:21), against the port on the same routes.  fp16 sums in a different order (the
+    device's index_add_ is unordered, and the device GEMMs accumulate in their own order): within
+    10 fp16 ulps at max(|y|, RMS), as the kernel-vs-port bar above, and mean relative 1e-3."""
+    E, H, I, topk, G = 8, 256, 128, 2, 64
+    print(f"fused_moe {form} T={T}", flush=True)
+    p, d = _problem(T, E, H, I, topk, G, seed=50 + T)
+    logits = _dev(p["logits"])
+    w1d, w2d = _dense_experts(d, G)
+    x = _dev(p["x"])
+    if form == "dense_gated":
+        w1, w2, w1p = torch.from_numpy(w1d).to(DEV), torch.from_numpy(w2d).to(DEV), w1d
+    elif form == "dense_ungated":
+        w1, w2, w1p = torch.from_numpy(w1d[:, :I]).to(DEV), torch.from_numpy(w2d).to(DEV), w1d[:, :I]
+    else:
+        w1 = MOE.AWQExperts(d["gq"][:, :, : I // 8].contiguous(), d["gs"][:, :, :I].contiguous(),
+                            d["gz"][:, :, : I // 8].contiguous(), G, layout="autoawq")
+        w2 = MOE.AWQExperts(d["dq"], d["ds"], d["dz"], G, layout="autoawq")
+        w1p = w1d[:, :I]
+    y = MOE.fused_moe(x, w1, w2, logits, topk).double().cpu().numpy()
+    tw, tid = ops.moe_route(logits, topk, flow="logits")
+    port = R.fused_moe_cpu(torch.from_numpy(p["x"]), torch.from_numpy(np.ascontiguousarray(w1p)),
+                           torch.from_numpy(w2d), topk_weights=tw.cpu(), topk_ids=tid.cpu().long()).double().numpy()
+    rms = float(np.sqrt(np.mean(port ** 2)))
+    d_ = np.abs(y - port)
+    print(f"  max ulp {(d_ / O.fp16_ulp(port, rms)).max():.2f}, mean rel {d_.sum() / np.abs(port).sum():.2e}", flush=True)
+    assert (d_ / O.fp16_ulp(port, rms)).max() <= 10.0
+    assert d_.sum() / np.abs(port).sum() <= 1e-3
+    if form == "awq_ungated":  # the dequantized stacks are held by the AWQ tensors, not rebuilt
+        held = ops.derived_copies(w1.qweight)
+        assert "moe_dense_experts" in held and tuple(held["moe_dense_experts"].shape) == (E, I, H)
+
+
+def test_fused_moe_rejects_mixed_and_misshaped_experts():
+    E, H, I, topk, G = 4, 128, 64, 2, 32
+    p, d = _problem(4, E, H, I, topk, G, seed=3)
+    w1 = MOE.AWQExperts(d["gq"], d["gs"], d["gz"], G, layout="autoawq")
+    dense = torch.zeros((E, H, I), dtype=torch.float16, device=DEV)
+    with pytest.raises(TypeError):
+        MOE.fused_moe(_dev(p["x"]), w1, dense, _dev(p["logits"]), topk)
+    with pytest.raises(ValueError):
+        MOE.fused_moe(_dev(p["x"]), torch.zeros((E, 3 * I, H), dtype=torch.float16, device=DEV), dense,
+                      _dev(p["logits"]), topk)

@@ -456,6 +456,45 @@ def test_rows_exact_single_launch_zero_point(M, K, N, G, split_k, dtype):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("N,copies", [(24576, {"ref_scales_zeros", "ref_decode_stream"}),
+                                      (4096, {"ref_scales_zeros", "ref_decode_narrow", "ref_decode_stream"})])
+def test_weight_holds_its_derived_copies(N, copies):
+    """A reference-layout ``AWQWeight`` after decode (M = 1) and prefill (M = 64) calls: its
+    qweight parameter holds its derived packs itself -- AutoAWQ scales and zeros, and one kernel
+    copy of the int4 weights per kernel family used (the stream copy serves decode and prefill
+    at N = 24576; at N = 4096 decode reads the narrow copy) -- and never the repacked AutoAWQ
+    qweight.  No module-level table holds any of them; they go with the weight.  Outputs stay
+    within 1 ulp of the exact oracle and equal the raw-tensor surface's."""
+    import gc
+    import weakref
+    from litevllm_amd import tensor as TT
+    print(f"derived copies N={N}", flush=True)
+    K, G = 4096, 128
+    p = make_awq_problem(M=64, K=K, N=N, group_size=G, seed=N)
+    qr, zr, sr = _ref_layout(p)
+    w = TT.AWQWeight(torch.from_numpy(qr).to(DEV), torch.from_numpy(sr).to(DEV), torch.from_numpy(zr).to(DEV), G,
+                     prefix="model.layers.0.self_attn.qkv_proj")
+    x = torch.from_numpy(p["x"]).to(DEV)
+    for m in (1, 64):
+        y = w.matmul(x[:m]).cpu().numpy()
+        wd = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"], G, out_dtype="float32" if m <= 32 else "float16")
+        rep = O.error_report(y, O.linear_exact(p["x"][:m], wd.T))
+        assert rep["max_ulp"] <= 1.0, (m, rep)
+        y2 = AFG.awq_fused_gemm(x[:m], w.qweight, w.scales, w.qzeros, G)
+        assert torch.equal(torch.from_numpy(y), y2.cpu())
+    held = ops.derived_copies(w.qweight)
+    assert set(held) == copies, sorted(held)
+    int4_bytes = K * N // 2
+    kernel_copies = [v for k, v in held.items() if k.startswith("ref_decode")]
+    assert all(v.numel() * v.element_size() <= int4_bytes * 1.01 for v in kernel_copies)
+    assert not any(isinstance(v, dict) and v for c in (ops.STREAM_CACHE, ops.REF_STREAM_CACHE) for v in vars(c).values())
+    ref = weakref.ref(held["ref_decode_stream"])
+    del held, kernel_copies, w
+    gc.collect()
+    assert ref() is None  # the copy went with the weight
+
+
+@pytest.mark.gpu
 def test_rows_exact_policy_in_packed_int4_weight():
     """``awq_rows_exact_msmall`` on: PackedInt4Weight.matmul at M = 2 / 4 takes the row-exact
     path (tensor.py:1200-1234) and equals per-row M = 1 calls; off: the generic path."""
