@@ -463,32 +463,33 @@ class AWQWeight(QuantizedLinearWeight):
     def matmul(self, x, bias=None, *, config: object | None = None):
         """``tensor.py:1008-1122``: the frozen decision (fused, falling back to the dense path
         on a refusal) or, on the first call, high fidelity -> dense, else the execution policy
-        (force, scope, ``awq_fused_gemm``, capability) decides and is frozen."""
+        (force, scope, ``awq_fused_gemm``, capability) decides, is frozen, and the call re-enters
+        (so the first call counts twice in ``matmul_calls``, as in the reference)."""
         _stat("awq_matmul_calls")
         _prefix_stat(self.prefix, "matmul_calls")
         decision = getattr(self, "_cached_fused_decision", None)
-        if decision is None:
-            if _should_use_high_fidelity_awq(self.prefix, self.high_fidelity):
-                self._cached_fused_decision = False
-                _prefix_stat(self.prefix, "high_fidelity_forced")
-                return self._slow_matmul_dequant(x, bias)
-            policy = resolve_awq_execution_policy(self.prefix, x, self.profile_hint, config=config)
-            use_fused, reason = should_use_awq_fused_path(
-                x, self.qweight, self.scales, self.qzeros, self.group_size, self.prefix, policy, config=config,
-                profile_hint=self.profile_hint, layout=self.layout)
-            if use_fused:
-                _prefix_stat(self.prefix, "decision_fused")
-            else:
-                _prefix_stat(self.prefix, "decision_dense")
-                if reason:
-                    _prefix_stat(self.prefix, f"reason:{reason}")
-            self._cached_fused_decision = bool(use_fused)
-            decision = self._cached_fused_decision
-        if decision:
-            out = self._try_fused(x, bias, config)
-            if out is not None:
-                return out
-        return self._slow_matmul_dequant(x, bias)
+        if decision is not None:
+            if decision:
+                out = self._try_fused(x, bias, config)
+                if out is not None:
+                    return out
+            return self._slow_matmul_dequant(x, bias)
+        if _should_use_high_fidelity_awq(self.prefix, self.high_fidelity):
+            self._cached_fused_decision = False
+            _prefix_stat(self.prefix, "high_fidelity_forced")
+            return self._slow_matmul_dequant(x, bias)
+        policy = resolve_awq_execution_policy(self.prefix, x, self.profile_hint, config=config)
+        use_fused, reason = should_use_awq_fused_path(
+            x, self.qweight, self.scales, self.qzeros, self.group_size, self.prefix, policy, config=config,
+            profile_hint=self.profile_hint, layout=self.layout)
+        if use_fused:
+            _prefix_stat(self.prefix, "decision_fused")
+        else:
+            _prefix_stat(self.prefix, "decision_dense")
+            if reason:
+                _prefix_stat(self.prefix, f"reason:{reason}")
+        self._cached_fused_decision = bool(use_fused)
+        return self.matmul(x, bias, config=config)
 
 
 class PackedInt4Weight(AWQWeight):

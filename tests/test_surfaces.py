@@ -285,7 +285,9 @@ def test_awqconfig_apply_reference_layout(M, K, N, G, zp):
     assert layer._quant_weight is first and torch.equal(y, y2)
     assert y.shape == (1, M, N)
     st = get_awq_runtime_stats()
-    assert st["awq_fused_success"] == 2 and st["awq_matmul_calls"] == 2
+    # the first call resolves the policy and re-enters, as the reference's does (tensor.py:1121-1122,
+    # 1443-1447): three counted entries for two calls
+    assert st["awq_fused_success"] == 2 and st["awq_matmul_calls"] == 3
     w = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"] if zp else None, G,
                       out_dtype="float32" if (M <= 32 and G in (32, 64, 128)) else "float16", zero_point=zp)
     ye = O.linear_exact(p["x"], w.T, bias.double().numpy())
@@ -333,7 +335,9 @@ def test_dense_fallback(mode, monkeypatch):
     y2 = w.matmul(x, config=cfg)
     assert torch.equal(y, y2)
     ps = TT.get_awq_runtime_prefix_stats()["fb.self_attn.q_proj"]
-    assert ps["dense_build"] == 1 and ps["cache_hit"] == 1 and ps["matmul_calls"] == 2
+    # the first call re-enters once its decision is made (not for a high-fidelity layer)
+    assert ps["dense_build"] == 1 and ps["cache_hit"] == 1
+    assert ps["matmul_calls"] == (2 if mode == "high_fidelity" else 3)
     if mode == "forced_refusal":
         # the decision stays fused (tensor.py:1034-1086): each call tries and falls back
         assert ps["decision_fused"] == 1 and ps["reason:forced"] == 2 and ps["fused_runtime_fallback"] == 2
