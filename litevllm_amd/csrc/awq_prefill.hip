@@ -242,7 +242,10 @@ __global__ void __launch_bounds__(128 * NWN, 2) prefill_stream_kernel(const Gemm
       }
       write_b(wb, j, bq[wslot], bs[wslot]);
       // issue order within the sub-step: the next sub-step's 6 operand reads spread over the
-      // first 6 MFMAs, the dequant arithmetic in the gaps, its store last
+      // first 6 MFMAs, the dequant arithmetic in the gaps, its store last.  The sub-step runs at
+      // raised wave priority, so the SIMD's other wave does not take issue slots between its
+      // MFMAs (M = 2048, N = 24576: 349.4 -> 345.8 us, A/B on one box)
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                          // MFMA
@@ -251,6 +254,7 @@ __global__ void __launch_bounds__(128 * NWN, 2) prefill_stream_kernel(const Gemm
       }
       __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);                            // LDS write
       __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_setprio(0);
     }
   };
 
