@@ -370,6 +370,34 @@ def _time_rotation(torch, ops, X, pool, Y, reps, fn=None, **kw):
     return ms * 1e3 / (inner * len(pool))
 
 
+def _read_ceiling(torch, dev, nbytes, copies, reps=20):
+    """The HBM read ceiling of one launch that moves ``nbytes``: ``awq_w4a16_probe_read`` (16-byte
+    non-temporal loads, nothing else) over ``copies`` rotated buffers, timed like the decode
+    launches (graph replays of >= 200 launches); the best of five grid shapes."""
+    from litevllm_amd import _lib as L
+    lib = L.load()
+    bufs = [torch.empty(nbytes // 4, dtype=torch.int32, device=dev) for _ in range(copies)]
+    sink = torch.zeros(64, dtype=torch.int32, device=dev)
+    inner = max(1, -(-200 // copies))
+    best = None
+    for blocks, threads, inflight in ((192, 1024, 2), (256, 1024, 4), (512, 512, 4), (1024, 256, 4), (2048, 256, 4)):
+        def run():
+            st = int(torch.cuda.current_stream(dev).cuda_stream)
+            for _ in range(inner):
+                for b in bufs:
+                    L.check("awq_w4a16_probe_read", lib.awq_w4a16_probe_read(
+                        int(b.data_ptr()), nbytes, blocks, threads, inflight, int(sink.data_ptr()), st))
+        ms, g = _time_graph(torch, run, reps)
+        del g
+        us = ms * 1e3 / (inner * copies)
+        if best is None or us < best[0]:
+            best = (us, f"{blocks} x {threads} threads, {inflight} loads in flight per lane")
+    del bufs
+    gbs = nbytes / (best[0] * 1e-6) / 1e9
+    return {"bytes": nbytes, "us": round(best[0], 3), "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "grid": best[1], "copies": copies}
+
+
 def _hbm_entry(us, M, K, N):
     b = alg_bytes(M, K, N)
     gbs = b / (us * 1e-6) / 1e9
@@ -387,7 +415,7 @@ def main():
     ap.add_argument("--no-rmsnorm", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip the configs[0], [2], [3] entries")
     ap.add_argument("--only", default="", help="profile mode: 'decode-m1n24576', 'prefill', 'moe-t16', "
-                    "'moe-t512' or 'copy-64MiB' (counter calibration) launches only")
+                    "'moe-t512', 'pureread' (the read-ceiling probe) or 'copy-64MiB' (counter calibration) launches only")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -424,6 +452,10 @@ def main():
                 tw, tid = ops.moe_route(logits, MOE_TOPK)
                 ops.moe(x, tw, tid, *st, MOE_G)
         torch.cuda.synchronize()
+        return
+    if args.only == "pureread":
+        c = _read_ceiling(torch, dev, alg_bytes(1, K_DEC, 24576) // 16 * 16, rot_copies(K_DEC, 24576), reps=args.steps)
+        print(f"read ceiling: {c}", flush=True)
         return
     if args.only == "copy-64MiB":
         src = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
@@ -489,7 +521,13 @@ def main():
                 "kernel": "decode_kn_kernel (decode stream layout) M=1 K=4096 N=24576",
                 "bytes_per_launch": alg_bytes(1, K_DEC, 24576), "avg_launch_us": r["us"],
                 "rotation_bytes": len(pools[24576]) * weight_bytes(K_DEC, 24576)}
+    ncopies = len(pools[24576])
     del pools, X, Y
+    # what a launch that only reads the same bytes achieves on this part, timed the same way
+    _progress("read ceiling")
+    ceil = _read_ceiling(torch, dev, alg_bytes(1, K_DEC, 24576) // 16 * 16, ncopies)
+    ceil["decode_over_ceiling"] = round(ceil["us"] / r["us"], 4)
+    roofline["read_ceiling"] = ceil
 
     # ---- configs[0], configs[2] (split-K 1/4/8), configs[3] (all four shapes) ----
     _progress("configs 0, 2, 3")

@@ -192,6 +192,15 @@ int awq_w4a16_gemm_rows_exact(const void* a, int64_t lda, const int32_t* qweight
                               int32_t act_dtype, int32_t scale_dtype, int32_t bias_dtype, void* workspace,
                               size_t workspace_bytes, void* stream);
 
+/* Measurement utility with no counterpart in the reference: one launch that only reads `bytes`
+ * of device memory (a multiple of 16, 16-byte aligned) with 16-byte non-temporal loads --
+ * `blocks` blocks of `threads` threads (a multiple of 64, at most 1024), each block a contiguous
+ * share, `in_flight` (2, 4 or 8) loads in flight per lane -- and discards the data (`sink`, 256
+ * bytes of device memory, is never written in practice).  bench.py times it like a decode
+ * launch of the same size to give that launch's HBM read ceiling. */
+int awq_w4a16_probe_read(const void* buf, int64_t bytes, int32_t blocks, int32_t threads, int32_t in_flight,
+                         void* sink, void* stream);
+
 /* Lossless repack of a reference-layout (NK_SEQ) weight into the AUTOAWQ layout:
  *   qweight_nk [N, K/8] -> qweight_kn [K, N/8];  qzeros_nk [N, ceil(K/G/8)] -> qzeros_kn [K/G, N/8]
  *   (qzeros may be NULL);  scales_nk [N, K/G] -> scales_kn [K/G, N] (2-byte elements). */

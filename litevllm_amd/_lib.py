@@ -55,6 +55,7 @@ SIGNATURES = {
                                            _c_p]),
     "awq_w4a16_moe_route_ex": (ctypes.c_int, [_c_p, _c_i64, _c_i32, _c_i64, _c_i32, _c_i32, ctypes.c_uint32,
                                               _c_p, _c_i32, _c_p, _c_p]),
+    "awq_w4a16_probe_read": (ctypes.c_int, [_c_p, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_p]),
     "awq_w4a16_gemm_rows_exact_workspace_bytes": (_c_sz, [_c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32]),
     "awq_w4a16_gemm_rows_exact": (ctypes.c_int, [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i64,
                                                  _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,

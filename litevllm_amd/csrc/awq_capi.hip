@@ -275,6 +275,15 @@ int awq_w4a16_gemm_rows_exact(const void* a, int64_t lda, const int32_t* qweight
   return AWQ_OK;
 }
 
+int awq_w4a16_probe_read(const void* buf, int64_t bytes, int32_t blocks, int32_t threads, int32_t in_flight,
+                         void* sink, void* stream) {
+  if (!buf || !sink) return AWQ_ERR_NULL;
+  if (bytes <= 0 || (bytes % 16) != 0 || (((uintptr_t)buf) & 15)) return AWQ_ERR_SHAPE;
+  if (blocks <= 0 || threads <= 0 || threads > 1024 || (threads % 64) != 0) return AWQ_ERR_SHAPE;
+  if (in_flight != 2 && in_flight != 4 && in_flight != 8) return AWQ_ERR_UNSUPPORTED;
+  return launch_probe_read(buf, bytes, blocks, threads, in_flight, sink, (hipStream_t)stream);
+}
+
 int awq_w4a16_repack_nk_to_autoawq(const int32_t* qweight_nk, const int32_t* qzeros_nk,
                                    const void* scales_nk, int32_t* qweight_kn, int32_t* qzeros_kn,
                                    void* scales_kn, int64_t N, int64_t K, int32_t group_size,

@@ -169,6 +169,28 @@ __global__ void __launch_bounds__(256) gate_up_interleave_kernel(const E* __rest
   out[idx] = sc < cols ? (is_up ? up : gate)[r * cols + sc] : (E)0;
 }
 
+// Roofline probe: block b reads its contiguous share of `n16` 16-byte pieces with non-temporal
+// loads, UNROLL in flight per lane, and discards them.  The store below needs both an
+// impossible fold of the data and n16 == 7, so it never runs for a real probe; it only keeps
+// the loads from being removed.
+template <int UNROLL>
+__global__ void __launch_bounds__(1024) probe_read_kernel(const u32x4* __restrict__ p, uint64_t n16, uint32_t* sink) {
+  const uint64_t per_block = n16 / gridDim.x;
+  const u32x4* base = p + (uint64_t)blockIdx.x * per_block;
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  for (uint64_t i = threadIdx.x; i < per_block; i += (uint64_t)blockDim.x * UNROLL) {
+    u32x4 v[UNROLL];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const uint64_t j = i + (uint64_t)u * blockDim.x;
+      v[u] = j < per_block ? __builtin_nontemporal_load(base + j) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) acc ^= v[u];
+  }
+  if ((acc[0] ^ acc[1] ^ acc[2] ^ acc[3]) == 0x9e3779b9u && n16 == 7) sink[threadIdx.x & 63] = 1u;
+}
+
 }  // namespace awq
 
 namespace awq_host {
@@ -272,6 +294,21 @@ int launch_pack_decode_stream(const int32_t* qweight_kn, int32_t* out, int64_t K
   if (n > 0)
     hipLaunchKernelGGL(pack_stream_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st,
                        (const uint32_t*)qweight_kn, (uint32_t*)out, K, NW, tiles);
+  return launch_status();
+}
+
+int launch_probe_read(const void* buf, int64_t bytes, int blocks, int threads, int in_flight, void* sink,
+                      hipStream_t st) {
+  const uint64_t n16 = (uint64_t)bytes / 16u;
+  if (in_flight == 2)
+    hipLaunchKernelGGL(probe_read_kernel<2>, dim3((unsigned)blocks), dim3((unsigned)threads), 0, st, (const u32x4*)buf,
+                       n16, (uint32_t*)sink);
+  else if (in_flight == 4)
+    hipLaunchKernelGGL(probe_read_kernel<4>, dim3((unsigned)blocks), dim3((unsigned)threads), 0, st, (const u32x4*)buf,
+                       n16, (uint32_t*)sink);
+  else
+    hipLaunchKernelGGL(probe_read_kernel<8>, dim3((unsigned)blocks), dim3((unsigned)threads), 0, st, (const u32x4*)buf,
+                       n16, (uint32_t*)sink);
   return launch_status();
 }
 

@@ -70,6 +70,10 @@ int launch_repack_nk_to_autoawq(const int32_t* qweight_nk, const int32_t* qzeros
                                 void* scales_kn, int64_t N, int64_t K, int32_t group_size,
                                 hipStream_t st);
 
+// Roofline probe: a launch that only reads `bytes` (awq_w4a16_probe_read).
+int launch_probe_read(const void* buf, int64_t bytes, int blocks, int threads, int in_flight, void* sink,
+                      hipStream_t st);
+
 // Gate/up interleave of the gated decode epilogue (elem_bytes 2 or 4).
 int launch_gate_up_interleave(const void* gate, const void* up, void* out, int64_t rows, int64_t cols,
                               int elem_bytes, int64_t half, hipStream_t st);

@@ -240,3 +240,17 @@ def test_workspace_grows_geometrically():
     live = ws.get(dev, 1).numel()
     assert live == 256 << 20 and len(ws._retired) == 3   # 32, 64 and 128 MiB
     assert sum(int(r.numel()) for r in ws._retired) < live
+
+
+def test_probe_read_rejects_bad_args_before_any_launch(lib):
+    """The read-ceiling probe checks its sizes on the host: nothing is launched for these."""
+    p = _fake()
+    f = lib.awq_w4a16_probe_read
+    assert f(None, 64, 1, 64, 2, p, None) == L.ERR_NULL
+    assert f(p, 64, 1, 64, 2, None, None) == L.ERR_NULL
+    assert f(p, 0, 1, 64, 2, p, None) == L.ERR_SHAPE
+    assert f(p, 72, 1, 64, 2, p, None) == L.ERR_SHAPE      # not a multiple of 16
+    assert f(p, 64, 0, 64, 2, p, None) == L.ERR_SHAPE
+    assert f(p, 64, 1, 96, 2, p, None) == L.ERR_SHAPE      # threads not a multiple of 64
+    assert f(p, 64, 1, 2048, 2, p, None) == L.ERR_SHAPE
+    assert f(p, 64, 1, 64, 3, p, None) == L.ERR_UNSUPPORTED
