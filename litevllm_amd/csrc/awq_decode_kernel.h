@@ -165,11 +165,14 @@ decode_kn_kernel(const GemmArgs p_in, const DecodeWork wk) {
           xr[slot][mt] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, (int)x_lane_off[mt], ks * 64, 0));
       // (the 16-wave M == 1 kernel without LDS activations keeps the per-unit loads: holding
       // a slot's constants across turns would not fit its 128 registers)
+      // The constants are read once, like the weights, and take the same non-temporal policy:
+      // with the default policy the M = 1, N = 24576 launch measured 0.2 us longer (11.04 against
+      // 10.83 us, bitwise equal results).
       if (first_turn || (ks & (SPG - 1)) == 0 || (ONE && !XL)) {  // wave-uniform
         const int g = ks / SPG;
         sz[slot].s4 = __builtin_bit_cast(
-            u32x4, __builtin_amdgcn_raw_buffer_load_b128(srs, (int)(16u * wc), (int)((uint32_t)g * (uint32_t)p.N * 2u), 0));
-        sz[slot].zw = ZP ? __builtin_amdgcn_raw_buffer_load_b32(zrs, (int)(4u * wc), (int)((uint32_t)g * (uint32_t)NW * 4u), 0)
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(srs, (int)(16u * wc), (int)((uint32_t)g * (uint32_t)p.N * 2u), kStreamNT));
+        sz[slot].zw = ZP ? __builtin_amdgcn_raw_buffer_load_b32(zrs, (int)(4u * wc), (int)((uint32_t)g * (uint32_t)NW * 4u), kStreamNT)
                          : 0x88888888u;
       }
     };
@@ -391,13 +394,19 @@ decode_kn_kernel(const GemmArgs p_in, const DecodeWork wk) {
   if (S == 1) return;
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed (device scope)
   __syncthreads();                // ... and every thread's
-  // The arrival count is an agent-scope acquire-release: its release orders the block's
-  // partials (every wave's, complete at the barrier above) before the count, and the acquire
-  // of the block that arrives last orders every other block's partials before its reads, by
-  // the memory model rather than by the cache-policy bits alone (which the partial stores and
-  // loads keep, so no line of the partials is served stale from another XCD's L2).
-  if (tid == 0)
-    s_last = __hip_atomic_fetch_add(&p.counters[t], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+  // The arrival count is an agent-scope release: it orders the block's partials (every wave's,
+  // complete at the barrier above) before the count.  The block that arrives last then takes
+  // an agent-scope acquire fence, which orders every other block's partials (their counts are
+  // in the release sequence its increment read from) before its reads -- by the memory model
+  // rather than by the cache-policy bits alone, which the partial stores and loads keep, so no
+  // line of the partials is served stale from another XCD's L2.  On gfx950 the release writes
+  // back this XCD's L2 and the acquire invalidates it; an acquire-release count in every block
+  // cost 0.7 - 1.8 us per launch against relaxed counts, this form 0.3 - 0.6 us (M = 16,
+  // N = 6144: 9.20 relaxed, 10.52 acquire-release, 9.77 this form).
+  if (tid == 0) {
+    s_last = __hip_atomic_fetch_add(&p.counters[t], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+    if (s_last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  }
   __syncthreads();
   if (!s_last) return;
   // the last of the S blocks of tile t sums the partials in split (k) order, adds the bias
