@@ -515,6 +515,9 @@ def main():
         us = _time_rotation(torch, ops, X[m], pools[n], Y[(m, n)], 20)
         per_shape[f"M{m}_N{n}"] = _hbm_entry(us, m, K_DEC, n)
         per_shape[f"M{m}_N{n}"]["copies"] = len(pools[n])
+        # 8-13 MB launches sit near the fixed cost of a launch (first-load latency, block
+        # hand-off, dispatch: about 3.9 us), so their GB/s figure measures latency
+        per_shape[f"M{m}_N{n}"]["bound"] = "hbm" if n >= 16384 else "latency"
     r = per_shape["M1_N24576"]
     roofline = {"bound": "hbm", "achieved": r["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(r["GBps"] / HBM_PEAK_GBS, 4), "traffic": _traffic(),
@@ -572,7 +575,7 @@ def main():
                 us = _time_rotation(torch, ops, x3, W3, y3, 5)
                 tfl = 2.0 * m * n * K_DEC / (us * 1e-6) / 1e12
                 c3[f"M{m}_N{n}"] = {"us": round(us, 1), "TFLOPs": round(tfl, 1),
-                                    "mfma_frac": round(tfl / MFMA_F16_PEAK_TFLOPS, 4)}
+                                    "mfma_frac": round(tfl / MFMA_F16_PEAK_TFLOPS, 4), "weight_copies": 3}
             del W3
         configs["config3"] = c3
 
@@ -587,7 +590,10 @@ def main():
         us = _time_rotation(torch, ops, xp, Wp, yp, 5)
         tflops = 2.0 * M * N * K_DEC / (us * 1e-6) / 1e12
         prefill = {"M": M, "K": K_DEC, "N": N, "us": round(us, 1), "TFLOPs": round(tflops, 1),
-                   "mfma_frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "peak_TFLOPs": MFMA_F16_PEAK_TFLOPS}
+                   "mfma_frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "peak_TFLOPs": MFMA_F16_PEAK_TFLOPS,
+                   # MFMA-bound: three rotated weight copies (151 MB) are enough, the launch
+                   # reads 6.8x its weight bytes from L2 / the MALL either way
+                   "weight_copies": 3}
         del Wp
 
     # ---- grouped MoE (configs[4]: E=64, top-8, H=2048, I=1024, g=128, zero points) ----
