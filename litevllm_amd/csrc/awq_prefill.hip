@@ -9,8 +9,10 @@
 //    positions (low or high half) over 8 k-rows, already paired row by row, so the exact
 //    magic-number dequant, (q - z) * s rounded once, needs no byte permutes, and each nibble
 //    position gives one 16-byte chunk (8 k-values of one column).  That is about 60 VALU
-//    instructions per thread and stage against 32 MFMAs per wave: the dequant of one wave runs
-//    while the other wave of its SIMD keeps the matrix pipe busy.
+//    instructions per thread and stage against 32 MFMAs per wave, and on this part VALU work
+//    overlaps the matrix pipe only in part (its issue time adds to the MFMAs' almost in full),
+//    so it is kept small: with groups of 128 rows or more the column constants (scale, biased
+//    zero) and their loads come once per pair of stages.
 //  * The activation tile goes straight from memory into LDS (buffer loads with the LDS
 //    modifier) one stage ahead; the weight pieces, scales and zeros of stage s + 2 are
 //    requested while stage s computes and wait in registers.
@@ -50,7 +52,7 @@ __device__ __forceinline__ int ps_swz(int r) { return (r ^ (r >> 3)) & 7; }
 
 constexpr int kPSBM = 256, kPSBK = 64;
 
-template <int NWN, bool ZP, typename T, bool FAST>
+template <int NWN, bool ZP, typename T, bool FAST, bool GPAIR>
 __global__ void __launch_bounds__(128 * NWN, 2) prefill_stream_kernel(const GemmArgs p, int scale_bf16, int tiles_m,
                                                                       int tiles_n, int log2g, int n_off) {
   constexpr int NT = 128 * NWN;                // threads
@@ -153,6 +155,11 @@ __global__ void __launch_bounds__(128 * NWN, 2) prefill_stream_kernel(const Gemm
   const u32x4 zrs = {(uint32_t)zbase, (uint32_t)(zbase >> 32) & 0xFFFFu, (uint32_t)((uint64_t)ngroups * NW * 4u),
                      0x00020000u};
   constexpr int NB = ZP ? 3 : 2;  // loads of one stage's weight data
+  // GPAIR (G >= 128): stages 2j and 2j + 1 lie in one group, so an odd stage loads its weight
+  // piece only and reuses the column constants of the even stage before it (M = 2048,
+  // N = 24576: 357.9 -> 350.6 us, bitwise equal, A/B on one box)
+  constexpr int NB_ODD = GPAIR ? 1 : NB;
+  ColConst cc[4];  // the column constants of the stage dequantized last (GPAIR)
 
   auto dma_a = [&](int s, int buf) {
     const uint32_t dst = lds_a0 + (uint32_t)buf * (uint32_t)sizeof(lds_a[0]);
@@ -173,6 +180,7 @@ __global__ void __launch_bounds__(128 * NWN, 2) prefill_stream_kernel(const Gemm
   // Its activations are zero, so the zero piece adds nothing.
   auto load_b = [&](int s, int slot) {
     bq[slot] = asm_load16(2 * s + pks < KS ? wrs : wrs0, w_voff, (uint32_t)s * 4096u);
+    if (GPAIR && slot == 1) return;  // odd stage (slot = stage parity): constants reused
     const int gi = min((s * BK + 8 * kchunk) >> log2g, ngroups - 1);
     bs[slot].s4 = asm_load16(srs, (uint32_t)((gi * p.N + 8 * wld) * 2), 0u);
     if constexpr (ZP) bs[slot].zw = asm_load4(zrs, (uint32_t)((gi * NW + wld) * 4));
@@ -180,7 +188,7 @@ __global__ void __launch_bounds__(128 * NWN, 2) prefill_stream_kernel(const Gemm
   };
   // nibble position P of the piece -> the 16-byte chunk of its column (column 2 P + e of the
   // word: scale half e of scale word P, zero nibble 4 e + P), stored into buffer buf
-  auto write_b = [&](int buf, int P, const u32x4& braw, const WordSZ& bsz) {
+  auto col_const = [&](int P, const WordSZ& bsz) {
     const uint32_t zn = (bsz.zw >> (16 * pe + 4 * P)) & 0xFu;
     const uint32_t sbits = (bsz.s4[P] >> (16 * pe)) & 0xFFFFu;
     ColConst c_;
@@ -192,6 +200,13 @@ __global__ void __launch_bounds__(128 * NWN, 2) prefill_stream_kernel(const Gemm
       c_.sc = 0;
       c_.scf = scale_bf16 ? bf_bits2f((uint16_t)sbits) : h_bits2f((uint16_t)sbits);
     }
+    return c_;
+  };
+  // fresh: the stage starts a group (its constants were loaded with it); otherwise (GPAIR, odd
+  // stages) the previous stage's constants
+  auto write_b = [&](int buf, int P, const u32x4& braw, const WordSZ& bsz, bool fresh) {
+    if (!GPAIR || fresh) cc[P] = col_const(P, bsz);
+    const ColConst c_ = cc[P];
     u32x4 v;
 #define AWQ_PS_CASE(PP)                                                        \
     case PP: {                                                                 \
@@ -234,13 +249,18 @@ __global__ void __launch_bounds__(128 * NWN, 2) prefill_stream_kernel(const Gemm
       if (j == 0) {
         // stage s + 1's weight loads (issued during stage s - 1) must have landed; the DMA and
         // the weight loads issued this stage may stay outstanding
-        if (dma_issued) AWQ_WAIT_VMCNT(ACH + NB);
-        else AWQ_WAIT_VMCNT(NB);
+        if (GPAIR && cb == 1) {  // this step's load_b was an odd stage's (weights only)
+          if (dma_issued) AWQ_WAIT_VMCNT(ACH + NB_ODD);
+          else AWQ_WAIT_VMCNT(NB_ODD);
+        } else {
+          if (dma_issued) AWQ_WAIT_VMCNT(ACH + NB);
+          else AWQ_WAIT_VMCNT(NB);
+        }
         pin_after_wait(bq[wslot]);
         pin_after_wait(bs[wslot].s4);
         pin_after_wait(bs[wslot].zw);
       }
-      write_b(wb, j, bq[wslot], bs[wslot]);
+      write_b(wb, j, bq[wslot], bs[wslot], wslot == 0);
       // issue order within the sub-step: the next sub-step's 6 operand reads spread over the
       // first 6 MFMAs, the dequant arithmetic in the gaps, its store last.  The sub-step runs at
       // raised wave priority, so the SIMD's other wave does not take issue slots between its
@@ -262,12 +282,12 @@ __global__ void __launch_bounds__(128 * NWN, 2) prefill_stream_kernel(const Gemm
   dma_a(0, 0);
   load_b(0, 0);
   load_b(1, 1);
-  AWQ_WAIT_VMCNT(NB);
+  AWQ_WAIT_VMCNT(NB_ODD);
   pin_after_wait(bq[0]);
   pin_after_wait(bs[0].s4);
   pin_after_wait(bs[0].zw);
 #pragma unroll
-  for (int P = 0; P < 4; ++P) write_b(0, P, bq[0], bs[0]);
+  for (int P = 0; P < 4; ++P) write_b(0, P, bq[0], bs[0], true);
   __syncthreads();
 
   // stage s (buffer s & 1): request stage s + 1's activations and stage s + 2's weights (slot
@@ -278,7 +298,8 @@ __global__ void __launch_bounds__(128 * NWN, 2) prefill_stream_kernel(const Gemm
     if (dma) dma_a(s + 1, cb ^ 1);
     load_b(s + 2, cb);
     stage(cb, cb ^ 1, dma);
-    AWQ_WAIT_VMCNT(NB);
+    if (GPAIR && cb == 1) AWQ_WAIT_VMCNT(NB_ODD);
+    else AWQ_WAIT_VMCNT(NB);
     __syncthreads();
   };
   int s = 0;
@@ -342,12 +363,18 @@ static void launch_ps(const GemmArgs& a, int sbf, int log2g, hipStream_t st) {
   const int tm = (int)cdiv(a.M, kPSBM);
   const int tn4 = (int)cdiv(a.N, 256);
   const int cus = num_cus();
+  // groups of 128 rows or more: both stages of a pair share their group
+  const bool gpair = a.G >= 128;
   auto wide = [&](int tiles_n, int n_off) {
-    hipLaunchKernelGGL((prefill_stream_kernel<4, ZP, T, FAST>), dim3(tm * tiles_n), dim3(512), 0, st, a, sbf, tm, tiles_n,
+    if (gpair) hipLaunchKernelGGL((prefill_stream_kernel<4, ZP, T, FAST, true>), dim3(tm * tiles_n), dim3(512), 0, st, a, sbf, tm, tiles_n,
+                       log2g, n_off);
+    else hipLaunchKernelGGL((prefill_stream_kernel<4, ZP, T, FAST, false>), dim3(tm * tiles_n), dim3(512), 0, st, a, sbf, tm, tiles_n,
                        log2g, n_off);
   };
   auto narrow = [&](int tiles_n, int n_off) {
-    hipLaunchKernelGGL((prefill_stream_kernel<2, ZP, T, FAST>), dim3(tm * tiles_n), dim3(256), 0, st, a, sbf, tm, tiles_n,
+    if (gpair) hipLaunchKernelGGL((prefill_stream_kernel<2, ZP, T, FAST, true>), dim3(tm * tiles_n), dim3(256), 0, st, a, sbf, tm, tiles_n,
+                       log2g, n_off);
+    else hipLaunchKernelGGL((prefill_stream_kernel<2, ZP, T, FAST, false>), dim3(tm * tiles_n), dim3(256), 0, st, a, sbf, tm, tiles_n,
                        log2g, n_off);
   };
   // 256-column blocks (two waves per SIMD) once they cover three quarters of the CUs; below
