@@ -132,6 +132,9 @@ SHAPES = [
     (256, 1024, 1024, 128), (300, 2048, 512, 128),
     # group size 32 in the prefill kernel: two groups per 64-row stage, and K % 64 == 32
     (40, 2080, 520, 32), (64, 1024, 1024, 32), (300, 96, 264, 32),
+    # group size 256: four stages per group in the prefill kernel (constants once per pair of
+    # stages), also for M <= 32, which the decode kernels do not take at this group size
+    (8, 1024, 512, 256), (48, 1024, 520, 256), (300, 2048, 264, 256),
 ]
 
 
