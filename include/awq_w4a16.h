@@ -175,8 +175,8 @@ int awq_w4a16_gemm_noalloc(const void* a, int64_t lda, const int32_t* qweight, c
  * 1066-1143, 2925-2998), whose contract is that M = 2 / 4 rows equal independent M = 1 calls
  * (tests/test_awq_fused_gemm_numerics.py:128-161); here for any M, group size and layout the
  * M = 1 call takes.  Arguments and requirements as awq_w4a16_gemm.  With group size 32, 64 or
- * 128 (the decode kernels) it is one launch over a grid of (the M = 1 call's blocks) x M, as the
- * reference's grid (cdiv(N, BN), M) (awq_fused_gemm.py:2980-2981): grid row m runs row m's
+ * 128 (the decode kernels) it is one launch of (the M = 1 call's blocks) x M blocks, as the
+ * reference's grid (cdiv(N, BN), M) (awq_fused_gemm.py:2980-2981): row m's blocks run row m's
  * M = 1 problem, with split-K counters and partials of its own, so the workspace holds M sets
  * of them (awq_w4a16_gemm_rows_exact_workspace_bytes).  Other group sizes take one launch per
  * row, in row order. */

@@ -58,8 +58,9 @@ decode_kn_kernel(const GemmArgs p_in, const DecodeWork wk) {
   // subtraction per pair of rows, a single multiply-add per group) are cheaper.
   constexpr bool BIASED = (SPG >= 2 && MT == 1) || (!std::is_same<T, f16>::value && !(MT == 2 && SPG == 1));
   constexpr int MROWS = ONE ? 1 : 16 * MT;  // token rows a wave can hold
-  // grid row y of a row-exact launch: row y's M = 1 problem (the call itself otherwise)
-  const GemmArgs p = row_slice(p_in, wk.tiles, wk.tiles * wk.splits * p_in.M * 128);
+  // row y of a row-exact launch: row y's M = 1 problem (the call itself otherwise)
+  const BlockXY bxy = decode_block(p_in.rows, wk.tiles * wk.splits);
+  const GemmArgs p = row_slice(p_in, wk.tiles, wk.tiles * wk.splits * p_in.M * 128, bxy.y);
   __shared__ float red[NWV * MROWS * 128];  // every wave's sums: [wave][token][tile column]
   __shared__ int s_last;
   extern __shared__ __align__(16) unsigned char xsm[];  // XL: activations k0 * 32 .. k1 * 32 of row 0
@@ -69,7 +70,7 @@ decode_kn_kernel(const GemmArgs p_in, const DecodeWork wk) {
   const int q = lane >> 4, r = lane & 15;
   const int NW = p.N >> 3;
   const int KS = wk.ksteps, S = wk.splits;
-  const int t = (int)blockIdx.x / S, part = (int)blockIdx.x - t * S;
+  const int t = bxy.x / S, part = bxy.x - t * S;
   // the block's k-step range of tile t, then this wave's contiguous share of it
   const int k0 = min(part * wk.per, KS), k1 = min(k0 + wk.per, KS);
   const int len = k1 - k0;
@@ -483,7 +484,7 @@ template <int MT, bool SEQ, bool ZP, typename T, bool SBF, bool STREAM, bool ONE
 inline void launch_x(const GemmArgs& a, const DecodePlan& s, uint32_t shmem, hipStream_t st) {
   const DecodeWork wk{s.tiles, s.ksteps, s.splits, s.per};
   constexpr int NWV = ONE ? 16 : 8, OCC = ONE ? 4 : 2;
-  const dim3 grid((unsigned)s.blocks, (unsigned)(a.rows > 1 ? a.rows : 1)), block(NWV * 64);
+  const dim3 grid((unsigned)(s.blocks * (a.rows > 1 ? a.rows : 1))), block(NWV * 64);
   const int spg = a.G / 32;
   if (spg == 4)
     hipLaunchKernelGGL((decode_kn_kernel<MT, NWV, 2, 4, SEQ, ZP, T, SBF, STREAM, ONE, OCC, XL>), grid, block, shmem, st, a, wk);

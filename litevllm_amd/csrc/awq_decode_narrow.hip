@@ -131,7 +131,7 @@ __global__ void __launch_bounds__(NWV * 64) decode_narrow_kernel(const GemmArgs 
   constexpr int MROWS = ONE ? 1 : 16 * MT;
   // grid row y of a row-exact launch: row y's M = 1 problem (the call itself otherwise); the
   // narrow kernel takes no workspace
-  const GemmArgs p = row_slice(p_in, 0, 0);
+  const GemmArgs p = row_slice(p_in, 0, 0, (int)blockIdx.y);
   extern __shared__ __align__(16) unsigned char smem[];
 
   const int tid = threadIdx.x, lane = tid & 63;
