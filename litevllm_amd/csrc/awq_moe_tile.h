@@ -113,8 +113,22 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
   const int stl = wave & (kTST - 1), kh = wave / kTST;
   const int q = lane >> 4, r = lane & 15;
 
-  const int cg = blockIdx.x % col_groups;
-  const int t_tile = blockIdx.x / col_groups;  // this block's row tile
+  // this block's column group and row tile: the column groups of one row tile run on one XCD
+  // (the hardware deals blocks to the 8 XCDs round robin; the launch makes the row tiles a
+  // multiple of 8), so they gather the tile's rows into that XCD's L2 once (T = 512: gate_up
+  // 65.2 -> 64.4 us, down 40.0 -> 38.8 us, kernel-trace A/B on one box)
+  int cg, t_tile;
+  {
+    const int b = (int)blockIdx.x, nrt = (int)gridDim.x / col_groups;
+    if ((nrt & 7) == 0) {
+      const int i = b >> 3;
+      cg = i % col_groups;
+      t_tile = (i / col_groups) * 8 + (b & 7);
+    } else {
+      cg = b % col_groups;
+      t_tile = b / col_groups;
+    }
+  }
   const int KS = p.K >> 5;
   const int NW = p.N >> 3;
   const int ngroups = p.K / p.G;
@@ -542,7 +556,9 @@ namespace awq_host {
 template <int MODE, bool ZP, typename T, bool FAST>
 void launch_moe_tile_t(const awq::MoeArgs& a, int E, int sbf, hipStream_t st) {
   const int col_groups = (int)awq::cdiv(a.tiles, awq::kTST);
-  const int64_t tiles_m = awq::cdiv(a.R, awq::kTBM) + E;  // each expert adds at most one partial tile
+  // each expert adds at most one partial tile; rounded up to whole rounds of the 8 XCDs (row
+  // tiles past the last one exit at once)
+  const int64_t tiles_m = (awq::cdiv(a.R, awq::kTBM) + E + 7) / 8 * 8;
   hipLaunchKernelGGL((awq::moe_tile_kernel<MODE, ZP, T, FAST>), dim3((unsigned)(tiles_m * col_groups)),
                      dim3(128 * awq::kTST), 0, st, a, sbf, E, col_groups);
 }
