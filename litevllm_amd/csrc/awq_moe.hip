@@ -208,9 +208,12 @@ __global__ void __launch_bounds__(256) moe_route_kernel(const void* logits, int6
   }
 }
 
-// Expert stack [E][K][NW] (AutoAWQ words) -> [E][tiles][K/32] runs of 2048 bytes; lane
-// l = 16q + r's u32 j (row 32s + 8q + j of word moe_word(t, r)) at byte 1024 (j / 4) + 16 l
-// + 4 (j % 4) of its run -- the decode stream layout, tile words chosen by moe_word.
+// Expert stack [E][K][NW] (AutoAWQ words) -> [E][tiles][K/32] runs of 2048 bytes: the decode
+// stream layout (pack_stream_kernel), tile words chosen by moe_word.  Lane l = 16q + r holds
+// rows 32s + 8q + 2v, 2v + 1 (v = 0..3) of word moe_word(t, r) paired into their low 16-bit
+// halves (u32 v of piece 0, byte 16 l + 4 v of the run) and their high halves (piece 1, byte
+// 1024 + 16 l + 4 v), so the kernels form the MFMA operands without byte permutes (T = 512
+// gate_up 64.8 -> 64.1 us against unpaired rows).
 __global__ void __launch_bounds__(256) moe_pack_stream_kernel(const uint32_t* __restrict__ in,
                                                               uint32_t* __restrict__ out, int64_t K,
                                                               int64_t NW, int64_t tiles, int half,
@@ -227,9 +230,11 @@ __global__ void __launch_bounds__(256) moe_pack_stream_kernel(const uint32_t* __
   const int w = moe_word((int)t, r, half, (int)NW);
   const uint32_t* src = in + e * K * NW;
   uint32_t* dst = out + run * 512;
-  for (int j = 0; j < 8; ++j) {
-    const int64_t row = s * 32 + 8 * q + j;
-    dst[(j >> 2) * 256 + l * 4 + (j & 3)] = w >= 0 ? src[row * NW + w] : 0u;
+  uint32_t rows[8];
+  for (int j = 0; j < 8; ++j) rows[j] = w >= 0 ? src[(s * 32 + 8 * q + j) * NW + w] : 0u;
+  for (int v = 0; v < 4; ++v) {
+    dst[l * 4 + v] = pair_lo(rows[2 * v], rows[2 * v + 1]);        // piece 0
+    dst[256 + l * 4 + v] = pair_hi(rows[2 * v], rows[2 * v + 1]);  // piece 1
   }
 }
 

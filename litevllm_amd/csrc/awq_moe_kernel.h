@@ -276,9 +276,9 @@ moe_gemm_kernel(const MoeArgs p) {
         constexpr bool FRESH = decltype(fresh)::value;
         uint32_t mlo[4], mhi[4];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          mlo[v] = pair_lo(raw[slot][2 * v], raw[slot][2 * v + 1]);
-          mhi[v] = pair_hi(raw[slot][2 * v], raw[slot][2 * v + 1]);
+        for (int v = 0; v < 4; ++v) {  // rows arrive paired (moe_pack_stream_kernel)
+          mlo[v] = raw[slot][v];
+          mhi[v] = raw[slot][4 + v];
         }
 #define AWQ_MOE_NIB(I)                                                                          \
         {                                                                                       \

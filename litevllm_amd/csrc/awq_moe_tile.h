@@ -160,8 +160,9 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
   };
   uint32_t a_voff0 = 0x80000000u, a_voff4 = 0x80000000u;  // set once the route list is in LDS
 
-  // ---- weights: the lane's piece of run (st, k-step): rows 8 q .. 8 q + 3 of word r at byte
-  // 16 lane of the run, rows 8 q + 4 .. 8 q + 7 at 1024 + 16 lane; the DMA puts them at the
+  // ---- weights: the lane's pieces of run (st, k-step): the low halves of rows 8 q .. 8 q + 7
+  // of word r, paired, at byte 16 lane of the run, the high halves at 1024 + 16 lane; the DMA
+  // puts them at the
   // same lane's place in LDS.  Scales (16 bytes: the word's 8 columns) and zeros (the word)
   // of the k-step's group likewise, by lanes 0..15 ----
   const uint32_t stream_bytes = (uint32_t)p.tiles * (uint32_t)KS * 2048u;
@@ -350,16 +351,14 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
 #pragma unroll
       for (int mt = 0; mt < NMT; ++mt) af[mt] = lds16(sb0 + a_rd(ln) + (uint32_t)(mt * 16 * CPR * 16));
       const u32x4 wv0 = lds16(sb0 + w_rd(ln)), wv1 = lds16(sb0 + w_rd(ln) + 1024u);
-      // the word at k-rows 8 q + j (j = 0..7); pair rows (2u, 2u + 1) into lo/hi 16-bit halves
+      // the word at k-rows 8 q .. 8 q + 7, rows (2v, 2v + 1) paired into lo / hi 16-bit halves
+      // by the packer (moe_pack_stream_kernel)
       uint32_t mlo[4], mhi[4];
-      mlo[0] = pair_lo(wv0[0], wv0[1]);
-      mhi[0] = pair_hi(wv0[0], wv0[1]);
-      mlo[1] = pair_lo(wv0[2], wv0[3]);
-      mhi[1] = pair_hi(wv0[2], wv0[3]);
-      mlo[2] = pair_lo(wv1[0], wv1[1]);
-      mhi[2] = pair_hi(wv1[0], wv1[1]);
-      mlo[3] = pair_lo(wv1[2], wv1[3]);
-      mhi[3] = pair_hi(wv1[2], wv1[3]);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        mlo[v] = wv0[v];
+        mhi[v] = wv1[v];
+      }
       // nibble I's operand: from the held constants, or (six tiles) from the raw words, which
       // pass through an opaque copy so that nothing derived from them is held across k-steps
       auto operand = [&](auto i_c) __attribute__((always_inline)) {
