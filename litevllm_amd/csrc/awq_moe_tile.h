@@ -178,12 +178,13 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
   // scales (1), zeros (1)
   constexpr int NB_REST = 2 + 1 + (ZP ? 1 : 0);
 
-  // piece `part` (0..3) of the request for this half's k-step s, into slot s % PD
+  // piece `part` (0..3) of the request for this half's k-step s, into the slot at byte address
+  // `slot` (slot s % PD; the k-loop keeps the slot indices as counters instead of dividing by
+  // PD for every piece: T = 512 gate_up 64.0 -> 63.5 us, down 38.1 -> 37.8 us)
   // (ln: the lane index, passed in so that a caller short of registers can have the lane
   // offsets formed anew each time)
-  auto issue_part = [&](int s, int part, int ln) __attribute__((always_inline)) {
+  auto issue_part = [&](int s, int part, int ln, uint32_t slot) __attribute__((always_inline)) {
     const int ks = s_first + s;
-    const uint32_t slot = lds0 + (uint32_t)(s % PD) * SLOT_BYTES;
     if (part == 0) {
       const uint32_t abase = slot + (uint32_t)(A_OFF + kh * BM * CPR) * 16u;
       lds_dma16(ars, abase + (uint32_t)(stl * 64) * 16u, a_voff0, (uint32_t)(ks * BK * 2));
@@ -206,7 +207,7 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
     for (int s = 0; s < PD - 1; ++s)
       if (s < n_my)
 #pragma unroll
-        for (int part = 1; part < 4; ++part) issue_part(s, part, lane);
+        for (int part = 1; part < 4; ++part) issue_part(s, part, lane, lds0 + (uint32_t)s * SLOT_BYTES);
   };
 
   // ---- the row tile is found from the route counts (one round of loads).  Before that, the
@@ -276,7 +277,7 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
   a_voff0 = a_off(stl);
   if (stl < A_TWO) a_voff4 = a_off(kTST + stl);
   for (int s = 0; s < PD - 1; ++s)
-    if (s < n_my) issue_part(s, 0, lane);
+    if (s < n_my) issue_part(s, 0, lane, lds0 + (uint32_t)s * SLOT_BYTES);
 
   // LDS byte offsets (within a slot) this lane reads
   auto a_rd = [&](int ln) __attribute__((always_inline)) {
@@ -296,8 +297,8 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
   };
   // byte address of k-step s's slot, opaque to the compiler (no per-slot copies of the lane
   // read addresses are kept)
-  auto slot_of = [&](int s) __attribute__((always_inline)) {
-    uint32_t b = lds0 + (uint32_t)(s % PD) * SLOT_BYTES;
+  auto slot_of = [&](int cs) __attribute__((always_inline)) {  // cs: the slot index s % PD
+    uint32_t b = lds0 + (uint32_t)cs * SLOT_BYTES;
     asm volatile("" : "+v"(b));
     return b;
   };
@@ -332,7 +333,7 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
       if constexpr (PACK) asm volatile("" : "+v"(l));
       return l;
     };
-    auto compute = [&](uint32_t sb0, int s, int req) __attribute__((always_inline)) {
+    auto compute = [&](uint32_t sb0, int s, int req, uint32_t rslot) __attribute__((always_inline)) {
       const int ln = lane_now();
       const int g = ((s_first + s) * BK) >> lg;
       if (g != cur_group) {  // wave-uniform
@@ -389,7 +390,7 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
 #define AWQ_RB_REQ(PART)                                                                    \
       if (req >= 0) {                                                                       \
         __builtin_amdgcn_sched_barrier(0);                                                  \
-        issue_part(req, PART, ln);                                                          \
+        issue_part(req, PART, ln, rslot);                                                   \
         __builtin_amdgcn_sched_barrier(0);                                                  \
       }
       AWQ_RB_NIB(0) AWQ_RB_NIB(1) AWQ_RB_REQ(0)
@@ -404,6 +405,7 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
     // scales, zeros) and after it (activations), so their order differs from one request per
     // k-step: all of them (and the route weights' DMA) are waited for here
     AWQ_WAIT_VMCNT0();
+    int cs = 0, rs = PD - 1;  // slot indices of k-step s and of request s + PD - 1
     for (int s = 0; s < n0; ++s) {
       // this k-step's DMAs have landed (the PD - 2 after it may stay in flight)
       if (s < n_my) {
@@ -426,7 +428,9 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
       // every wave's share of the k-step has landed, and slot (s + PD - 1) % PD, read in the
       // previous k-step, is free
       __syncthreads();
-      if (s < n_my) compute(slot_of(s), s, s + PD - 1 < n_my ? s + PD - 1 : -1);
+      if (s < n_my) compute(slot_of(cs), s, s + PD - 1 < n_my ? s + PD - 1 : -1, lds0 + (uint32_t)rs * SLOT_BYTES);
+      cs = cs == PD - 1 ? 0 : cs + 1;
+      rs = rs == PD - 1 ? 0 : rs + 1;
     }
 
     // ---- the K-halves meet.  down (and bf16 gate_up, short of registers for the exchange
