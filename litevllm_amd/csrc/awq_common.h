@@ -198,6 +198,19 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
   return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
 }
 
+// Inclusive prefix sum of an int over the 64 lanes of a wave, with no LDS traffic: shifts
+// right by 1, 2, 4 and 8 lanes inside each row of 16 (lanes whose source lies before the row
+// add zero), then the row broadcasts of lanes 15 and 31.
+__device__ __forceinline__ int wave_incl_scan_i32(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true);   // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true);   // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);   // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true);   // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15 into rows 1 and 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31 into rows 2 and 3
+  return v;
+}
+
 // 1 / sqrt(var / K + eps) of the RMSNorm prologue: var / K + eps in fp32 as the reference
 // computes it (rmsnorm_awq_fused.py:118), the reciprocal square root correctly rounded (fp64
 // square root and division, rounded once to fp32).
