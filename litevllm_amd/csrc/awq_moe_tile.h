@@ -176,8 +176,7 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
   // piece `part` (0..3) of the request for this half's k-step s, into the slot at byte address
   // `slot` (slot s % PD; the k-loop keeps the slot indices as counters instead of dividing by
   // PD for every piece: T = 512 gate_up 64.0 -> 63.5 us, down 38.1 -> 37.8 us)
-  // (ln: the lane index, passed in so that a caller short of registers can have the lane
-  // offsets formed anew each time)
+  // (ln: the lane index)
   auto issue_part = [&](int s, int part, int ln, uint32_t slot) __attribute__((always_inline)) {
     const int ks = s_first + s;
     if (part == 0) {
@@ -299,6 +298,10 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
   };
 
   const MagicK mk = magic_consts_s();
+  // the exponent bytes of a nibble pair's biased zeros (0x6400 | z, 0x5400 | z << 4), in an
+  // SGPR so that one byte permute can merge them with the zero word's byte
+  uint32_t zmag = 0x54006400u;
+  asm volatile("" : "+s"(zmag));
   const bool sb = scale_bf16 != 0;
 
   // the rest specialized on the number of token tiles holding routes (block-uniform)
@@ -311,27 +314,32 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
       for (int mt = 0; mt < NMT; ++mt) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     int cur_group = -1;
-    // the group's per-nibble constants; with six token tiles (192 accumulator registers) only
-    // the raw scale words and zero word are held (five registers) and each nibble's biased zero
-    // is formed where it is used (two instructions; the scale half and both zero halves reach
-    // the packed operations through their operand selects), which keeps the k-loop within the
-    // 256 registers of two waves per SIMD
-    constexpr bool PACK = FAST && NMT >= 6;
+    // the group's constants.  fp16 (FAST): the raw scale words (column c in half c & 1 of word
+    // c >> 1) and the biased zeros of each nibble pair in one register (nibble 2 j in the low
+    // half, 2 j + 1 in the high half); each nibble's packed subtract and multiply read their
+    // halves through operand selects, so no per-nibble constant is formed in the k-loop.  Six
+    // token tiles (192 accumulator registers) hold the zero word instead and form each pair's
+    // zeros before the pair (one byte permute and one AND), which keeps the k-loop within the
+    // 256 registers of two waves per SIMD.  (Against per-nibble broadcast constants, and six
+    // tiles forming each nibble's zero from opaque copies of the zero word and the lane
+    // offsets anew per k-step: T = 512 gate_up 60.2 -> 55.5 us, down 37.8 -> 35.8 us,
+    // kernel-trace A/B on one box, two alternating runs each.)
+    constexpr bool PACK = FAST;
+    constexpr bool ZWORD = PACK && NMT >= 6;
     ColConst cc[8];
     u32x4 s4p = {0u, 0u, 0u, 0u};
+    uint32_t zmp[4] = {0u, 0u, 0u, 0u};
     uint32_t zwp = 0u;
-    // one k-step from the slot at sb0; between nibble pairs, the pieces of request `req`
-    // the lane index as an opaque value per k-step where registers are short (six tiles): the
-    // lane offsets are then formed anew each k-step (a few VALU operations) instead of held
-    auto lane_now = [&]() __attribute__((always_inline)) {
-      int l = lane;
-      if constexpr (PACK) asm volatile("" : "+v"(l));
-      return l;
+    // byte j of the zero word into bytes 0 and 2, the exponent bytes into 1 and 3, masked to
+    // the nibbles: the biased zeros of nibbles 2 j and 2 j + 1
+    auto zero_pair = [&](uint32_t zw, int j) __attribute__((always_inline)) {
+      return __builtin_amdgcn_perm(zmag, zw, 0x07000500u | ((uint32_t)j << 16) | (uint32_t)j) & 0xFFF0FF0Fu;
     };
+    // one k-step from the slot at sb0; between nibble pairs, the pieces of request `req`
     // REQV: the request is known to exist (the main part of the k-loop)
     auto compute = [&](uint32_t sb0, int s, int req, uint32_t rslot, auto reqv) __attribute__((always_inline)) {
       constexpr bool REQV = decltype(reqv)::value;
-      const int ln = lane_now();
+      const int ln = lane;
       const int g = ((s_first + s) * BK) >> lg;
       if (g != cur_group) {  // wave-uniform
         WordSZ sz;
@@ -339,7 +347,10 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
         sz.zw = ZP ? lds4(sb0 + z_rd(ln)) : 0x88888888u;
         if constexpr (PACK) {
           s4p = sz.s4;
-          zwp = sz.zw;
+          if constexpr (ZWORD) zwp = sz.zw;
+          else
+#pragma unroll
+            for (int j = 0; j < 4; ++j) zmp[j] = zero_pair(sz.zw, j);
         } else {
           prep_consts<false, FAST>(sz, sb, cc);
         }
@@ -352,23 +363,21 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
       // the word at k-rows 8 q .. 8 q + 7, rows (2v, 2v + 1) paired into lo / hi 16-bit halves
       // by the packer (moe_pack_stream_kernel)
       uint32_t mlo[4], mhi[4];
+      uint32_t zcur = 0u;  // ZWORD: the current nibble pair's biased zeros
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         mlo[v] = wv0[v];
         mhi[v] = wv1[v];
       }
-      // nibble I's operand: from the held constants, or (six tiles) from the raw words, which
-      // pass through an opaque copy so that nothing derived from them is held across k-steps
+      // nibble I's operand from the group's constants
       auto operand = [&](auto i_c) __attribute__((always_inline)) {
         constexpr int I = decltype(i_c)::value;
         if constexpr (PACK) {
           constexpr int c = nib_col<false>(I);
-          uint32_t zw = zwp, sw = s4p[c >> 1];
-          asm volatile("" : "+v"(zw), "+v"(sw));
-          const uint32_t z = (zw >> (4 * I)) & 0xFu;
-          const f16x2 zh = as_h2((I & 1) ? (0x5400u | (z << 4)) : (0x6400u | z));
-          const f16x2 zb = __builtin_shufflevector(zh, zh, 0, 0);
-          const f16x2 sh = as_h2(sw);
+          if constexpr (ZWORD && (I & 1) == 0) zcur = zero_pair(zwp, I >> 1);
+          const f16x2 zh = as_h2(ZWORD ? zcur : zmp[I >> 1]);
+          const f16x2 zb = (I & 1) ? __builtin_shufflevector(zh, zh, 1, 1) : __builtin_shufflevector(zh, zh, 0, 0);
+          const f16x2 sh = as_h2(s4p[c >> 1]);
           const f16x2 sc = (c & 1) ? __builtin_shufflevector(sh, sh, 1, 1) : __builtin_shufflevector(sh, sh, 0, 0);
           u32x4 b;
 #pragma unroll
