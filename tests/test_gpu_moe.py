@@ -149,6 +149,8 @@ CASES = [
     # 128 experts at 32 routes each: the grouped tile kernels, whose tile search passes over
     # the experts 64 at a time
     (512, 128, 256, 128, 8, 128, True, "silu"),
+    # 4800 routes: the route lists kernel's rounds past the 4096 ids it requests at once
+    (600, 64, 256, 128, 8, 128, True, "silu"),
 ]
 
 
@@ -468,6 +470,22 @@ def test_moe_tile_path_experts_past_64_skewed():
     w1, w2 = _experts_used(p, d, G, True)
     exact = O.moe_grouped_exact(p["x"], tw.numpy(), tid.numpy(), w1, w2)
     _check(y.cpu().numpy(), exact, "E=128 skewed onto experts 64..127")
+
+
+def test_moe_tile_path_out_of_range_ids():
+    # ids outside [0, E) on the tile path (32 routes per expert): the route lists leave them
+    # out and the combine adds nothing for them
+    T, E, H, I, topk, G = 128, 8, 256, 128, 2, 64
+    assert _mfma_path(T, E, H, I, topk, G)
+    p, d = _problem(T, E, H, I, topk, G, seed=19)
+    tw, tid = _route_cpu(torch.from_numpy(p["logits"]), topk)
+    tid = tid.clone()
+    tid[::5, 1] = E + 3
+    tid[2::7, 0] = -1
+    y = ops.moe(_dev(p["x"]), tw.to(DEV), tid.to(DEV), d["gq"], d["gs"], d["gz"], d["dq"], d["ds"], d["dz"], G)
+    w1, w2 = _experts_used(p, d, G, True)
+    exact = O.moe_grouped_exact(p["x"], tw.numpy(), tid.numpy(), w1, w2)
+    _check(y.cpu().numpy(), exact, "tile path, ids outside [0, E)")
 
 
 def test_moe_tile_path_fewer_row_tiles_than_experts():
