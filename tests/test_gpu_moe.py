@@ -151,6 +151,10 @@ CASES = [
     (512, 128, 256, 128, 8, 128, True, "silu"),
     # 4800 routes: the route lists kernel's rounds past the 4096 ids it requests at once
     (600, 64, 256, 128, 8, 128, True, "silu"),
+    # 96 routes per expert (six token tiles: the body that forms each nibble pair's zeros from
+    # the held zero word), symmetric and with groups of 32 rows (a new group every k-step)
+    (192, 4, 256, 128, 2, 128, False, "silu"),
+    (192, 4, 256, 128, 2, 32, True, "gelu_pytorch_tanh"),
 ]
 
 
