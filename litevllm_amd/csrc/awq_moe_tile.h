@@ -100,7 +100,7 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
   __shared__ u32x4 lds_all[PD * SLOT];
   __shared__ int s_rt[BM];
   __shared__ float s_w[BM];
-  __shared__ int s_tile[3];
+  __shared__ int s_tile[4];
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) u32x4*)&lds_all[0];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -142,11 +142,11 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
   // issues DMA stl of its half, and waves stl < 2 also DMA 4 + stl ----
   const u32x4 ars = rsrc_words(p.a, (uint32_t)((uint64_t)p.rows_a * (uint64_t)p.lda * 2u));
   int rows = 0;
-  auto a_off = [&](int i) {
+  auto a_off = [&](int i, int lim) {
     const int row = 16 * i + (lane >> 2);
     const int kc = (lane & 3) ^ ((row >> 1) & 3);
     uint32_t off = 0x80000000u;  // rows past the tile's routes read as zero
-    if (row < rows) {
+    if (row < lim) {
       const int rt = s_rt[row];
       const int src = MODE == 0 ? rt / p.topk : rt;
       off = ((uint32_t)src * (uint32_t)p.lda + (uint32_t)(kc * 8)) * 2u;
@@ -196,37 +196,76 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
       }
     }
   };
-  // the first requests' weights, scales and zeros (they depend on the expert only)
-  auto issue_wsz = [&]() {
-    for (int s = 0; s < PD - 1; ++s)
-      if (s < n_my)
+  // the first requests, one k-step at a time (weights, scales and zeros depend on the expert
+  // only; activations on the route list)
+  auto issue_wsz_s = [&](int s) {
+    if (s < n_my)
 #pragma unroll
-        for (int part = 1; part < 4; ++part) issue_part(s, part, lane, lds0 + (uint32_t)s * SLOT_BYTES);
+      for (int part = 1; part < 4; ++part) issue_part(s, part, lane, lds0 + (uint32_t)s * SLOT_BYTES);
+  };
+  auto issue_a_s = [&](int s) {
+    if (s < n_my) issue_part(s, 0, lane, lds0 + (uint32_t)s * SLOT_BYTES);
   };
 
   // ---- the row tile is found from the route counts (one round of loads).  Before that, the
   // block bets on the usual prefill case, every expert with 1 .. BM - 1 routes: row tile t is
-  // then expert t's only tile, its routes from 0.  The bet's weights, scales and zeros and
-  // its first BM list entries are requested at once; a lost bet waits for them and asks
-  // again, so the bet changes only when the data arrive ----
+  // then expert t's only tile, its routes from 0, min(count, BM) of them.  The counts, the bet
+  // expert's count and first BM list entries (to LDS by DMA) and k-step 0's weights, scales and
+  // zeros go out first; once the list has landed, k-step 0's activation rows, then k-steps
+  // 1 .. PD - 2 whole, one after another.  So every block's first k-step is at the head of the
+  // memory queues (the first requests of all blocks are a 31 MB burst; requested weights-first
+  // for all four k-steps, k-step 0's activations came last; T = 512 A/Bs on two boxes: down
+  // 36.2 -> 34.8 and 35.8 -> 35.1 us, gate_up 56.1 -> 55.2 and 55.9 -> 56.0 us), and the
+  // k-loop's own waits (PD - 2 k-steps in flight) cover the
+  // first k-step.  A lost bet waits for all of them and asks again, so the bet changes only
+  // when the data arrive ----
   const bool bet = t_tile < E;  // block-uniform
-  // wave 0 requests the counts of experts 0..63 ahead of its bet (an assembly load, waited for
-  // below by count: the bet's DMAs after it stay in flight)
-  uint32_t cnt0 = 0;
+  // fp32 route weights (read by the epilogue only) go to LDS by DMA, with k-step 0's requests
+  const bool rw_dma = MODE == 0 && p.rw_dtype == AWQ_DTYPE_F32;
+  auto route_weight_dma = [&](int rt) {
+    const uint32_t sw_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)&s_w[0];
+    lds_dma4(rsrc_words(p.rw, (uint32_t)p.R * 4u), sw_lds + (uint32_t)wave * 256u, (uint32_t)rt * 4u, 0u);
+  };
+  // wave 0: the counts of experts 0..63 and the bet expert's count (assembly loads, waited for
+  // below by count: the DMAs after them stay in flight)
+  uint32_t cnt0 = 0, cnt_bet = 0;
   if (wave == 0) {
     const u32x4 crs = rsrc_words(p.counts, (uint32_t)E * 4u);  // lanes past E read zero
     asm volatile("buffer_load_dword %0, %1, %2, %3 offen" : "=v"(cnt0) : "v"((uint32_t)lane * 4u), "s"(crs), "s"(0u) : "memory");
+    if (bet)
+      asm volatile("buffer_load_dword %0, %1, %2, %3 offen" : "=v"(cnt_bet) : "v"((uint32_t)t_tile * 4u), "s"(crs), "s"(0u) : "memory");
   }
   int e_cur = bet ? t_tile : 0;
+  if (bet && tid < BM) {  // waves 0 and 1: list entries 0 .. BM - 1 of expert e_cur into s_rt
+    const uint32_t rt_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int*)&s_rt[0];
+    lds_dma4(rsrc_words(p.lists + (int64_t)e_cur * p.R, (uint32_t)p.R * 4u), rt_lds + (uint32_t)wave * 256u,
+             (uint32_t)tid * 4u, 0u);
+  }
   set_expert(e_cur);
-  if (bet) issue_wsz();
-  int rt_bet = 0;
-  if (bet && tid < BM && tid < p.R) rt_bet = p.lists[(int64_t)e_cur * p.R + tid];
+  if (bet) {
+    issue_wsz_s(0);
+    // the list (and wave 0's counts) landed: k-step 0's NB_REST DMAs were issued after them
+    if (wave < 2) {
+      if (n_my >= 1) AWQ_WAIT_VMCNT(NB_REST);
+      else AWQ_WAIT_VMCNT0();
+    }
+    if (wave == 0) {
+      pin_after_wait(cnt_bet);
+      if (lane == 0) s_tile[3] = min((int)cnt_bet, BM);
+    }
+    __syncthreads();
+    const int lim = s_tile[3];  // the bet's routes (a won bet's tile has exactly these)
+    a_voff0 = a_off(stl, lim);
+    if (stl < A_TWO) a_voff4 = a_off(kTST + stl, lim);
+    issue_a_s(0);
+    if (rw_dma && tid < lim) route_weight_dma(s_rt[tid]);
+    for (int s = 1; s < PD - 1; ++s) {
+      issue_wsz_s(s);
+      issue_a_s(s);
+    }
+  }
   if (wave == 0) {
-    // issued after the counts: the bet's NB_REST DMAs for each of its first PD - 1 k-steps (and
-    // the list load, not counted: a smaller count only waits longer)
-    if (bet && n_my >= PD - 1) AWQ_WAIT_VMCNT((PD - 1) * NB_REST);
-    else AWQ_WAIT_VMCNT0();
+    if (!bet) AWQ_WAIT_VMCNT0();
     pin_after_wait(cnt0);
     int te, tm0, trows;
     moe_row_tile_wave(p.counts, E, t_tile, te, tm0, trows, true, (int)cnt0);
@@ -246,32 +285,29 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
   }
   const int n_mt = (rows + 15) >> 4;  // token tiles holding routes (block-uniform)
   const bool won = bet && e == e_cur && m0 == 0;  // block-uniform
-  if (!won) {
-    AWQ_WAIT_VMCNT0();  // the bet's DMAs have landed before their slots are requested again
+  if (won) {
+    // s_rt holds the tile's routes and the first requests cover them; 16-bit route weights by
+    // plain loads
+    if (MODE == 0 && !rw_dma && tid < rows) s_w[tid] = load_route_weight(p.rw, p.rw_dtype, s_rt[tid]);
+  } else {
+    AWQ_WAIT_VMCNT0();  // this wave's bet DMAs (its slot, s_rt and s_w parts) have landed
     e_cur = e;
     set_expert(e);
-    issue_wsz();
-  }
-  {
-    const int* list = p.lists + (int64_t)e * p.R;
     int rt = 0;
     if (tid < rows) {
-      rt = won ? rt_bet : list[m0 + tid];
+      rt = p.lists[(int64_t)e * p.R + m0 + tid];
       s_rt[tid] = rt;
-      if (MODE == 0 && p.rw_dtype != AWQ_DTYPE_F32) s_w[tid] = load_route_weight(p.rw, p.rw_dtype, rt);
+      if (MODE == 0 && !rw_dma) s_w[tid] = load_route_weight(p.rw, p.rw_dtype, rt);
     }
     __syncthreads();
-    // fp32 route weights (read by the epilogue only) go to LDS by DMA, waited for with the
-    // first k-step's data
-    if (MODE == 0 && p.rw_dtype == AWQ_DTYPE_F32 && tid < rows) {
-      const uint32_t sw_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)&s_w[0];
-      lds_dma4(rsrc_words(p.rw, (uint32_t)p.R * 4u), sw_lds + (uint32_t)wave * 256u, (uint32_t)rt * 4u, 0u);
+    a_voff0 = a_off(stl, rows);
+    if (stl < A_TWO) a_voff4 = a_off(kTST + stl, rows);
+    for (int s = 0; s < PD - 1; ++s) {
+      issue_wsz_s(s);
+      issue_a_s(s);
+      if (s == 0 && rw_dma && tid < rows) route_weight_dma(rt);
     }
   }
-  a_voff0 = a_off(stl);
-  if (stl < A_TWO) a_voff4 = a_off(kTST + stl);
-  for (int s = 0; s < PD - 1; ++s)
-    if (s < n_my) issue_part(s, 0, lane, lds0 + (uint32_t)s * SLOT_BYTES);
 
   // LDS byte offsets (within a slot) this lane reads
   auto a_rd = [&](int ln) __attribute__((always_inline)) {
@@ -407,10 +443,9 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
 #undef AWQ_RB_NIB
     };
 
-    // the requests for this half's k-steps 0 .. PD - 2 went out before the route list (weights,
-    // scales, zeros) and after it (activations), so their order differs from one request per
-    // k-step: all of them (and the route weights' DMA) are waited for here
-    AWQ_WAIT_VMCNT0();
+    // the requests for this half's k-steps 0 .. PD - 2 went out one k-step after another (with
+    // the route list, counts and route weights before k-step 1's): the k-loop's waits below
+    // cover them
     int cs = 0, rs = PD - 1;  // slot indices of k-step s and of request s + PD - 1
     int s = 0;
     // main part: k-steps whose request s + PD - 1 exists in both halves (n_my >= n0 - 1) and
