@@ -549,6 +549,13 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
     // 8 word + nib_col(I) ----
     auto epilogue = [&](auto kind_c) __attribute__((always_inline)) {
       constexpr int KIND = decltype(kind_c)::value;
+      // the lane's first output column as a byte address and the row stride in bytes, so that a
+      // row's address is one 32 x 32 -> 64-bit multiply-add of its route index (route indices
+      // and row strides are below 2^32)
+      constexpr uint32_t EB = MODE == 0 ? 2u : 4u;  // bytes per output value
+      const int ocol = MODE == 0 ? (r < 8 ? 8 * word : 8 * (word - p.half) + 4) : 8 * word;
+      const uint64_t obase = (uint64_t)(uintptr_t)p.out + (uint64_t)(int64_t)ocol * EB;
+      const uint32_t ostride = (uint32_t)p.ldo * EB;
 #pragma unroll
       for (int mt = 0; mt < NMT; ++mt) {
         if (kh == 0 ? mt >= H0 : mt < H0) continue;  // the partner's tile (wave-uniform)
@@ -576,8 +583,7 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
               float h[4];
 #pragma unroll
               for (int j = 0; j < 4; ++j) h[j] = gated_act_fast<KIND>(gt[j]) * ut[j] * wgt;
-              const int col = r < 8 ? 8 * word : 8 * (word - p.half) + 4;
-              *(u32x2*)((uint16_t*)p.out + (int64_t)rt * p.ldo + col) = u32x2{pack2<T>(h[0], h[1]), pack2<T>(h[2], h[3])};
+              *(u32x2*)(uintptr_t)(obase + (uint64_t)(uint32_t)rt * ostride) = u32x2{pack2<T>(h[0], h[1]), pack2<T>(h[2], h[3])};
             }
           } else {
             if (m < rows && word >= 0) {
@@ -585,7 +591,7 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
               float y[8];
 #pragma unroll
               for (int I = 0; I < 8; ++I) y[nib_col<false>(I)] = acc[I][mt][v];
-              float* dst = (float*)p.out + (int64_t)rt * p.ldo + 8 * word;
+              float* dst = (float*)(uintptr_t)(obase + (uint64_t)(uint32_t)rt * ostride);
               *(f32x4*)dst = f32x4{y[0], y[1], y[2], y[3]};
               *(f32x4*)(dst + 4) = f32x4{y[4], y[5], y[6], y[7]};
             }
