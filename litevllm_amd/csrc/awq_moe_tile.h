@@ -550,8 +550,8 @@ __global__ void __launch_bounds__(128 * kTST) moe_tile_kernel(const MoeArgs p, i
     auto epilogue = [&](auto kind_c) __attribute__((always_inline)) {
       constexpr int KIND = decltype(kind_c)::value;
       // the lane's first output column as a byte address and the row stride in bytes, so that a
-      // row's address is one 32 x 32 -> 64-bit multiply-add of its route index (route indices
-      // and row strides are below 2^32)
+      // row's address is one 32 x 32 -> 64-bit multiply-add of its route index (the host keeps
+      // every per-route buffer, and so every route index and row stride, below 2^31 bytes)
       constexpr uint32_t EB = MODE == 0 ? 2u : 4u;  // bytes per output value
       const int ocol = MODE == 0 ? (r < 8 ? 8 * word : 8 * (word - p.half) + 4) : 8 * word;
       const uint64_t obase = (uint64_t)(uintptr_t)p.out + (uint64_t)(int64_t)ocol * EB;
