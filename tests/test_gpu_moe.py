@@ -173,6 +173,29 @@ def test_moe_vs_exact_oracle(T, E, H, I, topk, G, zp, act):
     _check(y.cpu().numpy(), exact, f"T={T} E={E} H={H} I={I} k={topk} G={G} zp={zp} {act}")
 
 
+@pytest.mark.parametrize("T", [24, 512])
+def test_moe_strided_rows(T):
+    """Activation and output rows at strides past H (x and out as column slices of wider
+    buffers), through the stream kernels (T = 24, 6 routes per expert) and the tile kernels
+    (T = 512, 128 per expert): the same bits as contiguous rows, and nothing written past H."""
+    E, H, I, topk, G = 16, 256, 128, 4, 64
+    assert _mfma_path(T, E, H, I, topk) == (T == 512)
+    p, d = _problem(T, E, H, I, topk, G, True, seed=T + 7)
+    tw, tid = _route_cpu(torch.from_numpy(p["logits"]), topk)
+    tw, tid = tw.to(DEV), tid.to(DEV)
+    x = _dev(p["x"])
+    args = (d["gq"], d["gs"], d["gz"], d["dq"], d["ds"], d["dz"], G)
+    y = ops.moe(x, tw, tid, *args)
+    xb = torch.zeros((T, H + 64), dtype=x.dtype, device=DEV)
+    xb[:, :H] = x
+    ob = torch.full((T, H + 32), 7.0, dtype=x.dtype, device=DEV)
+    ys = ops.moe(xb[:, :H], tw, tid, *args, out=ob[:, :H])
+    torch.cuda.synchronize()
+    assert ys.data_ptr() == ob.data_ptr()
+    assert torch.equal(ys, y)
+    assert bool((ob[:, H:] == 7.0).all())
+
+
 def test_moe_skewed_routing_multiple_passes():
     # every route on two experts: 600 rows per expert -> several wave-group passes
     T, E, H, I, topk, G = 600, 8, 256, 128, 2, 128
