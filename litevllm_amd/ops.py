@@ -397,7 +397,12 @@ def gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, qzeros: t
         raise ValueError(f"K mismatch: a has {a.shape[1]}, weight has {K}")
     qweight, scales, qzeros, lc = _kernel_weight(qweight, scales, qzeros, group_size, layout, M, N, K,
                                                  split_k, decode_stream, decode_layout)
-    a = a.contiguous()
+    # rows at any stride the kernels take (16-byte aligned, a multiple of 8 elements) are read in
+    # place, as the reference's kernel takes stride_am; anything else is made contiguous
+    lda = int(a.stride(0)) if M > 1 else K
+    if a.stride(1) != 1 or lda < K or lda % 8 != 0 or a.data_ptr() % 16 != 0:
+        a = a.contiguous()
+        lda = K
     if out is None:
         out = torch.empty((M, N), dtype=a.dtype, device=a.device)
     else:
@@ -409,7 +414,7 @@ def gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, qzeros: t
     ws_bytes = int(lib.awq_w4a16_gemm_workspace_bytes(M, N, K, int(group_size), int(split_k), lc))
     ws = WORKSPACE.get(dev, ws_bytes) if ws_bytes else None
     rc = lib.awq_w4a16_gemm(
-        _ptr(a), int(a.stride(0)), _ptr(qweight), _ptr(scales), _ptr(qzeros), _ptr(bias), _ptr(out),
+        _ptr(a), lda, _ptr(qweight), _ptr(scales), _ptr(qzeros), _ptr(bias), _ptr(out),
         int(out.stride(0)), M, N, K, int(group_size), int(split_k), lc, dtype_code(a.dtype),
         dtype_code(scales.dtype), dtype_code(bias.dtype) if bias is not None else L.DTYPE_NONE,
         _ptr(ws), ws_bytes if ws is not None else 0, stream)

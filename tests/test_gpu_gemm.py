@@ -156,6 +156,28 @@ def test_gemm_autoawq_vs_oracle(M, K, N, G, stream):
         _check_vs_ref(y, yr, f"M={M} K={K} N={N}")
 
 
+@pytest.mark.parametrize("M,layout", [(1, None), (4, None), (16, None), (1, "stream"), (16, "stream"),
+                                      (64, None), (512, None)])
+def test_gemm_strided_rows(M, layout):
+    """Activation rows at a stride past K (read in place through lda, as the reference's kernel
+    takes stride_am, awq_fused_gemm.py:1074) and output rows at a stride past N (ldc): the same
+    bits as contiguous rows on the narrow, stream and prefill kernels, nothing written past N."""
+    ops = _lib()
+    K, N, G = 1024, 2048, 128
+    _note(f"gemm strided rows M={M} layout={layout}")
+    t = _to_dev(make_awq_problem(M=M, K=K, N=N, group_size=G, seed=M + 3))
+    y = ops.gemm(t["x"], t["qweight"], t["scales"], t["qzeros"], G, layout="autoawq", decode_layout=layout)
+    xb = torch.zeros((M, K + 64), dtype=torch.float16, device=DEV)
+    xb[:, :K] = t["x"]
+    ob = torch.full((M, N + 64), 7.0, dtype=torch.float16, device=DEV)
+    ys = ops.gemm(xb[:, :K], t["qweight"], t["scales"], t["qzeros"], G, layout="autoawq", decode_layout=layout,
+                  out=ob[:, :N])
+    torch.cuda.synchronize()
+    assert ys.data_ptr() == ob.data_ptr()
+    assert torch.equal(ys, y), (M, layout)
+    assert bool((ob[:, N:] == 7.0).all())
+
+
 @pytest.mark.parametrize("M", [1, 7, 40])
 @pytest.mark.parametrize("bias_dtype", [torch.float16, torch.bfloat16, torch.float32])
 def test_gemm_bias(M, bias_dtype):
