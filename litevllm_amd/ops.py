@@ -323,8 +323,9 @@ def _narrow_fits(M: int, N: int, K: int, split_k: int) -> bool:
     whole K, no split-K hand-off) instead of the 128-column stream.
 
     ``split_k = 0`` ("auto"): where the narrow kernel is faster (measured on MI355X: up to two
-    16-column tiles per CU while the activation rows fit the kernel's LDS staging, M = 1 .. 4;
-    otherwise, up to M = 16, one tile per CU and K <= 4096).
+    16-column tiles per CU while the activation rows fit the kernel's LDS staging, M = 1 .. 4,
+    or M = 5 .. 8 with K <= 4096 (K = 4096, N = 6144 / 8192: 7.6-8.6 us against 8.5-9.5 us
+    for the stream kernel); otherwise, up to M = 16, one tile per CU and K <= 4096).
     ``split_k = 1`` (the whole K per block, the reference's non-split kernel): the same kernel
     as auto wherever auto does not split K, so a forced 1 and auto give the same bits there;
     where auto would split, the narrow kernel, whose N / 16 blocks cover the chip that the
@@ -333,7 +334,7 @@ def _narrow_fits(M: int, N: int, K: int, split_k: int) -> bool:
     if split_k > 1:
         return False
     tiles = -(-N // 16)
-    if M <= 4 and M * K * 2 <= 49152:
+    if (M <= 4 and M * K * 2 <= 49152) or (M <= 8 and K <= 4096):
         auto = tiles <= 2 * L.num_cus()
     else:
         auto = M <= 16 and tiles <= L.num_cus() and K <= 4096

@@ -130,6 +130,8 @@ SHAPES = [
     (5, 512, 264, 32), (8, 4096, 1024, 128), (16, 1024, 2048, 128), (17, 512, 520, 128),
     (32, 2048, 1536, 128), (33, 512, 512, 128), (64, 1024, 768, 64), (100, 512, 2056, 128),
     (256, 1024, 1024, 128), (300, 2048, 512, 128),
+    # M = 5 .. 8 with two 16-column tiles per CU: the narrow kernel under auto
+    (6, 4096, 6144, 128), (8, 2048, 8192, 64),
     # group size 32 in the prefill kernel: two groups per 64-row stage, and K % 64 == 32
     (40, 2080, 520, 32), (64, 1024, 1024, 32), (300, 96, 264, 32),
     # group size 256: four stages per group in the prefill kernel (constants once per pair of
