@@ -325,7 +325,10 @@ def _narrow_fits(M: int, N: int, K: int, split_k: int) -> bool:
     ``split_k = 0`` ("auto"): where the narrow kernel is faster (measured on MI355X: up to two
     16-column tiles per CU while the activation rows fit the kernel's LDS staging, M = 1 .. 4,
     or M = 5 .. 8 with K <= 4096 (K = 4096, N = 6144 / 8192: 7.6-8.6 us against 8.5-9.5 us
-    for the stream kernel); otherwise, up to M = 16, one tile per CU and K <= 4096).
+    for the stream kernel); otherwise one tile per CU with K <= 14336 up to M = 4, K <= 8192 up
+    to M = 8 and K <= 4096 up to M = 16 (N = 4096: M = 4, K = 8192 7.9 against 9.2 us, K = 14336
+    10.9 against 11.6 us; M = 8, K = 8192 8.9 against 9.4 us; M = 8, K = 14336 and every N = 6144
+    case past those limits ran faster on the split stream kernel)).
     ``split_k = 1`` (the whole K per block, the reference's non-split kernel): the same kernel
     as auto wherever auto does not split K, so a forced 1 and auto give the same bits there;
     where auto would split, the narrow kernel, whose N / 16 blocks cover the chip that the
@@ -337,7 +340,7 @@ def _narrow_fits(M: int, N: int, K: int, split_k: int) -> bool:
     if (M <= 4 and M * K * 2 <= 49152) or (M <= 8 and K <= 4096):
         auto = tiles <= 2 * L.num_cus()
     else:
-        auto = M <= 16 and tiles <= L.num_cus() and K <= 4096
+        auto = tiles <= L.num_cus() and ((M <= 4 and K <= 14336) or (M <= 8 and K <= 8192) or (M <= 16 and K <= 4096))
     if split_k == 0 or auto:
         return auto
     return _auto_splits(M, N, K) > 1

@@ -162,7 +162,9 @@ def test_decode_layout_choice():
     assert not ops._narrow_fits(1, 32 * cus + 16, 4096, 0)
     assert ops._narrow_fits(4, 32 * cus, 4096, 0) and not ops._narrow_fits(4, 32 * cus + 16, 4096, 0)
     assert not ops._narrow_fits(1, 4096, 4096, 2)          # an explicit split asks for the stream kernel
-    assert ops._narrow_fits(4, 16 * cus, 4096, 0) and not ops._narrow_fits(4, 16 * cus, 8192, 0)
+    assert ops._narrow_fits(4, 16 * cus, 4096, 0) and ops._narrow_fits(4, 16 * cus, 14336, 0)
+    assert not ops._narrow_fits(4, 16 * cus, 16384, 0) and not ops._narrow_fits(4, 16 * cus + 16, 8192, 0)
+    assert ops._narrow_fits(8, 16 * cus, 8192, 0) and not ops._narrow_fits(8, 16 * cus, 12288, 0)
     assert not ops._narrow_fits(16, 16 * cus + 16, 4096, 0) and not ops._narrow_fits(17, 4096, 4096, 0)
     # M = 5 .. 8: two tiles per CU at K <= 4096, one beyond (the M <= 16 rule)
     assert ops._narrow_fits(8, 32 * cus, 4096, 0) and not ops._narrow_fits(8, 32 * cus + 16, 4096, 0)

@@ -132,6 +132,8 @@ SHAPES = [
     (256, 1024, 1024, 128), (300, 2048, 512, 128),
     # M = 5 .. 8 with two 16-column tiles per CU: the narrow kernel under auto
     (6, 4096, 6144, 128), (8, 2048, 8192, 64),
+    # one tile per CU over a long K (M <= 4 up to K = 14336, M <= 8 up to 8192): narrow too
+    (4, 8192, 4096, 128), (8, 8192, 2048, 64),
     # group size 32 in the prefill kernel: two groups per 64-row stage, and K % 64 == 32
     (40, 2080, 520, 32), (64, 1024, 1024, 32), (300, 96, 264, 32),
     # group size 256: four stages per group in the prefill kernel (constants once per pair of
