@@ -159,8 +159,13 @@ def test_decode_layout_choice():
     from litevllm_amd import ops
     cus = L.num_cus()
     assert ops._narrow_fits(1, 4096, 4096, 0) and ops._narrow_fits(1, 32 * cus, 14336, 0)
-    assert not ops._narrow_fits(1, 32 * cus + 16, 4096, 0)
-    assert ops._narrow_fits(4, 32 * cus, 4096, 0) and not ops._narrow_fits(4, 32 * cus + 16, 4096, 0)
+    assert not ops._narrow_fits(1, 32 * cus + 16, 14336, 0)
+    # activation rows in the kernel's LDS: four tiles per CU at M <= 2 and K <= 4096, three at
+    # K <= 8192 (M <= 4), else two
+    assert ops._narrow_fits(1, 64 * cus, 4096, 0) and not ops._narrow_fits(1, 64 * cus + 16, 4096, 0)
+    assert ops._narrow_fits(2, 64 * cus, 4096, 0) and not ops._narrow_fits(4, 64 * cus, 4096, 0)
+    assert ops._narrow_fits(4, 48 * cus, 4096, 0) and not ops._narrow_fits(4, 48 * cus + 16, 4096, 0)
+    assert ops._narrow_fits(1, 48 * cus, 8192, 0) and not ops._narrow_fits(1, 48 * cus + 16, 8192, 0)
     assert not ops._narrow_fits(1, 4096, 4096, 2)          # an explicit split asks for the stream kernel
     assert ops._narrow_fits(4, 16 * cus, 4096, 0) and ops._narrow_fits(4, 16 * cus, 14336, 0)
     assert not ops._narrow_fits(4, 16 * cus, 16384, 0) and not ops._narrow_fits(4, 16 * cus + 16, 8192, 0)
