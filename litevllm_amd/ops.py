@@ -324,10 +324,11 @@ def _narrow_fits(M: int, N: int, K: int, split_k: int) -> bool:
 
     ``split_k = 0`` ("auto"): where the narrow kernel is faster (measured on MI355X: while the
     activation rows fit the kernel's LDS staging, M = 1 .. 4, up to four 16-column tiles per CU
-    at M <= 2 and K <= 4096 (K = 4096, N = 11008 .. 16384: 7.7-10.3 us against 9.2-11.8 us for
+    at M <= 3 and K <= 4096 (K = 4096, N = 11008 .. 16384: 7.7-10.7 us against 9.2-12.0 us for
     the stream kernel; at N = 20480 the stream kernel is ahead), up to three at K <= 8192
     (M = 4, N = 12288: 8.9 against 10.5 us; M = 1, K = 8192, N = 12288: 13.4 against 13.6 us),
-    else up to two; up to two tiles per CU at M = 5 .. 8 with K <= 4096 (K = 4096, N = 6144 / 8192: 7.6-8.6 us against 8.5-9.5 us
+    else up to two; with K <= 4096, up to three tiles per CU at M = 5 (N = 12288: 9.5 against
+    10.7 us) and two at M = 6 .. 8 (K = 4096, N = 6144 / 8192: 7.6-8.6 us against 8.5-9.5 us
     for the stream kernel); otherwise one tile per CU with K <= 14336 up to M = 4, K <= 8192 up
     to M = 8 and K <= 4096 up to M = 16 (N = 4096: M = 4, K = 8192 7.9 against 9.2 us, K = 14336
     10.9 against 11.6 us; M = 8, K = 8192 8.9 against 9.4 us; M = 8, K = 14336 and every N = 6144
@@ -341,10 +342,10 @@ def _narrow_fits(M: int, N: int, K: int, split_k: int) -> bool:
         return False
     tiles = -(-N // 16)
     if M <= 4 and M * K * 2 <= 49152:
-        per_cu = 4 if (M <= 2 and K <= 4096) else (3 if K <= 8192 else 2)
+        per_cu = 4 if (M <= 3 and K <= 4096) else (3 if K <= 8192 else 2)
         auto = tiles <= per_cu * L.num_cus()
     elif M <= 8 and K <= 4096:
-        auto = tiles <= 2 * L.num_cus()
+        auto = tiles <= (3 if M <= 5 else 2) * L.num_cus()
     else:
         auto = tiles <= L.num_cus() and ((M <= 4 and K <= 14336) or (M <= 8 and K <= 8192) or (M <= 16 and K <= 4096))
     if split_k == 0 or auto:

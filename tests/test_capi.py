@@ -163,7 +163,9 @@ def test_decode_layout_choice():
     # activation rows in the kernel's LDS: four tiles per CU at M <= 2 and K <= 4096, three at
     # K <= 8192 (M <= 4), else two
     assert ops._narrow_fits(1, 64 * cus, 4096, 0) and not ops._narrow_fits(1, 64 * cus + 16, 4096, 0)
-    assert ops._narrow_fits(2, 64 * cus, 4096, 0) and not ops._narrow_fits(4, 64 * cus, 4096, 0)
+    assert ops._narrow_fits(3, 64 * cus, 4096, 0) and not ops._narrow_fits(4, 64 * cus, 4096, 0)
+    assert ops._narrow_fits(5, 48 * cus, 4096, 0) and not ops._narrow_fits(5, 48 * cus + 16, 4096, 0)
+    assert ops._narrow_fits(6, 32 * cus, 4096, 0) and not ops._narrow_fits(6, 32 * cus + 16, 4096, 0)
     assert ops._narrow_fits(4, 48 * cus, 4096, 0) and not ops._narrow_fits(4, 48 * cus + 16, 4096, 0)
     assert ops._narrow_fits(1, 48 * cus, 8192, 0) and not ops._narrow_fits(1, 48 * cus + 16, 8192, 0)
     assert not ops._narrow_fits(1, 4096, 4096, 2)          # an explicit split asks for the stream kernel

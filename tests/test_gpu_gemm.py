@@ -135,7 +135,7 @@ SHAPES = [
     # one tile per CU over a long K (M <= 4 up to K = 14336, M <= 8 up to 8192): narrow too
     (4, 8192, 4096, 128), (8, 8192, 2048, 64),
     # three and four 16-column tiles per CU (M <= 2, K <= 4096): narrow under auto
-    (1, 2048, 12288, 128), (2, 4096, 16384, 64),
+    (1, 2048, 12288, 128), (2, 4096, 16384, 64), (3, 2048, 16384, 64), (5, 2048, 12288, 128),
     # group size 32 in the prefill kernel: two groups per 64-row stage, and K % 64 == 32
     (40, 2080, 520, 32), (64, 1024, 1024, 32), (300, 96, 264, 32),
     # group size 256: four stages per group in the prefill kernel (constants once per pair of
