@@ -63,7 +63,8 @@ extern "C" {
  *                      that the decode kernel reads it as contiguous 2 KiB runs; qzeros and
  *                      scales stay in the AUTOAWQ layout.  Accepted by awq_w4a16_gemm for every
  *                      M (K % 32 == 0): the decode kernel serves M <= 32 with group sizes
- *                      32/64/128, the prefill kernel the rest, so one copy serves both.
+ *                      32/64/128 (and 32-row chunks up to M = 64, or 128 at N <= 4096), the
+ *                      prefill kernel the rest, so one copy serves both.
  * AWQ_LAYOUT_DECODE_NARROW : an AUTOAWQ qweight re-ordered by awq_w4a16_pack_decode_narrow
  *                      into 16-column tiles cut along K into quads of four 32-row k-steps
  *                      (KQ = ceil(K / 128) quads per tile; k-steps past K are zero): the run of
@@ -124,9 +125,10 @@ size_t awq_w4a16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t g
                                       int32_t split_k, int32_t layout);
 
 /* C[M, N] = A[M, K] . dequant(W)^T (+ bias), products accumulated in fp32, one rounding to
- * act_dtype at the end.  M <= 32 with group_size 32, 64 or 128 (the decode kernel): the
- * weights enter unrounded, (q - z) * s in fp32 -- the reference's M = 1 formulation,
- * awq_fused_gemm.py:1966-1971.  Otherwise (the prefill kernel): W rounded once to act_dtype,
+ * act_dtype at the end.  M <= 32 with group_size 32, 64 or 128 (the decode kernel; calls up to
+ * M = 64, or 128 at N <= 4096, run as 32-row chunks on it, one launch each, in order on the
+ * stream): the weights enter unrounded, (q - z) * s in fp32 -- the reference's M = 1
+ * formulation, awq_fused_gemm.py:1966-1971.  Otherwise (the prefill kernel): W rounded once to act_dtype,
  * as awq_w4a16_dequant computes it (the reference's tl.dot branch, 1973-1976).
  *   a: [M, K] act_dtype (F16 or BF16), row stride lda (elements).
  *   layout: AUTOAWQ or KN_SEQ (qweight [K, N/8]), DECODE_STREAM (any M) or DECODE_NARROW

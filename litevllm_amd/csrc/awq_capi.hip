@@ -36,6 +36,16 @@ static bool decode_covers(int64_t M, int64_t G) {
   return M <= 32 && (G == 32 || G == 64 || G == 128);
 }
 
+// Calls a little above the decode kernels' 32 rows run as 32-row chunks on them, one launch
+// each: the prefill kernel's few 256-row tiles keep most CUs idle there, each tile's K loop
+// taking about 58 us at K = 4096 (measured on MI355X, K = 4096, graph replays: M = 48 / 64 /
+// 96 / 128 at N = 4096 57.6 / 57.7 / 57.8 / 57.9 us against 19.5 / 24.1 / 35.8 / 47.5 us in
+// chunks; M = 64 at N = 12288 / 24576 60.6 / 62.5 against 32.9 / 38.0 us; M = 128 at those N
+// the prefill kernel is ahead, 62.9 / 63.1 against 65.5 / 75.7 us).
+static bool decode_chunks(int64_t M, int64_t N, int64_t G) {
+  return M > 32 && decode_covers(32, G) && (M <= 64 || (M <= 128 && N <= 4096));
+}
+
 }  // namespace awq_host
 
 // ---- scratch of the allocation-free GEMM ------------------------------------------------
@@ -121,6 +131,7 @@ int awq_w4a16_dequant(const int32_t* qweight, const void* scales, const int32_t*
 size_t awq_w4a16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_size,
                                       int32_t split_k, int32_t layout) {
   if (M <= 0 || N <= 0 || K <= 0 || (N % 8) != 0 || split_k < 0) return 0;
+  if (decode_chunks(M, N, group_size)) M = 32;  // the chunks run one after another
   if (group_size <= 0 || (K % group_size) != 0 || !decode_covers(M, group_size)) return 0;
   if (layout == AWQ_LAYOUT_DECODE_NARROW) return 0;  // the narrow kernel does not split K
   // the plan also depends on the dtype path: size for the largest
@@ -204,6 +215,18 @@ static int gemm_impl(const void* a, int64_t lda, const int32_t* qweight, const v
     }
     if (!launch_decode(ga, sp, mode, seq, zp, act_dtype, scale_dtype, st)) return AWQ_ERR_UNSUPPORTED;
     return launch_status();
+  }
+  if (rows <= 1 && decode_chunks(M, N, group_size)) {
+    // 32-row chunks in order on the stream, sharing the workspace (each chunk's split-K
+    // counters return to zero before the next starts)
+    for (int64_t m0 = 0; m0 < M; m0 += 32) {
+      const int64_t mc = M - m0 < 32 ? M - m0 : 32;
+      const int rc = gemm_impl((const uint16_t*)a + m0 * lda, lda, qweight, scales, qzeros, bias, (uint16_t*)c + m0 * ldc,
+                               ldc, mc, N, K, group_size, split_k, layout, act_dtype, scale_dtype, bias_dtype, workspace,
+                               workspace_bytes, stream, 0);
+      if (rc != AWQ_OK) return rc;
+    }
+    return AWQ_OK;
   }
   if ((K % 32) != 0) return AWQ_ERR_SHAPE;
   if (layout == AWQ_LAYOUT_DECODE_STREAM) {

@@ -235,7 +235,10 @@ def test_rmsnorm_gemm_workspace_is_host_only(lib):
     wbf = lib.awq_w4a16_rmsnorm_gemm_workspace_bytes(1, 4096, 12288, 128, 8, 0, L.DTYPE_BF16)
     assert w16 >= g + 12288 * 2 and wbf >= w16 + 4096 * 2
     # no GEMM workspace (prefill): the counter region is still kept clear
-    assert lib.awq_w4a16_rmsnorm_gemm_workspace_bytes(64, 4096, 4096, 128, 0, 0, L.DTYPE_F16) == 65536 + 64 * 4096 * 2
+    assert lib.awq_w4a16_gemm_workspace_bytes(256, 4096, 4096, 128, 0, 0) == 0
+    assert lib.awq_w4a16_rmsnorm_gemm_workspace_bytes(256, 4096, 4096, 128, 0, 0, L.DTYPE_F16) == 65536 + 256 * 4096 * 2
+    # M = 64 runs as two 32-row decode chunks, one after another: one chunk's workspace
+    assert lib.awq_w4a16_gemm_workspace_bytes(64, 4096, 4096, 128, 0, 0) == lib.awq_w4a16_gemm_workspace_bytes(32, 4096, 4096, 128, 0, 0)
 
 
 def test_workspace_grows_geometrically():

@@ -10,6 +10,7 @@ import torch.nn as nn
 from litevllm_amd.fused_pair import _lora_is_active, try_fused_awq_pair_matmul
 from oracle import awq_oracle as O
 from oracle.gen import make_awq_problem
+from kernel_paths import decode_serves
 
 
 def _lin(p, layout="autoawq", dev="cpu", bias=None, zeros=True, **kw):
@@ -67,8 +68,8 @@ def test_fused_pair_matches_oracle_and_separate_calls(M, zeros):
     assert torch.equal(y, y2)
     za = pa["qzeros"] if zeros else None
     zb = pb["qzeros"] if zeros else None
-    # the skinny kernel (M <= 32) multiplies unrounded weights, the prefill one fp16 ones
-    wdt = "float32" if M <= 32 else "float16"
+    # the skinny kernels (M <= 32, and 32-row chunks of them up to 64) multiply unrounded weights, the prefill one fp16 ones
+    wdt = "float32" if decode_serves(M, 2 * N, G) else "float16"
     wa = O.dequant_awq(pa["qweight"], pa["scales"], za, G, out_dtype=wdt, zero_point=zeros)
     wb = O.dequant_awq(pb["qweight"], pb["scales"], zb, G, out_dtype=wdt, zero_point=zeros)
     w = np.concatenate([wa, wb], axis=1).T                       # [2N, K]

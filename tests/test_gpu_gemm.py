@@ -18,6 +18,7 @@ import torch
 from oracle import awq_oracle as O
 from oracle import ref_cpu as R
 from oracle.gen import make_awq_problem
+from kernel_paths import decode_serves
 
 pytestmark = pytest.mark.gpu
 
@@ -37,18 +38,14 @@ def _note(msg):
     print(msg, flush=True)
 
 
-def _decode_path(M, G):
-    """Calls the skinny kernel serves (M <= 32, G in {32, 64, 128}).  It feeds the MFMA the
-    exact integers q - z and scales each group's fp32 sum, so its weights enter unrounded, as
-    in the reference's M = 1 branch (awq_fused_gemm.py:1966-1971); the prefill kernel rounds
-    them to the activation dtype first, as the reference's tl.dot branch does (1973-1976)."""
-    return M <= 32 and G in (32, 64, 128)
-
-
 def _w_used(p, M, G, zp=True, half="float16"):
-    """Dequantized [K, N] weights as the kernel serving (M, G) multiplies them: float32
-    unrounded on the decode path, else rounded once to ``half``."""
-    out = "float32" if _decode_path(M, G) else half
+    """Dequantized [K, N] weights as the kernel serving the call multiplies them: the skinny
+    kernels (M <= 32, and 32-row chunks of them a little above) feed the MFMA the exact
+    integers q - z and scale each group's fp32 sum, so their weights enter unrounded, as in the
+    reference's M = 1 branch (awq_fused_gemm.py:1966-1971); the prefill kernels round them to
+    the activation dtype first, as the reference's tl.dot branch does (1973-1976)."""
+    N = int(p["qweight"].shape[1]) * 8
+    out = "float32" if decode_serves(M, N, G) else half
     w = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"] if zp else None, G, out_dtype=out, zero_point=zp)
     return O.bf16_bits_to_f32(w) if out == "bfloat16" else w
 

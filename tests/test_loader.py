@@ -6,6 +6,7 @@ import torch
 
 from oracle import awq_oracle as O
 from oracle.gen import make_awq_problem
+from kernel_paths import decode_serves
 
 DEV = torch.device("cuda:0")
 
@@ -75,6 +76,6 @@ def test_adapted_weight_matmul(fmt, M):
     y = w.matmul(t(p["x"]).to(DEV), config={"kernel_policy": {"awq_fused_scope": "all"}}).float().cpu().numpy()
     zp = fmt != "symmetric"
     wd = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"] if zp else None, G,
-                       out_dtype="float32" if M <= 32 else "float16", zero_point=zp)
+                       out_dtype="float32" if decode_serves(M, N, G) else "float16", zero_point=zp)
     rep = O.error_report(y, O.linear_exact(p["x"], wd.T))
     assert rep["max_ulp"] <= 1.0, rep

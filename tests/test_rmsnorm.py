@@ -7,7 +7,7 @@ the normalised rows with the pinned oracle (``oracle.awq_oracle.rmsnorm_rows``) 
 oracle on the device's own normalised rows to one ulp of the output at ``max(|y|, 1)`` (the
 GEMM kernels' bar), and the whole call with the reference's formulation (oracle rows,
 fp16-rounded weights) to one ulp plus a per-output bound of the two known differences: the
-decode kernels (M <= 32) multiply by the unrounded weights, as the reference's own M = 1
+decode kernels (M <= 32, and 32-row chunks a little above) multiply by the unrounded weights, as the reference's own M = 1
 GEMM does (``awq_fused_gemm.py:1966-1971``), and a normalised element may sit one fp16 ulp
 from the oracle's.  bf16 results are the fp16 result converted once, which adds half a bf16
 ulp (four fp16 ulps) to each bound.
@@ -17,6 +17,7 @@ import pytest
 import torch
 
 from oracle import awq_oracle as O
+from kernel_paths import decode_serves
 
 DEV = torch.device("cuda:0")
 
@@ -69,18 +70,18 @@ def test_rmsnorm_awq_fused_linear_vs_oracle(M, N, K, G, dt):
     torch.cuda.synchronize()
     assert y.dtype == dt and y.shape == (M, N)
     xn = ops.rmsnorm(d(x), d(nw), 1e-6).cpu().numpy()
-    w = O.dequant_ref(qw.numpy(), sc.float().numpy(), qz.numpy(), G, out_dtype="float32" if M <= 32 else "float16")
+    w = O.dequant_ref(qw.numpy(), sc.float().numpy(), qz.numpy(), G, out_dtype="float32" if decode_serves(M, N, G) else "float16")
     exact = O.linear_exact(xn, w)
     yv = _np(y.cpu())
     ref = O.rmsnorm_awq_linear(_np(x), _np(nw), 1e-6, qw.numpy(), sc.numpy(), qz.numpy(), G)
     conv = 0.0 if dt == torch.float16 else 4.0  # fp16 -> bf16: half a bf16 ulp = 4 fp16 ulps
     assert _ulps(yv, exact).max() <= 1.0 + conv
     # against the reference's own formulation: within one ulp plus the two documented
-    # differences, bounded term by term -- unrounded weights for M <= 32 (each fp16 weight is
+    # differences, bounded term by term -- unrounded weights on the decode kernels (each fp16 weight is
     # within 2^-11 of the product, relatively) and a normalised element one fp16 ulp apart
     xo = O.rmsnorm_rows(_np(x), _np(nw), 1e-6).astype(np.float64)
     w16 = np.abs(O.dequant_ref(qw.numpy(), sc.numpy(), qz.numpy(), G).astype(np.float64))
-    dev_terms = (np.abs(xo) * 2.0 ** -11 if M <= 32 else 0.0) + O.fp16_ulp(xo, floor=2.0 ** -14)
+    dev_terms = (np.abs(xo) * 2.0 ** -11 if decode_serves(M, N, G) else 0.0) + O.fp16_ulp(xo, floor=2.0 ** -14)
     bound = dev_terms @ w16.T
     excess = np.abs(yv.astype(np.float64) - ref) - bound
     assert (excess / O.fp16_ulp(ref, 1.0)).max() <= 1.0 + conv

@@ -26,6 +26,7 @@ import torch
 from litevllm_amd import ops
 from oracle import awq_oracle as O
 from oracle.gen import make_awq_problem
+from kernel_paths import decode_serves
 
 # the modules themselves (the package re-exports functions of the same names)
 AFG = importlib.import_module("litevllm_amd.awq_fused_gemm")
@@ -289,7 +290,7 @@ def test_awqconfig_apply_reference_layout(M, K, N, G, zp):
     # 1443-1447): three counted entries for two calls
     assert st["awq_fused_success"] == 2 and st["awq_matmul_calls"] == 3
     w = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"] if zp else None, G,
-                      out_dtype="float32" if (M <= 32 and G in (32, 64, 128)) else "float16", zero_point=zp)
+                      out_dtype="float32" if decode_serves(M, N, G) else "float16", zero_point=zp)
     ye = O.linear_exact(p["x"], w.T, bias.double().numpy())
     rep = O.error_report(y.view(M, N).cpu().numpy(), ye)
     assert rep["max_ulp"] <= 1.0, rep
@@ -361,7 +362,7 @@ def test_dense_fallback(mode, monkeypatch):
 def test_awq_gemm_triton_split_k_iters(M, split):
     """``awq_gemm_triton(input, qweight, scales, zeros, group_size, split_k_iters)`` on
     reference-layout tensors: split 1 and 4 each within 1 ulp of the exact oracle, split 4
-    bitwise reproducible (the prefill kernel at M = 64 takes no split)."""
+    bitwise reproducible (M = 64 runs as two 32-row chunks of the decode kernels)."""
     print(f"awq_gemm_triton M={M} split={split}", flush=True)
     K, N, G = 4096, 1024, 128
     p = make_awq_problem(M=M, K=K, N=N, group_size=G, seed=5 * M + split)
@@ -371,7 +372,7 @@ def test_awq_gemm_triton_split_k_iters(M, split):
     y = AT.awq_gemm_triton(x, *args, group_size=G, split_k_iters=split)
     y2 = AT.awq_gemm_triton(x, *args, group_size=G, split_k_iters=split)
     assert torch.equal(y, y2)
-    w = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"], G, out_dtype="float32" if M <= 32 else "float16")
+    w = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"], G, out_dtype="float32" if decode_serves(M, N, G) else "float16")
     rep = O.error_report(y.cpu().numpy(), O.linear_exact(p["x"], w.T))
     assert rep["max_ulp"] <= 1.0, rep
 
@@ -481,7 +482,8 @@ def test_weight_holds_its_derived_copies(N, copies):
     x = torch.from_numpy(p["x"]).to(DEV)
     for m in (1, 64):
         y = w.matmul(x[:m]).cpu().numpy()
-        wd = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"], G, out_dtype="float32" if m <= 32 else "float16")
+        wd = O.dequant_awq(p["qweight"], p["scales"], p["qzeros"], G,
+                           out_dtype="float32" if decode_serves(m, N, G) else "float16")
         rep = O.error_report(y, O.linear_exact(p["x"][:m], wd.T))
         assert rep["max_ulp"] <= 1.0, (m, rep)
         y2 = AFG.awq_fused_gemm(x[:m], w.qweight, w.scales, w.qzeros, G)
