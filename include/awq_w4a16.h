@@ -63,8 +63,8 @@ extern "C" {
  *                      that the decode kernel reads it as contiguous 2 KiB runs; qzeros and
  *                      scales stay in the AUTOAWQ layout.  Accepted by awq_w4a16_gemm for every
  *                      M (K % 32 == 0): the decode kernel serves M <= 32 with group sizes
- *                      32/64/128 (and 32-row chunks up to M = 64, or 128 at N <= 4096), the
- *                      prefill kernel the rest, so one copy serves both.
+ *                      32/64/128 (and 32-row chunks of it up to M = 64), the prefill
+ *                      kernel the rest, so one copy serves both.
  * AWQ_LAYOUT_DECODE_NARROW : an AUTOAWQ qweight re-ordered by awq_w4a16_pack_decode_narrow
  *                      into 16-column tiles cut along K into quads of four 32-row k-steps
  *                      (KQ = ceil(K / 128) quads per tile; k-steps past K are zero): the run of
@@ -117,7 +117,8 @@ int awq_w4a16_dequant(const int32_t* qweight, const void* scales, const int32_t*
 
 /* Workspace bytes awq_w4a16_gemm needs for these arguments (0 if none).  The workspace
  * starts with a fixed 64 KiB region of per-tile arrival counters followed by fp32 split-K
- * partials.  The counter region must be zero the first time a workspace is used; every
+ * partials (the decode kernels', or the prefill kernel's K ranges: [ranges][M][N]; a prefill
+ * call given less than that runs its whole K per tile).  The counter region must be zero the first time a workspace is used; every
  * call leaves it zero again, so a workspace allocated zeroed once can be reused by later
  * calls of any shape on the same stream.  Two calls that may run concurrently must not
  * share a workspace. */
@@ -126,8 +127,8 @@ size_t awq_w4a16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t g
 
 /* C[M, N] = A[M, K] . dequant(W)^T (+ bias), products accumulated in fp32, one rounding to
  * act_dtype at the end.  M <= 32 with group_size 32, 64 or 128 (the decode kernel; calls up to
- * M = 64, or 128 at N <= 4096, run as 32-row chunks on it, one launch each, in order on the
- * stream): the weights enter unrounded, (q - z) * s in fp32 -- the reference's M = 1
+ * M = 64 run as 32-row chunks on it, one launch each, in order on the stream): the weights
+ * enter unrounded, (q - z) * s in fp32 -- the reference's M = 1
  * formulation, awq_fused_gemm.py:1966-1971.  Otherwise (the prefill kernel): W rounded once to act_dtype,
  * as awq_w4a16_dequant computes it (the reference's tl.dot branch, 1973-1976).
  *   a: [M, K] act_dtype (F16 or BF16), row stride lda (elements).
@@ -139,8 +140,11 @@ size_t awq_w4a16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t g
  *   bias: NULL or [N] of bias_dtype (F16, BF16 or F32), added once in fp32.
  *   c: [M, N] act_dtype, row stride ldc.
  *   split_k: number of contiguous K partitions of the decode kernel whose fp32 partial sums
- *            are added in a fixed order (0 = choose automatically; the prefill kernel does
- *            not split K).  For a given (M, N, K, split_k) the result is bitwise
+ *            are added in a fixed order (0 = choose automatically; with 0 and the
+ *            DECODE_STREAM layout the prefill kernel cuts K into 3 .. 8 ranges of whole
+ *            64-row stage pairs where its 256 x 256 tiles cover at most a third of the CUs
+ *            and the workspace holds their fp32 partials, summed in range order; otherwise
+ *            the prefill kernel does not split K).  For a given (M, N, K, split_k) the result is bitwise
  *            reproducible.  Partition s covers rows [64 s I, min(64 (s+1) I, K)) with
  *            I = ceil(ceil(K / 64) / split_k), as in awq_fused_gemm.py:1798-1800.  The
  *            DECODE_NARROW layout never splits K (split_k is ignored there).

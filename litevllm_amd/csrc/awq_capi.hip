@@ -36,14 +36,41 @@ static bool decode_covers(int64_t M, int64_t G) {
   return M <= 32 && (G == 32 || G == 64 || G == 128);
 }
 
-// Calls a little above the decode kernels' 32 rows run as 32-row chunks on them, one launch
-// each: the prefill kernel's few 256-row tiles keep most CUs idle there, each tile's K loop
-// taking about 58 us at K = 4096 (measured on MI355X, K = 4096, graph replays: M = 48 / 64 /
-// 96 / 128 at N = 4096 57.6 / 57.7 / 57.8 / 57.9 us against 19.5 / 24.1 / 35.8 / 47.5 us in
-// chunks; M = 64 at N = 12288 / 24576 60.6 / 62.5 against 32.9 / 38.0 us; M = 128 at those N
-// the prefill kernel is ahead, 62.9 / 63.1 against 65.5 / 75.7 us).
+// Calls of 33 .. 64 rows run as 32-row chunks on the decode kernels, one launch each: the
+// prefill kernel's one 256-row tile per column tile keeps most CUs idle there, each tile's K
+// loop taking about 58 us at K = 4096 (measured on MI355X, K = 4096, graph replays: M = 48 / 64
+// at N = 4096 57.6 / 57.7 us against 19.5 / 24.1 us in chunks; M = 64 at N = 12288 / 24576
+// 60.6 / 62.5 against 32.9 / 38.0 us).  Above 64 rows the prefill kernel's K ranges (below)
+// are ahead of more chunks (M = 128, N = 4096: 26-27 us against 47.5 us in four chunks).
 static bool decode_chunks(int64_t M, int64_t N, int64_t G) {
-  return M > 32 && decode_covers(32, G) && (M <= 64 || (M <= 128 && N <= 4096));
+  (void)N;
+  return M > 32 && M <= 64 && decode_covers(32, G);
+}
+
+// K ranges of the prefill stream kernel (split_k = 0, stream layout): where its 256 x 256 tiles
+// cover at most a third of the CUs, each tile's K loop is cut into 3 .. 8 ranges of whole stage
+// pairs (fp32 partials, summed in range order by a second launch), so that tiles x ranges
+// comes near one block per CU.  1 = no split.  Measured on MI355X (K = 4096, graph replays,
+// whole K against ranges): M = 128 .. 384 at N = 2048 .. 8192 57-64 us against 26-51 us
+// (M = 256, N = 4096: 57.9 against 26.8 us); two ranges lost (M = 384 / 512 at N = 12288 and
+// M = 2048 at N = 4096: 2-12% slower), so three is the least.
+static int prefill_splits(int64_t M, int64_t N, int64_t K, int64_t G, int32_t split_k, int32_t layout) {
+  if (split_k != 0 || layout != AWQ_LAYOUT_DECODE_STREAM || M <= 32 || decode_chunks(M, N, G)) return 1;
+  if (G <= 0 || (G & (G - 1)) != 0 || (K % 32) != 0 || (N % 8) != 0) return 1;
+  const int64_t tiles = ((M + 255) / 256) * ((N + 255) / 256);
+  const int64_t nst = (K + 63) / 64;
+  const int64_t cus = num_cus();
+  if (tiles * 3 > cus || nst < 12) return 1;
+  int64_t S = cus / tiles;
+  S = S > 8 ? 8 : S;
+  S = S > nst / 4 ? nst / 4 : S;  // ranges of at least four stages
+  return S < 3 ? 1 : (int)S;
+}
+// The partials go after the decode kernels' counter region, which a workspace shared between
+// calls keeps zero.
+static size_t prefill_split_bytes(int64_t M, int64_t N, int64_t K, int64_t G, int32_t split_k, int32_t layout) {
+  const int S = prefill_splits(M, N, K, G, split_k, layout);
+  return S > 1 ? kCounterBytes + (size_t)S * (size_t)M * (size_t)N * sizeof(float) : 0;
 }
 
 }  // namespace awq_host
@@ -128,8 +155,11 @@ int awq_w4a16_dequant(const int32_t* qweight, const void* scales, const int32_t*
                         out_dtype, (hipStream_t)stream);
 }
 
-size_t awq_w4a16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_size,
-                                      int32_t split_k, int32_t layout) {
+// The decode kernels' workspace (split-K counters and partials) alone: what the allocation-free
+// entry point provides; the prefill kernel's K ranges run only where the caller's workspace
+// holds them.
+static size_t decode_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_size, int32_t split_k,
+                                     int32_t layout) {
   if (M <= 0 || N <= 0 || K <= 0 || (N % 8) != 0 || split_k < 0) return 0;
   if (decode_chunks(M, N, group_size)) M = 32;  // the chunks run one after another
   if (group_size <= 0 || (K % group_size) != 0 || !decode_covers(M, group_size)) return 0;
@@ -143,6 +173,14 @@ size_t awq_w4a16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t g
     ws = b > ws ? b : ws;
   }
   return ws;
+}
+
+size_t awq_w4a16_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t group_size,
+                                      int32_t split_k, int32_t layout) {
+  if (M <= 0 || N <= 0 || K <= 0 || (N % 8) != 0 || split_k < 0) return 0;
+  const size_t pre = (group_size > 0 && (K % group_size) == 0) ? prefill_split_bytes(M, N, K, group_size, split_k, layout) : 0;
+  const size_t dec = decode_workspace_bytes(M, N, K, group_size, split_k, layout);
+  return pre > dec ? pre : dec;
 }
 
 }  // extern "C"
@@ -230,6 +268,13 @@ static int gemm_impl(const void* a, int64_t lda, const int32_t* qweight, const v
   }
   if ((K % 32) != 0) return AWQ_ERR_SHAPE;
   if (layout == AWQ_LAYOUT_DECODE_STREAM) {
+    // K ranges where the workspace holds their fp32 partials (else the whole K per tile)
+    const int S = rows <= 1 ? prefill_splits(M, N, K, group_size, split_k, layout) : 1;
+    if (S > 1 && workspace && !(((uintptr_t)workspace) & 15) &&
+        workspace_bytes >= kCounterBytes + (size_t)S * (size_t)M * (size_t)N * sizeof(float)) {
+      ga.partial = (float*)((char*)workspace + kCounterBytes);
+      ga.ksplit = S;
+    }
     if (!launch_prefill_stream(ga, zp, act_dtype, scale_dtype, st)) return AWQ_ERR_UNSUPPORTED;
   } else if (!launch_prefill(ga, seq, zp, act_dtype, scale_dtype, st)) {
     return AWQ_ERR_UNSUPPORTED;
@@ -256,7 +301,9 @@ int awq_w4a16_gemm_noalloc(const void* a, int64_t lda, const int32_t* qweight, c
                            int32_t scale_dtype, int32_t bias_dtype, void* stream) {
   if (M < 0 || N < 0 || K <= 0 || group_size <= 0 || split_k < 0) return AWQ_ERR_SHAPE;
   if (M == 0 || N == 0) return AWQ_OK;
-  const size_t need = awq_w4a16_gemm_workspace_bytes(M, N, K, group_size, split_k, layout);
+  // the decode kernels' split-K needs only: prefill calls get no workspace here, so each of
+  // their tiles takes the whole K
+  const size_t need = decode_workspace_bytes(M, N, K, group_size, split_k, layout);
   if (need > kNoallocScratchBytes) return AWQ_ERR_WORKSPACE;  // beyond the fixed scratch
   void* ws = nullptr;
   if (need > 0) {

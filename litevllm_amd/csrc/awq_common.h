@@ -243,6 +243,9 @@ struct GemmArgs {
   // decode kernels only: > 1 = a row-exact launch (awq_w4a16_gemm_rows_exact) of that many grid
   // rows, M = 1: grid row y computes row y of the call as a lone M = 1 call would (row_slice)
   int rows;
+  // prefill stream kernel only: > 1 = split K into that many ranges of whole stage pairs, each
+  // writing its fp32 sums to partial[split][M][N], summed in split order by a second launch
+  int ksplit;
 };
 
 // Block coordinates of a stream-kernel decode launch: x = the block of the M = 1 plan (nblocks

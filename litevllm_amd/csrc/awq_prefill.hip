@@ -54,7 +54,7 @@ constexpr int kPSBM = 256, kPSBK = 64;
 
 template <int NWN, bool ZP, typename T, bool FAST, bool GPAIR>
 __global__ void __launch_bounds__(128 * NWN, 2) prefill_stream_kernel(const GemmArgs p, int scale_bf16, int tiles_m,
-                                                                      int tiles_n, int log2g, int n_off) {
+                                                                      int tiles_n, int log2g, int n_off, int s_per) {
   constexpr int NT = 128 * NWN;                // threads
   constexpr int BM = kPSBM, BN = 64 * NWN, BK = kPSBK;
   constexpr int CPR = BK / 8;                  // 16-byte chunks per LDS row
@@ -81,6 +81,11 @@ __global__ void __launch_bounds__(128 * NWN, 2) prefill_stream_kernel(const Gemm
 
   const int KS = p.K >> 5;                     // 32-row k-steps of the stream layout
   const int nst = (p.K + BK - 1) / BK;
+  // split-K (s_per > 0): grid row blockIdx.y takes stages s_beg .. s_end - 1 (s_per even, so the
+  // stage pairs that share constants stay whole)
+  const int split = blockIdx.y;
+  const int s_beg = s_per > 0 ? split * s_per : 0;
+  const int s_end = s_per > 0 ? min(s_beg + s_per, nst) : nst;
   const int ngroups = p.K / p.G;
   const int NW = p.N >> 3;
 
@@ -188,7 +193,7 @@ __global__ void __launch_bounds__(128 * NWN, 2) prefill_stream_kernel(const Gemm
   // half stage when K % 64 == 32) reads through an empty descriptor instead: zeros, no traffic.
   // Its activations are zero, so the zero piece adds nothing.
   auto load_b = [&](int s, int slot) {
-    bq[slot] = asm_load16(2 * s + pks < KS ? wrs : wrs0, w_voff, (uint32_t)s * 4096u);
+    bq[slot] = asm_load16(2 * s + pks < KS && s < s_end ? wrs : wrs0, w_voff, (uint32_t)s * 4096u);
     if (GPAIR && slot == 1) return;  // odd stage (slot = stage parity): constants reused
     const int gi = min((s * BK + 8 * kchunk) >> log2g, ngroups - 1);
     bs[slot].s4 = asm_load16(srs, (uint32_t)((gi * p.N + 8 * wld) * 2), 0u);
@@ -302,10 +307,10 @@ __global__ void __launch_bounds__(128 * NWN, 2) prefill_stream_kernel(const Gemm
     }
   };
 
-  // prologue: stage 0's activations and weights, stage 1's weights in flight
-  dma_a(0, 0);
-  load_b(0, 0);
-  load_b(1, 1);
+  // prologue: stage s_beg's activations and weights, the next stage's weights in flight
+  dma_a(s_beg, 0);
+  load_b(s_beg, 0);
+  load_b(s_beg + 1, 1);
   AWQ_WAIT_VMCNT(NB_ODD);
   pin_after_wait(bq[0]);
   pin_after_wait(bs[0].s4);
@@ -318,7 +323,7 @@ __global__ void __launch_bounds__(128 * NWN, 2) prefill_stream_kernel(const Gemm
   // s & 1), compute stage s and write stage s + 1's weights (slot (s + 1) & 1); one barrier per
   // stage once this wave's activation DMA has landed
   auto step = [&](int s, int cb) {
-    const bool dma = s + 1 < nst;
+    const bool dma = s + 1 < s_end;
     if (dma) dma_a(s + 1, cb ^ 1);
     load_b(s + 2, cb);
     stage(cb, cb ^ 1, dma);
@@ -326,12 +331,12 @@ __global__ void __launch_bounds__(128 * NWN, 2) prefill_stream_kernel(const Gemm
     else AWQ_WAIT_VMCNT(NB);
     __syncthreads();
   };
-  int s = 0;
-  for (; s + 1 < nst; s += 2) {
+  int s = s_beg;
+  for (; s + 1 < s_end; s += 2) {
     step(s, 0);
     step(s + 1, 1);
   }
-  if (s < nst) step(s, 0);
+  if (s < s_end) step(s, 0);
   // the last stages' (empty) weight loads: their registers stay reserved until they have landed
   AWQ_WAIT_VMCNT0();
 #pragma unroll
@@ -341,6 +346,23 @@ __global__ void __launch_bounds__(128 * NWN, 2) prefill_stream_kernel(const Gemm
     pin_after_wait(bs[k].zw);
   }
 
+  if (s_per > 0) {
+    // split-K: this range's fp32 sums (no bias) into partial[split]; 32 lanes store 32
+    // consecutive columns of a row
+    float* part = p.partial + (size_t)split * (size_t)p.M * (size_t)p.N;
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const int gcol = n0 + 64 * wn + 32 * nt + l32;
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int grow = m0 + 128 * wm + 32 * mt + 8 * (r >> 2) + 4 * lh + (r & 3);
+          if (grow < p.M && gcol < p.N) part[(size_t)grow * (size_t)p.N + gcol] = acc[mt][nt][r];
+        }
+    }
+    return;
+  }
   // Epilogue through LDS (the k loop's last barrier has passed, so every stage buffer is free):
   // lane l holds acc[mt][nt][r] = C[128 wm + 32 mt + 8 (r / 4) + 4 (l / 32) + r % 4]
   // [64 wn + 32 nt + l % 32] of the tile; each value (+ bias, rounded once) goes to the
@@ -377,6 +399,23 @@ __global__ void __launch_bounds__(128 * NWN, 2) prefill_stream_kernel(const Gemm
   }
 }
 
+// c[m][n .. n + 3] = round(sum over splits, in split order, of partial[s][m][n ..] + bias)
+template <typename T>
+__global__ void __launch_bounds__(256) prefill_split_reduce(const GemmArgs p, int S) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // 4-column group
+  const int64_t n4 = p.N >> 2;
+  if (i >= (int64_t)p.M * n4) return;
+  const int64_t m = i / n4, n = (i - m * n4) * 4;
+  const size_t plane = (size_t)p.M * (size_t)p.N;
+  const float* src = p.partial + (size_t)m * (size_t)p.N + (size_t)n;
+  f32x4 acc = *(const f32x4*)src;
+  for (int s = 1; s < S; ++s) acc += *(const f32x4*)(src + (size_t)s * plane);
+  float v[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] = acc[j] + (p.bias ? load_bias(p.bias, p.bias_dtype, (int)n + j) : 0.0f);
+  *(u32x2*)(p.c + m * p.ldc + n) = u32x2{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])};
+}
+
 }  // namespace awq
 
 namespace awq_host {
@@ -389,17 +428,29 @@ static void launch_ps(const GemmArgs& a, int sbf, int log2g, hipStream_t st) {
   const int cus = num_cus();
   // groups of 128 rows or more: both stages of a pair share their group
   const bool gpair = a.G >= 128;
+  if (a.ksplit > 1) {
+    // split-K: 256-column blocks over K ranges of whole stage pairs, then the ordered sum
+    const int nst = (int)cdiv(a.K, kPSBK);
+    const int per = (int)((cdiv(nst, a.ksplit) + 1) / 2 * 2);
+    const int S = (int)cdiv(nst, per);
+    const dim3 grid((unsigned)(tm * tn4), (unsigned)S);
+    if (gpair) hipLaunchKernelGGL((prefill_stream_kernel<4, ZP, T, FAST, true>), grid, dim3(512), 0, st, a, sbf, tm, tn4, log2g, 0, per);
+    else hipLaunchKernelGGL((prefill_stream_kernel<4, ZP, T, FAST, false>), grid, dim3(512), 0, st, a, sbf, tm, tn4, log2g, 0, per);
+    const int64_t groups = (int64_t)a.M * (a.N / 4);
+    hipLaunchKernelGGL((prefill_split_reduce<T>), dim3((unsigned)cdiv(groups, 256)), dim3(256), 0, st, a, S);
+    return;
+  }
   auto wide = [&](int tiles_n, int n_off) {
     if (gpair) hipLaunchKernelGGL((prefill_stream_kernel<4, ZP, T, FAST, true>), dim3(tm * tiles_n), dim3(512), 0, st, a, sbf, tm, tiles_n,
-                       log2g, n_off);
+                       log2g, n_off, 0);
     else hipLaunchKernelGGL((prefill_stream_kernel<4, ZP, T, FAST, false>), dim3(tm * tiles_n), dim3(512), 0, st, a, sbf, tm, tiles_n,
-                       log2g, n_off);
+                       log2g, n_off, 0);
   };
   auto narrow = [&](int tiles_n, int n_off) {
     if (gpair) hipLaunchKernelGGL((prefill_stream_kernel<2, ZP, T, FAST, true>), dim3(tm * tiles_n), dim3(256), 0, st, a, sbf, tm, tiles_n,
-                       log2g, n_off);
+                       log2g, n_off, 0);
     else hipLaunchKernelGGL((prefill_stream_kernel<2, ZP, T, FAST, false>), dim3(tm * tiles_n), dim3(256), 0, st, a, sbf, tm, tiles_n,
-                       log2g, n_off);
+                       log2g, n_off, 0);
   };
   // 256-column blocks (two waves per SIMD) once they cover three quarters of the CUs; below
   // that, twice as many 128-column blocks.  Measured on MI355X (K = 4096): M = 512, N = 24576

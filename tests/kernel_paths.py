@@ -5,6 +5,6 @@ exact reference takes the matching weights."""
 
 
 def decode_serves(M: int, N: int, G: int) -> bool:
-    """M <= 32 on the decode kernels, and 32-row chunks of them up to M = 64 (M = 128 at
-    N <= 4096), for group sizes 32, 64 and 128."""
-    return int(G) in (32, 64, 128) and (M <= 64 or (M <= 128 and N <= 4096))
+    """M <= 32 on the decode kernels, and 32-row chunks of them up to M = 64, for group sizes
+    32, 64 and 128 (N does not enter the rule)."""
+    return int(G) in (32, 64, 128) and M <= 64

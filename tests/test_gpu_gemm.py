@@ -159,6 +159,36 @@ def test_gemm_autoawq_vs_oracle(M, K, N, G, stream):
         _check_vs_ref(y, yr, f"M={M} K={K} N={N}")
 
 
+@pytest.mark.parametrize("M,K,N,G", [(128, 2048, 8192, 128), (256, 4096, 1024, 64), (384, 1024, 2056, 128),
+                                     (200, 512, 512, 32), (300, 2080, 520, 32)])
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_prefill_k_ranges(M, K, N, G, dt):
+    """Prefill calls whose 256 x 256 tiles cover at most half the CUs split K into ranges of
+    whole stage pairs (fp32 partials summed in range order by a second launch; the last range
+    of K % 64 == 32 ends on a half stage): within 1 ulp of the exact oracle on the fp16-rounded
+    weights, bias added once, bitwise reproducible."""
+    ops = _lib()
+    _note(f"prefill k ranges M={M} K={K} N={N} G={G} {dt}")
+    p = make_awq_problem(M=M, K=K, N=N, group_size=G, seed=M + K + G)
+    t = _to_dev(p)
+    x = t["x"].to(dt)
+    b = torch.randn(N, generator=torch.Generator().manual_seed(N)).to(dt)
+    y = ops.gemm(x, t["qweight"], t["scales"], t["qzeros"], G, bias=b.to(DEV), layout="autoawq")
+    y2 = ops.gemm(x, t["qweight"], t["scales"], t["qzeros"], G, bias=b.to(DEV), layout="autoawq")
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+    half = "float16" if dt == torch.float16 else "bfloat16"
+    w = _w_used(p, M, G, half=half)
+    xe = x.float().cpu().numpy()
+    ye = O.linear_exact(xe, w.T, b.float().double().numpy())
+    yv = y.float().cpu().numpy()
+    if dt == torch.float16:
+        _check_vs_exact(yv, ye, f"M={M} K={K} N={N} G={G}")
+    else:  # one bf16 rounding of the fp32 sum: |d| <= 1 bf16 ulp of max(|y|, 1)
+        ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(ye), 1.0))) - 7)
+        assert (np.abs(yv - ye) <= ulp).all(), float((np.abs(yv - ye) / ulp).max())
+
+
 @pytest.mark.parametrize("M,layout", [(1, None), (4, None), (16, None), (1, "stream"), (16, "stream"),
                                       (64, None), (512, None)])
 def test_gemm_strided_rows(M, layout):
