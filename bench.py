@@ -578,6 +578,19 @@ def main():
                                     "mfma_frac": round(tfl / MFMA_F16_PEAK_TFLOPS, 4), "weight_copies": 3}
             del W3
         configs["config3"] = c3
+        # calls between the decode batch and the prefill headline (not a configs[] shape): 33 .. 64
+        # rows run as 32-row decode chunks, larger small calls cut K into ranges
+        sm = {}
+        Ws = _weights(torch, K_DEC, 4096, rot_copies(K_DEC, 4096), dev, 57)
+        for m in (48, 128, 256):
+            xs = torch.randn((m, K_DEC), device=dev, generator=gen).half()
+            ys = torch.empty((m, 4096), device=dev, dtype=torch.float16)
+            us = _time_rotation(torch, ops, xs, Ws, ys, 10)
+            tfl = 2.0 * m * 4096 * K_DEC / (us * 1e-6) / 1e12
+            sm[f"M{m}_N4096"] = {"us": round(us, 2), "TFLOPs": round(tfl, 1),
+                                 "path": "decode chunks" if m <= 64 else "prefill, K ranges"}
+        del Ws
+        configs["small_m"] = sm
 
     # ---- prefill headline (configs[3], M=2048, N=24576) ----
     _progress("prefill")
