@@ -318,7 +318,7 @@ def _auto_splits(M: int, N: int, K: int) -> int:
     return max(1, min(-(-K // 64), by_k, fit))
 
 
-def _narrow_fits(M: int, N: int, K: int, split_k: int) -> bool:
+def _narrow_fits(M: int, N: int, K: int, split_k: int, bf16: bool = False) -> bool:
     """Whether a decode-shaped call reads the narrow layout (one block per 16 columns over the
     whole K, no split-K hand-off) instead of the 128-column stream.
 
@@ -337,10 +337,22 @@ def _narrow_fits(M: int, N: int, K: int, split_k: int) -> bool:
     as auto wherever auto does not split K, so a forced 1 and auto give the same bits there;
     where auto would split, the narrow kernel, whose N / 16 blocks cover the chip that the
     N / 128 whole-K stream blocks leave mostly idle.
-    ``split_k > 1`` fixes a partition of K, which only the stream kernel takes."""
+    ``split_k > 1`` fixes a partition of K, which only the stream kernel takes.
+    ``bf16`` activations keep the narrow kernel to two tiles per CU at M <= 4 and one at
+    M <= 16, K <= 4096: their narrow path trails the stream kernel past that (K = 4096, M = 1,
+    N = 12288 / 16384 11.1 / 14.1 us against 9.5 / 11.5 us; M = 4, K = 14336, N = 4096 15.4
+    against 11.7 us)."""
     if split_k > 1:
         return False
     tiles = -(-N // 16)
+    if bf16:
+        if M <= 4 and M * K * 2 <= 49152:
+            auto = tiles <= 2 * L.num_cus()
+        else:
+            auto = M <= 16 and tiles <= L.num_cus() and K <= 4096
+        if split_k == 0 or auto:
+            return auto
+        return _auto_splits(M, N, K) > 1
     if M <= 4 and M * K * 2 <= 49152:
         per_cu = 4 if (M <= 3 and K <= 4096) else (3 if K <= 8192 else 2)
         auto = tiles <= per_cu * L.num_cus()
@@ -353,7 +365,8 @@ def _narrow_fits(M: int, N: int, K: int, split_k: int) -> bool:
     return _auto_splits(M, N, K) > 1
 
 
-def _kernel_weight(qweight, scales, qzeros, group_size, layout, M, N, K, split_k, decode_stream, decode_layout):
+def _kernel_weight(qweight, scales, qzeros, group_size, layout, M, N, K, split_k, decode_stream, decode_layout,
+                   bf16=False):
     """The weight copy and layout code the kernels read for this call.  Decode-shaped calls
     take the narrow or stream copy and prefill-sized ones the stream copy (see ``gemm``); both
     are held by the caller's weight tensor.  A reference-layout weight holds its scales and
@@ -374,7 +387,7 @@ def _kernel_weight(qweight, scales, qzeros, group_size, layout, M, N, K, split_k
         if decode_layout == "narrow" and not _decode_shaped(M, g):
             raise ValueError("the narrow layout needs M <= 32 and group 32/64/128")
         narrow = _decode_shaped(M, g) and (
-            decode_layout == "narrow" or (decode_layout is None and _narrow_fits(M, N, K, int(split_k))))
+            decode_layout == "narrow" or (decode_layout is None and _narrow_fits(M, N, K, int(split_k), bf16)))
         if ref:
             cache = REF_NARROW_CACHE if narrow else REF_STREAM_CACHE
             qweight = cache.get(src_qw, src_sc, src_qz, args=(g,))
@@ -407,7 +420,8 @@ def gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, qzeros: t
     if int(a.shape[1]) != K:
         raise ValueError(f"K mismatch: a has {a.shape[1]}, weight has {K}")
     qweight, scales, qzeros, lc = _kernel_weight(qweight, scales, qzeros, group_size, layout, M, N, K,
-                                                 split_k, decode_stream, decode_layout)
+                                                 split_k, decode_stream, decode_layout,
+                                                 a.dtype == torch.bfloat16)
     # rows at any stride the kernels take (16-byte aligned, a multiple of 8 elements) are read in
     # place, as the reference's kernel takes stride_am; anything else is made contiguous
     lda = int(a.stride(0)) if M > 1 else K
@@ -452,7 +466,7 @@ def gemm_rows_exact(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor
         raise ValueError(f"K mismatch: a has {a.shape[1]}, weight has {K}")
     # the weight copy and plan of an M = 1 call
     qweight, scales, qzeros, lc = _kernel_weight(qweight, scales, qzeros, group_size, layout, 1, N, K,
-                                                 split_k, None, None)
+                                                 split_k, None, None, a.dtype == torch.bfloat16)
     a = a.contiguous()
     if out is None:
         out = torch.empty((M, N), dtype=a.dtype, device=a.device)
@@ -506,7 +520,8 @@ def rmsnorm_gemm(x: torch.Tensor, norm_w: torch.Tensor, eps: float, qweight: tor
     if int(x.shape[1]) != K or int(norm_w.shape[0]) != K:
         raise ValueError(f"K mismatch: x has {x.shape[1]}, norm_w {norm_w.shape[0]}, weight {K}")
     qweight, scales, qzeros, lc = _kernel_weight(qweight, scales, qzeros, group_size, layout, M, N, K,
-                                                 split_k, decode_stream, decode_layout)
+                                                 split_k, decode_stream, decode_layout,
+                                                 x.dtype == torch.bfloat16)
     x, norm_w = x.contiguous(), norm_w.contiguous()
     if out is None:
         out = torch.empty((M, N), dtype=x.dtype, device=dev)
@@ -613,7 +628,8 @@ def gate_up_act(x: torch.Tensor, gate_qweight: torch.Tensor, up_qweight: torch.T
     kind = "autoawq"
     if K % 32 == 0 and M <= DECODE_MAX_M:
         n_narrow = 2 * (-(-I // 8)) * 8
-        narrow = decode_layout == "narrow" or (decode_layout is None and _narrow_fits(M, n_narrow, K, int(split_k)))
+        narrow = decode_layout == "narrow" or (decode_layout is None and
+                                               _narrow_fits(M, n_narrow, K, int(split_k), x.dtype == torch.bfloat16))
         kind = "narrow" if narrow else "stream"
     qw, sc, qz, st = GATE_UP_CACHE.get(gate_qweight, up_qweight, gate_scales, up_scales, gate_qzeros,
                                        up_qzeros, args=(int(group_size), layout, kind))

@@ -177,6 +177,10 @@ def test_decode_layout_choice():
     assert ops._narrow_fits(8, 32 * cus, 4096, 0) and not ops._narrow_fits(8, 32 * cus + 16, 4096, 0)
     assert not ops._narrow_fits(8, 32 * cus, 8192, 0) and ops._narrow_fits(8, 16 * cus, 4096, 0)
     assert not ops._narrow_fits(9, 32 * cus, 4096, 0)
+    # bf16 activations keep two tiles per CU at M <= 4 and one at M <= 16, K <= 4096
+    assert ops._narrow_fits(1, 32 * cus, 4096, 0, bf16=True) and not ops._narrow_fits(1, 48 * cus, 4096, 0, bf16=True)
+    assert not ops._narrow_fits(4, 16 * cus, 14336, 0, bf16=True) and not ops._narrow_fits(8, 32 * cus, 4096, 0, bf16=True)
+    assert ops._narrow_fits(8, 16 * cus, 4096, 0, bf16=True)
 
 
 def test_forced_split1_kernel_choice():
