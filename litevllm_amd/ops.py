@@ -338,18 +338,17 @@ def _narrow_fits(M: int, N: int, K: int, split_k: int, bf16: bool = False) -> bo
     where auto would split, the narrow kernel, whose N / 16 blocks cover the chip that the
     N / 128 whole-K stream blocks leave mostly idle.
     ``split_k > 1`` fixes a partition of K, which only the stream kernel takes.
-    ``bf16`` activations keep the narrow kernel to two tiles per CU at M <= 4 and one at
-    M <= 16, K <= 4096: their narrow path trails the stream kernel past that (K = 4096, M = 1,
-    N = 12288 / 16384 11.1 / 14.1 us against 9.5 / 11.5 us; M = 4, K = 14336, N = 4096 15.4
-    against 11.7 us)."""
+    ``bf16`` activations take the narrow kernel only at K <= 4096 with one tile per CU up to
+    M = 16, or two at M = 1 (K = 4096, N = 4096: 6.1 / 6.5 / 7.9 us at M = 1 / 4 / 16 against
+    7.6 / 7.8 / 9.2 us on the stream kernel; M = 1, N = 8192 8.9 against 9.4 us): their narrow
+    path trails the stream kernel past that (M = 4, N = 6144 / 8192 9.9 / 10.2 against 8.5 /
+    9.2 us; M = 1, K = 12288, N = 4096 12.5 against 10.6 us; M = 1, N = 12288 11.1 against
+    9.5 us)."""
     if split_k > 1:
         return False
     tiles = -(-N // 16)
     if bf16:
-        if M <= 4 and M * K * 2 <= 49152:
-            auto = tiles <= 2 * L.num_cus()
-        else:
-            auto = M <= 16 and tiles <= L.num_cus() and K <= 4096
+        auto = K <= 4096 and ((M <= 16 and tiles <= L.num_cus()) or (M == 1 and tiles <= 2 * L.num_cus()))
         if split_k == 0 or auto:
             return auto
         return _auto_splits(M, N, K) > 1

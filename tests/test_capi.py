@@ -177,10 +177,11 @@ def test_decode_layout_choice():
     assert ops._narrow_fits(8, 32 * cus, 4096, 0) and not ops._narrow_fits(8, 32 * cus + 16, 4096, 0)
     assert not ops._narrow_fits(8, 32 * cus, 8192, 0) and ops._narrow_fits(8, 16 * cus, 4096, 0)
     assert not ops._narrow_fits(9, 32 * cus, 4096, 0)
-    # bf16 activations keep two tiles per CU at M <= 4 and one at M <= 16, K <= 4096
+    # bf16 activations: K <= 4096 with one tile per CU up to M = 16, two at M = 1
     assert ops._narrow_fits(1, 32 * cus, 4096, 0, bf16=True) and not ops._narrow_fits(1, 48 * cus, 4096, 0, bf16=True)
-    assert not ops._narrow_fits(4, 16 * cus, 14336, 0, bf16=True) and not ops._narrow_fits(8, 32 * cus, 4096, 0, bf16=True)
-    assert ops._narrow_fits(8, 16 * cus, 4096, 0, bf16=True)
+    assert not ops._narrow_fits(4, 32 * cus, 4096, 0, bf16=True) and ops._narrow_fits(4, 16 * cus, 4096, 0, bf16=True)
+    assert not ops._narrow_fits(1, 16 * cus, 12288, 0, bf16=True) and not ops._narrow_fits(4, 16 * cus, 14336, 0, bf16=True)
+    assert ops._narrow_fits(16, 16 * cus, 4096, 0, bf16=True) and not ops._narrow_fits(17, 16 * cus, 4096, 0, bf16=True)
 
 
 def test_forced_split1_kernel_choice():
